@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the autograd-pair hot path on one MI355X.
+
+Metric: fwd+bwd step latency (us) + % HBM/MFMA roofline per op;
+saved bytes vs CPU. The headline ``value`` is the full-step (forward + backward)
+latency of RMSNorm bf16 x[16384, 4096], eps 1e-6; every other
+BASELINE configuration is measured the same way and reported under ``ops``.
+
+A step is one forward_with_saved + backward_from_saved of the HIP pair over
+synthetic seeded inputs already resident in HBM. Before every timed region a
+512 MiB write evicts L2 and the 256 MB Infinity Cache; each region is bracketed
+by HIP events on torch's current stream, which is the stream the library
+launches on. ``steps`` regions are timed per phase after ``warmup`` untimed ones
+and medians are reported.
+
+The CPU baseline is the reference's eager PyTorch autograd path (the oracle
+package's restated forwards, fused ``F.rms_norm``/``F.layer_norm`` where the
+reference declares a runtime forward, ``F.scaled_dot_product_attention`` for
+attention) on a bounded row/head sample of the same workload, timed on this
+host's cores and scaled linearly to the full workload.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--ops a,b] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd step latency (us) + % HBM/MFMA roofline per op; saved bytes vs CPU"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
+HEADLINE = "rmsnorm"
+ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------ algorithmic work
+def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
+    """Bytes (memory-bound ops) or FLOPs (attention) per forward and backward,
+    counting each tensor the op must read or write exactly once."""
+    d = w.dims
+    es = {"float32": 4, "float16": 2, "bfloat16": 2}[w.dtype]
+    if name == "softmax":
+        n = d["rows"] * d["cols"] * es
+        return {"unit": "bytes", "fwd": 2 * n, "bwd": 3 * n}
+    if name == "rmsnorm":
+        R, H = d["rows"], d["hidden"]
+        n = R * H * es
+        return {"unit": "bytes", "fwd": 2 * n + H * es + 4 * R,
+                "bwd": 3 * n + 4 * R + 2 * H * es}
+    if name == "layernorm":
+        R, H = d["rows"], d["hidden"]
+        n = R * H * es
+        return {"unit": "bytes", "fwd": 2 * n + 2 * H * es + 8 * R,
+                "bwd": 3 * n + 8 * R + 3 * H * es}
+    if name == "swiglu":
+        n = d["rows"] * d["cols"] * es
+        return {"unit": "bytes", "fwd": 3 * n, "bwd": 5 * n}
+    if name == "rope":
+        B, H, T, D = d["B"], d["n_heads"], d["T"], d["head_dim"]
+        xb = B * (H + extra_k_heads) * T * D * es
+        tables = 2 * T * D * 4
+        return {"unit": "bytes", "fwd": 2 * xb + tables, "bwd": 2 * xb + tables}
+    if name == "causal_attention":
+        B, H, S, D = d["B"], d["H"], d["S"], d["D"]
+        dense = 2.0 * S * S * D * B * H  # one S x S x D product
+        return {"unit": "flops", "fwd": 2 * dense / 2, "bwd": 5 * dense / 2}
+    raise KeyError(name)
+
+
+# ----------------------------------------------------------------- GPU side
+def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
+    import torch
+
+    from evograd_amd import decls, pair_module
+    from evograd_amd.bind import backward_inactive_kwargs, bind, lookup_pair
+    from evograd_amd.harness import saved_state_report, summarize, time_regions
+    from evograd_amd.inputs import make_case_inputs
+
+    op = decls.get_op(name)
+    mod = pair_module(name)
+    w = op.benchmark[0]
+    inputs = make_case_inputs(op, w, "cuda")
+    k_heads = 0
+    if name == "rope":
+        # joint q/k launch: q [B, 32, T, D] from the declared recipe, k [B, 8, T, D]
+        k_heads = int(w.extra["k_heads"])
+        q = inputs["x"]
+        torch.manual_seed(w.dims["T"] * 100003 + k_heads * 1009 + w.dims["head_dim"])
+        k = torch.randn((q.shape[0], k_heads, q.shape[2], q.shape[3]), device="cuda",
+                        dtype=q.dtype)
+        dk = torch.randn_like(k)
+        cos, sin = inputs["cos"], inputs["sin"]
+        fwd = lambda: mod.rope_qk_forward_with_saved(q, k, cos, sin)  # noqa: E731
+        bwd_call = lambda saved: mod.rope_qk_backward_from_saved((inputs["dy"], dk), saved)  # noqa: E731
+        values = {"q": q, "k": k, "cos": cos, "sin": sin}
+        autograd_fn = None
+    else:
+        f, b = lookup_pair(op, mod)
+        args = [inputs.get(a.name, getattr(a, "default", None)) for a in op.args]
+        kw = backward_inactive_kwargs(op, b, inputs)
+        dy = inputs[op.upstream_grad_name]
+        fwd = lambda: f(*args)  # noqa: E731
+        bwd_call = lambda saved: b(dy, saved, **kw)  # noqa: E731
+        values = {a.name: inputs[a.name] for a in op.args if a.name in inputs}
+        bound = bind(op, mod)
+        leaves = [a.detach().requires_grad_(True) if torch.is_tensor(a) and a.is_floating_point()
+                  and isinstance(spec, decls.Active) else a
+                  for a, spec in zip(args, op.args)]
+
+        def autograd_fn():
+            y = bound(*leaves)
+            y.backward(dy)
+
+    with torch.no_grad():
+        _, saved = fwd()
+        report = saved_state_report(saved, values)
+    state = {}
+
+    def setup_bwd():
+        state["saved"] = fwd()[1]
+
+    fwd_ms = time_regions(fwd, reps=steps, warmup=warmup, flush=flush)
+    bwd_ms = time_regions(lambda: bwd_call(state["saved"]), reps=steps, warmup=warmup,
+                          flush=flush, setup=setup_bwd)
+    full_ms = time_regions(lambda: bwd_call(fwd()[1]), reps=steps, warmup=warmup, flush=flush)
+    ag = None
+    if autograd_fn is not None:
+        for lf in leaves:
+            if torch.is_tensor(lf):
+                lf.grad = None
+        ag = summarize(time_regions(autograd_fn, reps=steps, warmup=warmup, flush=flush))
+    work = algorithmic_work(name, w, k_heads)
+    sf, sb, sfull = summarize(fwd_ms), summarize(bwd_ms), summarize(full_ms)
+    out = {
+        "config": {"dims": w.dims, "dtype": w.dtype, **({"k_heads": k_heads} if k_heads else {})},
+        "fwd_us": sf["median_ms"] * 1e3,
+        "bwd_us": sb["median_ms"] * 1e3,
+        "full_us": sfull["median_ms"] * 1e3,
+        "full_q20_us": sfull["q20_ms"] * 1e3,
+        "full_q80_us": sfull["q80_ms"] * 1e3,
+        "autograd_full_us": ag["median_ms"] * 1e3 if ag else None,
+        "saved": {k: v for k, v in report.items() if k != "saved_tensors"},
+        "saved_tensors": report["saved_tensors"],
+    }
+    mem_inputs = sum(values[n].numel() * values[n].element_size()
+                     for n in op.memory_input_names() if n in values and torch.is_tensor(values[n]))
+    out["saved"]["ratio_to_memory_inputs"] = (report["logical_saved_bytes"] / mem_inputs
+                                              if mem_inputs else None)
+    if work["unit"] == "bytes":
+        for phase, ms in (("fwd", sf["median_ms"]), ("bwd", sb["median_ms"])):
+            out[f"{phase}_gbs"] = work[phase] / (ms * 1e-3) / 1e9
+        full_gbs = (work["fwd"] + work["bwd"]) / (sfull["median_ms"] * 1e-3) / 1e9
+        out.update(algorithmic_bytes=work, full_gbs=full_gbs,
+                   hbm_frac_full=full_gbs / HBM_PEAK_GBS,
+                   hbm_frac_bwd=out["bwd_gbs"] / HBM_PEAK_GBS)
+    else:
+        for phase, ms in (("fwd", sf["median_ms"]), ("bwd", sb["median_ms"])):
+            out[f"{phase}_tflops"] = work[phase] / (ms * 1e-3) / 1e12
+        full_tf = (work["fwd"] + work["bwd"]) / (sfull["median_ms"] * 1e-3) / 1e12
+        out.update(algorithmic_flops=work, full_tflops=full_tf,
+                   mfma_frac_full=full_tf / BF16_PEAK_TFLOPS)
+    del inputs, saved, state
+    torch.cuda.empty_cache()
+    return out
+
+
+# ----------------------------------------------------------------- CPU side
+def cpu_baseline(name: str) -> dict:
+    """Eager PyTorch autograd on the host cores over a bounded sample, scaled."""
+    import torch
+
+    from evograd_amd import decls
+    from evograd_amd.opdecl import Workload
+    from oracle.oracle import resolve_runtime_forward
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    op = decls.get_op(name)
+    w = op.benchmark[0]
+    d = dict(w.dims)
+    if name in ("softmax", "rmsnorm", "layernorm", "swiglu"):
+        full_rows = d["rows"]
+        d["rows"] = max(1, full_rows // 8)
+        scale = full_rows / d["rows"]
+        sample = f"{d['rows']} of {full_rows} rows"
+    elif name == "rope":
+        full = d["B"] * (d["n_heads"] + int(w.extra["k_heads"]))
+        d["B"], d["n_heads"] = 1, 8
+        scale = full / 8
+        sample = f"8 of {full} (batch, head) rows of q and k"
+    else:
+        full = d["B"] * d["H"]
+        d["B"], d["H"] = 1, 1
+        scale = float(full)
+        sample = f"1 of {full} (batch, head) pairs"
+    sw = Workload(dims=d, dtype=w.dtype, label=w.label, extra=w.extra)
+    from evograd_amd.inputs import make_case_inputs
+
+    inputs = make_case_inputs(op, sw, "cpu")
+    fwd = resolve_runtime_forward(op)
+    args = []
+    leaves = []
+    for a in op.args:
+        v = inputs.get(a.name, getattr(a, "default", None))
+        if isinstance(a, decls.Active):
+            v = v.detach().requires_grad_(True)
+            leaves.append(v)
+        args.append(v)
+    dy = inputs[op.upstream_grad_name]
+
+    def step():
+        for lf in leaves:
+            lf.grad = None
+        y = fwd(*args)
+        y.backward(dy)
+
+    step()
+    samples = []
+    t_end = time.perf_counter() + 10.0
+    while len(samples) < 3 or (len(samples) < 7 and time.perf_counter() < t_end):
+        t0 = time.perf_counter_ns()
+        step()
+        samples.append((time.perf_counter_ns() - t0) / 1e3)
+    us = statistics.median(samples) * scale
+    return {"value": us, "unit": "us", "cores": cores, "kind": "port",
+            "sample": f"{sample}, {len(samples)} reps, median scaled x{scale:g}",
+            "what": f"eager torch autograd on CPU of {op.runtime_forward or op.forward}"}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# --------------------------------------------------------------------- main
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ops", default=",".join(ALL_OPS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: every operator's work shards with no or one "
+              "16 KB exchange (see DESIGN.md), and no multi-GPU run is part of this build.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    from evograd_amd import _lib
+    from evograd_amd.harness import CacheFlusher
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    flush = CacheFlusher("cuda")
+    ops = [o for o in args.ops.split(",") if o]
+    if HEADLINE not in ops:
+        ops.insert(0, HEADLINE)
+    results = {}
+    torch.cuda.synchronize()
+    for name in ops:
+        log(f"gpu {name} ...")
+        try:
+            results[name] = gpu_op(name, args.steps, args.warmup, flush)
+        except Exception as e:  # recorded, as the reference's harness does
+            results[name] = {"error": f"{type(e).__name__}: {e}"}
+            if name == HEADLINE:
+                raise
+        log(f"gpu {name}: " + json.dumps({k: v for k, v in results[name].items()
+                                          if k in ("fwd_us", "bwd_us", "full_us", "error")}))
+    torch.cuda.synchronize()
+
+    cpu = {}
+    if not args.no_cpu:
+        for name in ops:
+            log(f"cpu {name} ...")
+            try:
+                cpu[name] = cpu_baseline(name)
+            except Exception as e:
+                cpu[name] = {"error": f"{type(e).__name__}: {e}"}
+            if "value" in results.get(name, {}) or "full_us" in results.get(name, {}):
+                if "value" in cpu[name]:
+                    results[name]["cpu_full_us"] = cpu[name]["value"]
+                    results[name]["speedup_vs_cpu"] = cpu[name]["value"] / results[name]["full_us"]
+
+    head = results[HEADLINE]
+    w = head["config"]
+    dims = w["dims"]
+    # Dominant kernel of the headline step: the RMSNorm backward launch
+    # (rmsnorm_bwd_kernel + its fixed-order column sum), timed as one region.
+    bwd_bytes = head["algorithmic_bytes"]["bwd"]
+    achieved = bwd_bytes / (head["bwd_us"] * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(head["full_us"], 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["full_us"] / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"rmsnorm fwd+bwd bf16 x[{dims['rows']},{dims['hidden']}] eps=1e-6 "
+                        "(BASELINE configs[1])",
+            "rows": dims["rows"], "hidden": dims["hidden"],
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "rmsnorm backward (rmsnorm_bwd_kernel + colsum_kernel)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": ({k: v for k, v in cpu[HEADLINE].items() if k != "what"}
+                         if HEADLINE in cpu and "value" in cpu[HEADLINE] else None),
+        "cpu_model": cpu_model(),
+        "ops": results,
+    }
+    if line["cpu_baseline"] is not None:
+        line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 1)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,192 @@
+// Shared device helpers for the gfx950 kernels: dtype conversion with
+// round-to-nearest-even (the rounding torch's .to(dtype) uses), 16-byte vector
+// memory access, wave64 and workgroup reductions with a fixed combine order,
+// and the thread-local error slot behind eg_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/evograd_hip.h"
+
+namespace eg {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ------------------------------------------------------------------ errors
+void set_error(const char* fmt, ...);
+void clear_error();
+// Turns a failed launch into an error return; reads (and clears) the HIP
+// runtime's sticky launch error.
+int check_launch(const char* what);
+
+// ------------------------------------------------------------ dtype tags
+struct bf16_t { uint16_t bits; };
+typedef _Float16 f16_t;
+
+template <typename T> struct DT;
+template <> struct DT<float>  { static constexpr int id = EG_F32; };
+template <> struct DT<f16_t>  { static constexpr int id = EG_F16; };
+template <> struct DT<bf16_t> { static constexpr int id = EG_BF16; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(f16_t v) { return (float)v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+  return __uint_as_float(((uint32_t)v.bits) << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) { return (f16_t)v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+  bf16_t r; r.bits = f32_to_bf16_bits(v); return r;
+}
+
+// Round an fp32 value to T and widen it back (the value a .to(T) would hold).
+template <typename T> __device__ __forceinline__ float round_to(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+// ------------------------------------------------------- vector memory access
+// VEC elements of T packed into one naturally aligned load/store (16 bytes when
+// VEC * sizeof(T) == 16, which the hot paths use: global_load_dwordx4).
+template <typename T, int VEC>
+struct alignas(sizeof(T) * VEC) Pack {
+  T v[VEC];
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&out)[VEC]) {
+  Pack<T, VEC> pk = *reinterpret_cast<const Pack<T, VEC>*>(p);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) out[i] = to_f32(pk.v[i]);
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&in)[VEC]) {
+  Pack<T, VEC> pk;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) pk.v[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<Pack<T, VEC>*>(p) = pk;
+}
+
+// Streaming variants: data touched once per kernel; the non-temporal hint keeps
+// it from displacing reused lines (tables, weights) in L2.
+template <typename T, int VEC>
+__device__ __forceinline__ void load_f32_nt(const T* __restrict__ p, float (&out)[VEC]) {
+  static_assert(sizeof(T) * VEC == 16, "nt path is for 16-byte packs");
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  Pack<T, VEC> pk;
+  __builtin_memcpy(&pk, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) out[i] = to_f32(pk.v[i]);
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_f32_nt(T* __restrict__ p, const float (&in)[VEC]) {
+  static_assert(sizeof(T) * VEC == 16, "nt path is for 16-byte packs");
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  Pack<T, VEC> pk;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) pk.v[i] = from_f32<T>(in[i]);
+  u32x4 raw;
+  __builtin_memcpy(&raw, &pk, 16);
+  __builtin_nontemporal_store(raw, reinterpret_cast<u32x4*>(p));
+}
+
+// ------------------------------------------------------------- reductions
+struct SumOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+  static __device__ __forceinline__ float identity() { return 0.f; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+  static __device__ __forceinline__ float identity() { return -INFINITY; }
+};
+
+// Butterfly over the 64 lanes; every lane ends with the same value, combined in
+// the same order on every run.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Workgroup reduction of BLOCK threads. `lds` must hold BLOCK/64 floats. The
+// per-wave results are combined in wave order, so the result is bit-identical
+// across runs. Ends with every thread holding the result; callers that reuse
+// `lds` must __syncthreads() first (done here at entry).
+template <int BLOCK, typename Op>
+__device__ __forceinline__ float block_reduce(float v, Op op, float* lds) {
+  constexpr int NW = BLOCK / kWave;
+  v = wave_reduce(v, op);
+  if constexpr (NW == 1) {
+    return v;
+  } else {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    __syncthreads();
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    float r = lds[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = op(r, lds[w]);
+    return r;
+  }
+}
+
+// Two sums at once (one barrier pair instead of two); used by the norm backwards.
+template <int BLOCK>
+__device__ __forceinline__ void block_reduce2(float& a, float& b, float* lds) {
+  constexpr int NW = BLOCK / kWave;
+  a = wave_reduce(a, SumOp());
+  b = wave_reduce(b, SumOp());
+  if constexpr (NW > 1) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    __syncthreads();
+    if (lane == 0) { lds[wid] = a; lds[NW + wid] = b; }
+    __syncthreads();
+    float ra = lds[0], rb = lds[NW];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) { ra += lds[w]; rb += lds[NW + w]; }
+    a = ra; b = rb;
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Zeroes `bytes` bytes with a small kernel (no hipMemsetAsync, so the call is
+// safe inside a captured graph). Returns 0 or an error code.
+int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
+
+// Number of compute units of the current device (cached per device ordinal).
+int device_cus();
+
+}  // namespace eg
+
+// Dispatch on the runtime dtype tag; `FN` is a generic lambda taking a T* tag.
+#define EG_DISPATCH_FLOAT(dtype, name, ...)                                      \
+  [&]() -> int {                                                                 \
+    switch (dtype) {                                                             \
+      case EG_F32: { using scalar_t = float; return __VA_ARGS__(); }             \
+      case EG_F16: { using scalar_t = eg::f16_t; return __VA_ARGS__(); }         \
+      case EG_BF16: { using scalar_t = eg::bf16_t; return __VA_ARGS__(); }       \
+      default: eg::set_error("%s: unsupported dtype %d", name, (int)(dtype));    \
+               return 1;                                                         \
+    }                                                                            \
+  }()

@@ -1,0 +1,525 @@
+// RMSNorm and LayerNorm forward/backward for gfx950.
+//
+// RMSNorm follows rmsnorm_forward_ref (src/evograd/ops/level1/rmsnorm/forward_ref.py:6-21)
+// and the backward rule at src/evograd/ops/level1/rmsnorm/__init__.py:85-86.
+// LayerNorm follows layernorm_forward_ref (src/evograd/ops/level1/layernorm/forward_ref.py:6-23)
+// and its autograd backward (grads declared at layernorm/__init__.py:124-171).
+//
+// Layout: x, y, dy, dx are [rows, hidden] row-major in HBM; weight/bias [hidden];
+// the saved statistics (rstd, and mean for LayerNorm) are fp32 [rows].
+//
+// Forward: one workgroup per row, the row held in registers (16-byte packs),
+// statistics reduced by wave butterflies and one LDS exchange.
+//
+// Backward: G = min(rows, kPartialBlocks) workgroups walk the rows with stride G.
+// Each thread owns a fixed set of columns for the whole walk, so it keeps its
+// weight values and its dweight (and dbias) accumulators in registers; the next
+// row's loads are issued before the current row is reduced. At the end every
+// workgroup writes one fp32 partial row to the workspace [G, hidden], and a second
+// kernel sums the G partials per column in a fixed order. No atomics: the result
+// is bit-identical from run to run.
+#include "eg_common.hpp"
+
+#include <initializer_list>
+
+namespace eg {
+namespace {
+
+constexpr int kPartialBlocks = 512;
+
+inline int64_t partial_blocks(int64_t rows) {
+  return rows < kPartialBlocks ? (rows > 0 ? rows : 1) : kPartialBlocks;
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__device__ __forceinline__ void load_cols(const T* __restrict__ p, int n, float (&v)[ITEMS][VEC]) {
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+    if (c < n) {
+      load_f32<T, VEC>(p + c, v[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[it][i] = 0.f;
+    }
+  }
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__device__ __forceinline__ void store_cols(T* __restrict__ p, int n, const float (&v)[ITEMS][VEC]) {
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+    if (c < n) store_f32<T, VEC>(p + c, v[it]);
+  }
+}
+
+// ------------------------------------------------------------------ RMSNorm
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_kernel(const T* __restrict__ x,
+                                                            const T* __restrict__ w,
+                                                            T* __restrict__ y,
+                                                            float* __restrict__ rstd_out,
+                                                            int hidden, float eps) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t row = blockIdx.x;
+  const int64_t off = row * hidden;
+  float xv[ITEMS][VEC], wv[ITEMS][VEC];
+  load_cols<T, VEC, ITEMS, BLOCK>(x + off, hidden, xv);
+  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) ss += xv[it][i] * xv[it][i];
+  ss = block_reduce<BLOCK>(ss, SumOp(), lds);
+  const float rstd = rsqrtf(ss / (float)hidden + eps);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) xv[it][i] = (xv[it][i] * rstd) * wv[it][i];
+  store_cols<T, VEC, ITEMS, BLOCK>(y + off, hidden, xv);
+  if (threadIdx.x == 0) rstd_out[row] = rstd;
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
+    const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ partial,
+    int64_t rows, int hidden) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t G = gridDim.x;
+  float wv[ITEMS][VEC], acc[ITEMS][VEC];
+  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[it][i] = 0.f;
+  const float inv_h = 1.0f / (float)hidden;
+
+  int64_t row = blockIdx.x;
+  float xv[ITEMS][VEC], gv[ITEMS][VEC];
+  float r = 0.f;
+  if (row < rows) {
+    load_cols<T, VEC, ITEMS, BLOCK>(x + row * hidden, hidden, xv);
+    load_cols<T, VEC, ITEMS, BLOCK>(dy + row * hidden, hidden, gv);
+    r = rstd[row];
+  }
+  while (row < rows) {
+    // Prefetch the next row of this workgroup while the current one reduces.
+    const int64_t nrow = row + G;
+    float nx[ITEMS][VEC], ng[ITEMS][VEC];
+    float nr = 0.f;
+    if (nrow < rows) {
+      load_cols<T, VEC, ITEMS, BLOCK>(x + nrow * hidden, hidden, nx);
+      load_cols<T, VEC, ITEMS, BLOCK>(dy + nrow * hidden, hidden, ng);
+      nr = rstd[nrow];
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float xh = xv[it][i] * r;
+        acc[it][i] += gv[it][i] * xh;
+        const float g = gv[it][i] * wv[it][i];
+        xv[it][i] = xh;
+        gv[it][i] = g;
+        dot += g * xh;
+      }
+    dot = block_reduce<BLOCK>(dot, SumOp(), lds) * inv_h;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) gv[it][i] = (gv[it][i] - xv[it][i] * dot) * r;
+    store_cols<T, VEC, ITEMS, BLOCK>(dx + row * hidden, hidden, gv);
+    row = nrow;
+    if (row < rows) {
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) { xv[it][i] = nx[it][i]; gv[it][i] = ng[it][i]; }
+      r = nr;
+    }
+  }
+  float* pp = partial + (int64_t)blockIdx.x * hidden;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+    if (c < hidden) store_f32<float, VEC>(pp + c, acc[it]);
+  }
+}
+
+// ---------------------------------------------------------------- LayerNorm
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void layernorm_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b,
+    T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
+    int hidden, float eps) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t row = blockIdx.x;
+  const int64_t off = row * hidden;
+  float xv[ITEMS][VEC];
+  load_cols<T, VEC, ITEMS, BLOCK>(x + off, hidden, xv);
+  float s = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) s += xv[it][i];
+  const float mean = block_reduce<BLOCK>(s, SumOp(), lds) / (float)hidden;
+  float q = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float d = (c + i < hidden) ? xv[it][i] - mean : 0.f;
+      q += d * d;
+    }
+  }
+  const float var = block_reduce<BLOCK>(q, SumOp(), lds) / (float)hidden;
+  const float rstd = rsqrtf(var + eps);
+  float wv[ITEMS][VEC], bv[ITEMS][VEC];
+  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
+  load_cols<T, VEC, ITEMS, BLOCK>(b, hidden, bv);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i)
+      xv[it][i] = ((xv[it][i] - mean) * rstd) * wv[it][i] + bv[it][i];
+  store_cols<T, VEC, ITEMS, BLOCK>(y + off, hidden, xv);
+  if (threadIdx.x == 0) { mean_out[row] = mean; rstd_out[row] = rstd; }
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
+    const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
+    float* __restrict__ partial_w, float* __restrict__ partial_b, int64_t rows, int hidden) {
+  __shared__ float lds[2 * (BLOCK / kWave)];
+  const int64_t G = gridDim.x;
+  float wv[ITEMS][VEC], accw[ITEMS][VEC], accb[ITEMS][VEC];
+  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { accw[it][i] = 0.f; accb[it][i] = 0.f; }
+  const float inv_h = 1.0f / (float)hidden;
+
+  int64_t row = blockIdx.x;
+  float xv[ITEMS][VEC], gv[ITEMS][VEC];
+  float mu = 0.f, r = 0.f;
+  if (row < rows) {
+    load_cols<T, VEC, ITEMS, BLOCK>(x + row * hidden, hidden, xv);
+    load_cols<T, VEC, ITEMS, BLOCK>(dy + row * hidden, hidden, gv);
+    mu = mean[row];
+    r = rstd[row];
+  }
+  while (row < rows) {
+    const int64_t nrow = row + G;
+    float nx[ITEMS][VEC], ng[ITEMS][VEC];
+    float nmu = 0.f, nr = 0.f;
+    if (nrow < rows) {
+      load_cols<T, VEC, ITEMS, BLOCK>(x + nrow * hidden, hidden, nx);
+      load_cols<T, VEC, ITEMS, BLOCK>(dy + nrow * hidden, hidden, ng);
+      nmu = mean[nrow];
+      nr = rstd[nrow];
+    }
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        // Padding columns load zeros for x but must also give xhat = 0.
+        const float xh = (c + i < hidden) ? (xv[it][i] - mu) * r : 0.f;
+        accw[it][i] += gv[it][i] * xh;
+        accb[it][i] += gv[it][i];
+        const float g = gv[it][i] * wv[it][i];
+        xv[it][i] = xh;
+        gv[it][i] = g;
+        sg += g;
+        sgx += g * xh;
+      }
+    }
+    block_reduce2<BLOCK>(sg, sgx, lds);
+    sg *= inv_h;
+    sgx *= inv_h;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) gv[it][i] = r * ((gv[it][i] - sg) - xv[it][i] * sgx);
+    store_cols<T, VEC, ITEMS, BLOCK>(dx + row * hidden, hidden, gv);
+    row = nrow;
+    if (row < rows) {
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) { xv[it][i] = nx[it][i]; gv[it][i] = ng[it][i]; }
+      mu = nmu;
+      r = nr;
+    }
+  }
+  float* pw = partial_w + (int64_t)blockIdx.x * hidden;
+  float* pb = partial_b + (int64_t)blockIdx.x * hidden;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+    if (c < hidden) {
+      store_f32<float, VEC>(pw + c, accw[it]);
+      store_f32<float, VEC>(pb + c, accb[it]);
+    }
+  }
+}
+
+// ------------------------------------------------- stage 2: column sums
+// out[c] = sum_{g=0..G-1} partial[g, c], combined in a fixed order: 4 row
+// groups per column (g = grp, grp+4, ...) summed in order, then the 4 group sums
+// added in group order. blockIdx.y selects one of up to two (partial, out) pairs.
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ p0,
+                                                     T* __restrict__ o0,
+                                                     const float* __restrict__ p1,
+                                                     T* __restrict__ o1, int G, int hidden) {
+  __shared__ float lds[4][64];
+  const float* p = blockIdx.y == 0 ? p0 : p1;
+  T* o = blockIdx.y == 0 ? o0 : o1;
+  const int cx = threadIdx.x & 63;
+  const int grp = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + cx;
+  float s = 0.f;
+  if (c < hidden)
+    for (int g = grp; g < G; g += 4) s += p[(int64_t)g * hidden + c];
+  lds[grp][cx] = s;
+  __syncthreads();
+  if (grp == 0 && c < hidden) {
+    const float t = ((lds[0][cx] + lds[1][cx]) + lds[2][cx]) + lds[3][cx];
+    o[c] = from_f32<T>(t);
+  }
+}
+
+// ------------------------------------------------------------- dispatch
+template <typename F>
+bool pick_norm_config(int64_t npack, F&& f) {
+  if (npack <= 64) return f.template go<64, 1>();
+  if (npack <= 128) return f.template go<128, 1>();
+  if (npack <= 256) return f.template go<256, 1>();
+  if (npack <= 512) return f.template go<512, 1>();
+  if (npack <= 1024) return f.template go<512, 2>();
+  if (npack <= 2048) return f.template go<1024, 2>();
+  if (npack <= 4096) return f.template go<1024, 4>();
+  if (npack <= 8192) return f.template go<1024, 8>();
+  return false;
+}
+
+template <typename T, int VEC>
+struct RmsFwd {
+  const T *x, *w; T* y; float* rstd; int64_t rows; int hidden; float eps; hipStream_t st;
+  template <int BLOCK, int ITEMS> bool go() {
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+                       dim3(BLOCK), 0, st, x, w, y, rstd, hidden, eps);
+    return true;
+  }
+};
+
+template <typename T, int VEC>
+struct RmsBwd {
+  const T *dy, *x, *w; const float* rstd; T* dx; float* part; int64_t rows; int hidden;
+  hipStream_t st;
+  template <int BLOCK, int ITEMS> bool go() {
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, VEC, ITEMS, BLOCK>),
+                       dim3((unsigned)partial_blocks(rows)), dim3(BLOCK), 0, st, dy, x, w, rstd,
+                       dx, part, rows, hidden);
+    return true;
+  }
+};
+
+template <typename T, int VEC>
+struct LnFwd {
+  const T *x, *w, *b; T* y; float *mean, *rstd; int64_t rows; int hidden; float eps;
+  hipStream_t st;
+  template <int BLOCK, int ITEMS> bool go() {
+    hipLaunchKernelGGL((layernorm_fwd_kernel<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+                       dim3(BLOCK), 0, st, x, w, b, y, mean, rstd, hidden, eps);
+    return true;
+  }
+};
+
+template <typename T, int VEC>
+struct LnBwd {
+  const T *dy, *x, *w; const float *mean, *rstd; T* dx; float *pw, *pb; int64_t rows;
+  int hidden; hipStream_t st;
+  template <int BLOCK, int ITEMS> bool go() {
+    hipLaunchKernelGGL((layernorm_bwd_kernel<T, VEC, ITEMS, BLOCK>),
+                       dim3((unsigned)partial_blocks(rows)), dim3(BLOCK), 0, st, dy, x, w, mean,
+                       rstd, dx, pw, pb, rows, hidden);
+    return true;
+  }
+};
+
+int check_norm_dims(const char* what, int64_t rows, int64_t hidden) {
+  if (rows < 0 || hidden <= 0) {
+    set_error("%s: bad size rows=%lld hidden=%lld", what, (long long)rows, (long long)hidden);
+    return 1;
+  }
+  if (rows > (int64_t)0x7fffffff || hidden > 8192 * 8) {
+    set_error("%s: size out of range rows=%lld hidden=%lld", what, (long long)rows,
+              (long long)hidden);
+    return 1;
+  }
+  return 0;
+}
+
+template <typename T>
+bool vec_ok(int hidden, std::initializer_list<const void*> ptrs) {
+  constexpr int V = 16 / sizeof(T);
+  if (hidden % V) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  return true;
+}
+
+}  // namespace
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" size_t eg_rmsnorm_workspace_bytes(int64_t rows, int64_t hidden) {
+  if (rows <= 0 || hidden <= 0) return 0;
+  return (size_t)partial_blocks(rows) * (size_t)hidden * sizeof(float);
+}
+
+extern "C" size_t eg_layernorm_workspace_bytes(int64_t rows, int64_t hidden) {
+  return 2 * eg_rmsnorm_workspace_bytes(rows, hidden);
+}
+
+extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd,
+                              int64_t rows, int64_t hidden, float eps, int dtype,
+                              void* stream) {
+  clear_error();
+  if (check_norm_dims("eg_rmsnorm_fwd", rows, hidden)) return 1;
+  if (rows == 0) return 0;
+  if (!x || !weight || !y || !rstd) { set_error("eg_rmsnorm_fwd: null pointer"); return 1; }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_rmsnorm_fwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const int h = (int)hidden;
+    bool ok;
+    if (vec_ok<T>(h, {x, weight, y})) {
+      RmsFwd<T, V> f{(const T*)x, (const T*)weight, (T*)y, rstd, rows, h, eps, st};
+      ok = pick_norm_config((h + V - 1) / V, f);
+    } else {
+      RmsFwd<T, 1> f{(const T*)x, (const T*)weight, (T*)y, rstd, rows, h, eps, st};
+      ok = pick_norm_config(h, f);
+    }
+    if (!ok) { set_error("eg_rmsnorm_fwd: hidden=%d too wide", h); return 1; }
+    return check_launch("eg_rmsnorm_fwd");
+  });
+}
+
+extern "C" int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight,
+                              const float* rstd, void* dx, void* dweight, void* workspace,
+                              int64_t rows, int64_t hidden, int dtype, void* stream) {
+  clear_error();
+  if (check_norm_dims("eg_rmsnorm_bwd", rows, hidden)) return 1;
+  if (!dweight) { set_error("eg_rmsnorm_bwd: null dweight"); return 1; }
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    // Empty batch: dweight is a sum over no rows.
+    size_t es = dtype == EG_F32 ? 4 : 2;
+    return zero_fill(dweight, (size_t)hidden * es, st, "eg_rmsnorm_bwd");
+  }
+  if (!dy || !x || !weight || !rstd || !dx || !workspace) {
+    set_error("eg_rmsnorm_bwd: null pointer");
+    return 1;
+  }
+  return EG_DISPATCH_FLOAT(dtype, "eg_rmsnorm_bwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const int h = (int)hidden;
+    float* part = (float*)workspace;
+    bool ok;
+    if (vec_ok<T>(h, {dy, x, weight, dx})) {
+      RmsBwd<T, V> f{(const T*)dy, (const T*)x, (const T*)weight, rstd, (T*)dx, part, rows, h, st};
+      ok = pick_norm_config((h + V - 1) / V, f);
+    } else {
+      RmsBwd<T, 1> f{(const T*)dy, (const T*)x, (const T*)weight, rstd, (T*)dx, part, rows, h, st};
+      ok = pick_norm_config(h, f);
+    }
+    if (!ok) { set_error("eg_rmsnorm_bwd: hidden=%d too wide", h); return 1; }
+    if (int rc = check_launch("eg_rmsnorm_bwd")) return rc;
+    const int G = (int)partial_blocks(rows);
+    hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((h + 63) / 64), 1), dim3(256), 0, st,
+                       part, (T*)dweight, part, (T*)dweight, G, h);
+    return check_launch("eg_rmsnorm_bwd(colsum)");
+  });
+}
+
+extern "C" int eg_layernorm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                                float* mean, float* rstd, int64_t rows, int64_t hidden,
+                                float eps, int dtype, void* stream) {
+  clear_error();
+  if (check_norm_dims("eg_layernorm_fwd", rows, hidden)) return 1;
+  if (rows == 0) return 0;
+  if (!x || !weight || !bias || !y || !mean || !rstd) {
+    set_error("eg_layernorm_fwd: null pointer");
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_layernorm_fwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const int h = (int)hidden;
+    bool ok;
+    if (vec_ok<T>(h, {x, weight, bias, y})) {
+      LnFwd<T, V> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
+      ok = pick_norm_config((h + V - 1) / V, f);
+    } else {
+      LnFwd<T, 1> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
+      ok = pick_norm_config(h, f);
+    }
+    if (!ok) { set_error("eg_layernorm_fwd: hidden=%d too wide", h); return 1; }
+    return check_launch("eg_layernorm_fwd");
+  });
+}
+
+extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weight,
+                                const float* mean, const float* rstd, void* dx, void* dweight,
+                                void* dbias, void* workspace, int64_t rows, int64_t hidden,
+                                int dtype, void* stream) {
+  clear_error();
+  if (check_norm_dims("eg_layernorm_bwd", rows, hidden)) return 1;
+  if (!dweight || !dbias) { set_error("eg_layernorm_bwd: null dweight/dbias"); return 1; }
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    size_t es = dtype == EG_F32 ? 4 : 2;
+    if (int rc = zero_fill(dweight, (size_t)hidden * es, st, "eg_layernorm_bwd")) return rc;
+    return zero_fill(dbias, (size_t)hidden * es, st, "eg_layernorm_bwd");
+  }
+  if (!dy || !x || !weight || !mean || !rstd || !dx || !workspace) {
+    set_error("eg_layernorm_bwd: null pointer");
+    return 1;
+  }
+  return EG_DISPATCH_FLOAT(dtype, "eg_layernorm_bwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const int h = (int)hidden;
+    float* pw = (float*)workspace;
+    float* pb = pw + partial_blocks(rows) * (int64_t)h;
+    bool ok;
+    if (vec_ok<T>(h, {dy, x, weight, dx})) {
+      LnBwd<T, V> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
+      ok = pick_norm_config((h + V - 1) / V, f);
+    } else {
+      LnBwd<T, 1> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
+      ok = pick_norm_config(h, f);
+    }
+    if (!ok) { set_error("eg_layernorm_bwd: hidden=%d too wide", h); return 1; }
+    if (int rc = check_launch("eg_layernorm_bwd")) return rc;
+    const int G = (int)partial_blocks(rows);
+    hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((h + 63) / 64), 2), dim3(256), 0, st,
+                       pw, (T*)dweight, pb, (T*)dbias, G, h);
+    return check_launch("eg_layernorm_bwd(colsum)");
+  });
+}

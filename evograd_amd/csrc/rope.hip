@@ -1,0 +1,153 @@
+// Half-rotated RoPE forward/backward for gfx950, q and k in one launch.
+//
+// Follows rope_forward_ref (src/evograd/ops/level1/rope/forward_ref.py:28-47):
+//   y = x * cos + rotate_half(x) * sin, rotate_half(x) = [-x2, x1]
+// evaluated in fp32 and cast back. The backward declared at
+// src/evograd/ops/level1/rope/__init__.py:124-130 is the transpose rotation,
+//   dx = dy * cos + [dy2, -dy1] * sin,
+// which is this kernel with the sine negated (`inverse`).
+//
+// Layout: x [batch, heads, tokens, head_dim] row-major; cos/sin [tokens, head_dim].
+// A thread owns one (token, chunk) pair, chunk = VEC consecutive lanes of the
+// first half plus the matching VEC lanes of the second half. It loads its four
+// table slices once and then walks a group of heads of one batch entry, so the
+// tables cost one read per (batch, head group) instead of one per row, and the
+// x traffic is pure 16-byte streaming.
+#include "eg_common.hpp"
+
+namespace eg {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <typename T, typename TT, int VEC>
+__global__ __launch_bounds__(kBlock) void rope_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo, T* __restrict__ ko,
+    const TT* __restrict__ cosv, const TT* __restrict__ sinv, int heads_q, int heads_k,
+    int tokens, int head_dim, int hpg, int groups_q, int groups_k, float sgn) {
+  const int half = head_dim >> 1;
+  const int cpr = half / VEC;  // chunks per row
+  const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int t = (int)(idx / cpr);
+  if (t >= tokens) return;
+  const int ch = (int)(idx - (int64_t)t * cpr);
+  const int groups = groups_q + groups_k;
+  const int b = blockIdx.y / groups;
+  const int g = blockIdx.y - b * groups;
+
+  const T* src;
+  T* dst;
+  int heads, h0;
+  if (g < groups_q) { src = q; dst = qo; heads = heads_q; h0 = g * hpg; }
+  else { src = k; dst = ko; heads = heads_k; h0 = (g - groups_q) * hpg; }
+  int h1 = h0 + hpg;
+  if (h1 > heads) h1 = heads;
+
+  const int64_t toff = (int64_t)t * head_dim + ch * VEC;
+  float c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+  load_f32<TT, VEC>(cosv + toff, c1);
+  load_f32<TT, VEC>(cosv + toff + half, c2);
+  load_f32<TT, VEC>(sinv + toff, s1);
+  load_f32<TT, VEC>(sinv + toff + half, s2);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) { s1[i] *= -sgn; s2[i] *= sgn; }
+
+  const int64_t row_stride = (int64_t)tokens * head_dim;
+  const int64_t off0 = ((int64_t)b * heads + h0) * row_stride + toff;
+#pragma unroll 4
+  for (int h = h0; h < h1; ++h) {
+    const int64_t off = off0 + (int64_t)(h - h0) * row_stride;
+    float x1[VEC], x2[VEC];
+    load_f32<T, VEC>(src + off, x1);
+    load_f32<T, VEC>(src + off + half, x2);
+    float y1[VEC], y2[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      y1[i] = x1[i] * c1[i] + x2[i] * s1[i];
+      y2[i] = x2[i] * c2[i] + x1[i] * s2[i];
+    }
+    store_f32<T, VEC>(dst + off, y1);
+    store_f32<T, VEC>(dst + off + half, y2);
+  }
+}
+
+inline bool aligned_to(const void* p, size_t n) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) % n) == 0;
+}
+
+template <typename T, typename TT, int VEC>
+int launch_rope(const void* q, const void* k, void* qo, void* ko, const void* cosv,
+                const void* sinv, int64_t batch, int64_t hq, int64_t hk, int64_t tokens,
+                int64_t head_dim, float sgn, hipStream_t st) {
+  // Heads per group: enough groups to fill the chip, few enough to amortise the
+  // table loads over several rows.
+  const int hpg = 4;
+  const int gq = (int)((hq + hpg - 1) / hpg);
+  const int gk = (int)((hk + hpg - 1) / hpg);
+  const int64_t gy = batch * (gq + gk);
+  const int64_t threads = tokens * (head_dim / 2 / VEC);
+  const int64_t gx = (threads + kBlock - 1) / kBlock;
+  if (gy > 65535 || gx > 0x7fffffffLL) {
+    set_error("eg_rope: grid too large (batch*groups=%lld)", (long long)gy);
+    return 1;
+  }
+  hipLaunchKernelGGL((rope_kernel<T, TT, VEC>), dim3((unsigned)gx, (unsigned)gy), dim3(kBlock),
+                     0, st, (const T*)q, (const T*)k, (T*)qo, (T*)ko, (const TT*)cosv,
+                     (const TT*)sinv, (int)hq, (int)hk, (int)tokens, (int)head_dim, hpg, gq, gk,
+                     sgn);
+  return check_launch("eg_rope");
+}
+
+template <typename T, typename TT>
+int rope_dispatch_vec(const void* q, const void* k, void* qo, void* ko, const void* cosv,
+                      const void* sinv, int64_t batch, int64_t hq, int64_t hk, int64_t tokens,
+                      int64_t head_dim, float sgn, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  const int64_t half = head_dim / 2;
+  const bool vec = half % V == 0 && aligned_to(q, 16) && aligned_to(k, 16) &&
+                   aligned_to(qo, 16) && aligned_to(ko, 16) &&
+                   aligned_to(cosv, sizeof(TT) * V) && aligned_to(sinv, sizeof(TT) * V);
+  if (vec)
+    return launch_rope<T, TT, V>(q, k, qo, ko, cosv, sinv, batch, hq, hk, tokens, head_dim, sgn, st);
+  return launch_rope<T, TT, 1>(q, k, qo, ko, cosv, sinv, batch, hq, hk, tokens, head_dim, sgn, st);
+}
+
+}  // namespace
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" int eg_rope(const void* q, const void* k, void* q_out, void* k_out, const void* cos,
+                       const void* sin, int64_t batch, int64_t heads_q, int64_t heads_k,
+                       int64_t tokens, int64_t head_dim, int dtype, int table_dtype,
+                       int inverse, void* stream) {
+  clear_error();
+  if (batch < 0 || heads_q < 0 || heads_k < 0 || tokens < 0 || head_dim <= 0) {
+    set_error("eg_rope: bad sizes");
+    return 1;
+  }
+  if (head_dim % 2) { set_error("eg_rope: head_dim must be even, got %lld", (long long)head_dim); return 1; }
+  if (tokens > 0x3fffffff || head_dim > 0x3fffffff || heads_q > 0x3fffffff || heads_k > 0x3fffffff) {
+    set_error("eg_rope: size out of range");
+    return 1;
+  }
+  if (batch == 0 || tokens == 0 || heads_q + heads_k == 0) return 0;
+  if ((heads_q > 0 && (!q || !q_out)) || (heads_k > 0 && (!k || !k_out)) || !cos || !sin) {
+    set_error("eg_rope: null pointer");
+    return 1;
+  }
+  if (table_dtype != EG_F32 && table_dtype != dtype) {
+    set_error("eg_rope: table dtype must be fp32 or the tensor dtype");
+    return 1;
+  }
+  const float sgn = inverse ? -1.0f : 1.0f;
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_rope", [&] {
+    using T = scalar_t;
+    if (table_dtype == EG_F32)
+      return rope_dispatch_vec<T, float>(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k,
+                                         tokens, head_dim, sgn, st);
+    return rope_dispatch_vec<T, T>(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k, tokens,
+                                   head_dim, sgn, st);
+  });
+}

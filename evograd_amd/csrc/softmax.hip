@@ -1,0 +1,262 @@
+// Row softmax forward/backward for gfx950.
+//
+// Forward follows softmax_forward_ref (src/evograd/ops/level1/softmax/forward_ref.py:6-7):
+// y = exp(x - max) / sum(exp(x - max)) in fp32, cast to the I/O dtype. Backward is
+// the rule declared at src/evograd/ops/level1/softmax/__init__.py:78:
+// dx = y * (dy - sum(dy * y)).
+//
+// One workgroup per row. When the row fits in registers (BLOCK threads x ITEMS
+// packs x VEC elements >= cols) it is read from HBM exactly once with 16-byte
+// loads, reduced with wave butterflies + one LDS exchange, and written once.
+// Wider rows (vocabulary-sized) take a two-read online path.
+#include "eg_common.hpp"
+
+namespace eg {
+namespace {
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__device__ __forceinline__ void load_row(const T* __restrict__ row, int cols, float fill,
+                                         float (&v)[ITEMS][VEC]) {
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+    if (c < cols) {
+      load_f32<T, VEC>(row + c, v[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[it][i] = fill;
+    }
+  }
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__device__ __forceinline__ void store_row(T* __restrict__ row, int cols,
+                                          const float (&v)[ITEMS][VEC]) {
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
+    if (c < cols) store_f32<T, VEC>(row + c, v[it]);
+  }
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_fwd_reg(const T* __restrict__ x,
+                                                         T* __restrict__ y, int cols) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  float v[ITEMS][VEC];
+  load_row<T, VEC, ITEMS, BLOCK>(x + off, cols, -INFINITY, v);
+  float m = -INFINITY;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) m = fmaxf(m, v[it][i]);
+  m = block_reduce<BLOCK>(m, MaxOp(), lds);
+  float s = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      v[it][i] = expf(v[it][i] - m);
+      s += v[it][i];
+    }
+  s = block_reduce<BLOCK>(s, SumOp(), lds);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[it][i] *= inv;
+  store_row<T, VEC, ITEMS, BLOCK>(y + off, cols, v);
+}
+
+template <typename T, int VEC, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_bwd_reg(const T* __restrict__ y,
+                                                         const T* __restrict__ dy,
+                                                         T* __restrict__ dx, int cols) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  float yv[ITEMS][VEC], gv[ITEMS][VEC];
+  load_row<T, VEC, ITEMS, BLOCK>(y + off, cols, 0.f, yv);
+  load_row<T, VEC, ITEMS, BLOCK>(dy + off, cols, 0.f, gv);
+  float d = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) d += gv[it][i] * yv[it][i];
+  d = block_reduce<BLOCK>(d, SumOp(), lds);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) gv[it][i] = yv[it][i] * (gv[it][i] - d);
+  store_row<T, VEC, ITEMS, BLOCK>(dx + off, cols, gv);
+}
+
+// ---- wide rows: online (max, sum) in one read, then a second read to write.
+template <typename T, int VEC, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_fwd_loop(const T* __restrict__ x,
+                                                          T* __restrict__ y, int cols) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  const T* xr = x + off;
+  float m = -INFINITY, s = 0.f;
+  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
+    float v[VEC];
+    load_f32<T, VEC>(xr + c, v);
+    float cm = v[0];
+#pragma unroll
+    for (int i = 1; i < VEC; ++i) cm = fmaxf(cm, v[i]);
+    const float nm = fmaxf(m, cm);
+    float cs = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) cs += expf(v[i] - nm);
+    s = (m == -INFINITY ? 0.f : s * expf(m - nm)) + cs;
+    m = nm;
+  }
+  const float gm = block_reduce<BLOCK>(m, MaxOp(), lds);
+  float part = (m == -INFINITY) ? 0.f : s * expf(m - gm);
+  const float gs = block_reduce<BLOCK>(part, SumOp(), lds);
+  const float inv = 1.0f / gs;
+  T* yr = y + off;
+  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
+    float v[VEC];
+    load_f32<T, VEC>(xr + c, v);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[i] = expf(v[i] - gm) * inv;
+    store_f32<T, VEC>(yr + c, v);
+  }
+}
+
+template <typename T, int VEC, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_bwd_loop(const T* __restrict__ y,
+                                                          const T* __restrict__ dy,
+                                                          T* __restrict__ dx, int cols) {
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  float d = 0.f;
+  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
+    float a[VEC], b[VEC];
+    load_f32<T, VEC>(y + off + c, a);
+    load_f32<T, VEC>(dy + off + c, b);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) d += a[i] * b[i];
+  }
+  d = block_reduce<BLOCK>(d, SumOp(), lds);
+  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
+    float a[VEC], b[VEC];
+    load_f32<T, VEC>(y + off + c, a);
+    load_f32<T, VEC>(dy + off + c, b);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) b[i] = a[i] * (b[i] - d);
+    store_f32<T, VEC>(dx + off + c, b);
+  }
+}
+
+// Picks (BLOCK, ITEMS) so that BLOCK * ITEMS packs cover the row; returns false
+// when the row is too wide for the register path.
+template <typename Launch>
+bool pick_row_config(int64_t npack, Launch&& launch) {
+  if (npack <= 64) return launch.template go<64, 1>();
+  if (npack <= 128) return launch.template go<128, 1>();
+  if (npack <= 256) return launch.template go<256, 1>();
+  if (npack <= 512) return launch.template go<256, 2>();
+  if (npack <= 1024) return launch.template go<256, 4>();
+  if (npack <= 2048) return launch.template go<512, 4>();
+  if (npack <= 4096) return launch.template go<1024, 4>();
+  if (npack <= 8192) return launch.template go<1024, 8>();
+  return false;
+}
+
+template <typename T, int VEC>
+struct FwdLaunch {
+  const T* x; T* y; int64_t rows; int cols; hipStream_t st;
+  template <int BLOCK, int ITEMS> bool go() {
+    hipLaunchKernelGGL((softmax_fwd_reg<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+                       dim3(BLOCK), 0, st, x, y, cols);
+    return true;
+  }
+};
+
+template <typename T, int VEC>
+struct BwdLaunch {
+  const T* y; const T* dy; T* dx; int64_t rows; int cols; hipStream_t st;
+  template <int BLOCK, int ITEMS> bool go() {
+    hipLaunchKernelGGL((softmax_bwd_reg<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+                       dim3(BLOCK), 0, st, y, dy, dx, cols);
+    return true;
+  }
+};
+
+template <typename T, int VEC>
+void softmax_fwd_vec(const T* x, T* y, int64_t rows, int cols, hipStream_t st) {
+  FwdLaunch<T, VEC> l{x, y, rows, cols, st};
+  if (!pick_row_config((cols + VEC - 1) / VEC, l))
+    hipLaunchKernelGGL((softmax_fwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
+                       st, x, y, cols);
+}
+
+template <typename T, int VEC>
+void softmax_bwd_vec(const T* y, const T* dy, T* dx, int64_t rows, int cols, hipStream_t st) {
+  BwdLaunch<T, VEC> l{y, dy, dx, rows, cols, st};
+  if (!pick_row_config((cols + VEC - 1) / VEC, l))
+    hipLaunchKernelGGL((softmax_bwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
+                       st, y, dy, dx, cols);
+}
+
+int check_dims(const char* what, int64_t rows, int64_t cols) {
+  if (rows < 0 || cols < 0) {
+    set_error("%s: negative size rows=%lld cols=%lld", what, (long long)rows, (long long)cols);
+    return 1;
+  }
+  if (cols > (int64_t)1 << 30 || rows > (int64_t)0x7fffffff) {
+    set_error("%s: size out of range rows=%lld cols=%lld", what, (long long)rows,
+              (long long)cols);
+    return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" int eg_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
+                              void* stream) {
+  clear_error();
+  if (check_dims("eg_softmax_fwd", rows, cols)) return 1;
+  if (rows == 0 || cols == 0) return 0;
+  if (!x || !y) { set_error("eg_softmax_fwd: null pointer"); return 1; }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_softmax_fwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const T* xp = static_cast<const T*>(x);
+    T* yp = static_cast<T*>(y);
+    if (cols % V == 0 && aligned16(x) && aligned16(y))
+      softmax_fwd_vec<T, V>(xp, yp, rows, (int)cols, st);
+    else
+      softmax_fwd_vec<T, 1>(xp, yp, rows, (int)cols, st);
+    return check_launch("eg_softmax_fwd");
+  });
+}
+
+extern "C" int eg_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows,
+                              int64_t cols, int dtype, void* stream) {
+  clear_error();
+  if (check_dims("eg_softmax_bwd", rows, cols)) return 1;
+  if (rows == 0 || cols == 0) return 0;
+  if (!y || !dy || !dx) { set_error("eg_softmax_bwd: null pointer"); return 1; }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_softmax_bwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const T* yp = static_cast<const T*>(y);
+    const T* gp = static_cast<const T*>(dy);
+    T* dp = static_cast<T*>(dx);
+    if (cols % V == 0 && aligned16(y) && aligned16(dy) && aligned16(dx))
+      softmax_bwd_vec<T, V>(yp, gp, dp, rows, (int)cols, st);
+    else
+      softmax_bwd_vec<T, 1>(yp, gp, dp, rows, (int)cols, st);
+    return check_launch("eg_softmax_bwd");
+  });
+}

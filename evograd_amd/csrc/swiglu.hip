@@ -1,0 +1,145 @@
+// SwiGLU forward/backward for gfx950: pure streaming elementwise work.
+//
+// Forward follows swiglu_forward_ref (src/evograd/ops/level1/swiglu/forward_ref.py:6-9):
+//   c = silu(a.float()).to(a.dtype) * b
+// i.e. the silu is rounded to the I/O dtype before the product, and the product of
+// two dtype values is rounded again, exactly as the two torch ops round.
+// Backward is the rule declared at src/evograd/ops/level1/swiglu/__init__.py:70-73
+// with the sigmoid recomputed from a (nothing but a and b is saved):
+//   s = sigmoid(a); db = dc * (a * s); da = dc * b * (s + a * s * (1 - s))
+// evaluated in fp32 and rounded once.
+//
+// Each thread moves UNROLL 16-byte packs per tensor, all loads issued before any
+// math, so a wave keeps UNROLL * 16 B * 64 lanes per stream in flight.
+#include "eg_common.hpp"
+
+namespace eg {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ float sigmoidf_(float a) { return 1.0f / (1.0f + expf(-a)); }
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(const T* __restrict__ a,
+                                                            const T* __restrict__ b,
+                                                            T* __restrict__ c, int64_t npack) {
+  const int64_t base = (int64_t)blockIdx.x * kUnroll * kBlock + threadIdx.x;
+  float av[kUnroll][VEC], bv[kUnroll][VEC];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t p = base + (int64_t)u * kBlock;
+    if (p < npack) {
+      load_f32<T, VEC>(a + p * VEC, av[u]);
+      load_f32<T, VEC>(b + p * VEC, bv[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t p = base + (int64_t)u * kBlock;
+    if (p < npack) {
+      float cv[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float x = av[u][i];
+        const float silu = round_to<T>(x / (1.0f + expf(-x)));
+        cv[i] = silu * bv[u][i];
+      }
+      store_f32<T, VEC>(c + p * VEC, cv);
+    }
+  }
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(const T* __restrict__ dc,
+                                                            const T* a, const T* b, T* da,
+                                                            T* db, int64_t npack) {
+  // a/da and b/db may alias (in-place backward): no __restrict__ on them. Every
+  // element is loaded before the same thread stores to it.
+  const int64_t base = (int64_t)blockIdx.x * kUnroll * kBlock + threadIdx.x;
+  float gv[kUnroll][VEC], av[kUnroll][VEC], bv[kUnroll][VEC];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t p = base + (int64_t)u * kBlock;
+    if (p < npack) {
+      load_f32<T, VEC>(dc + p * VEC, gv[u]);
+      load_f32<T, VEC>(a + p * VEC, av[u]);
+      load_f32<T, VEC>(b + p * VEC, bv[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t p = base + (int64_t)u * kBlock;
+    if (p < npack) {
+      float dav[VEC], dbv[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float x = av[u][i];
+        const float s = sigmoidf_(x);
+        const float xs = x * s;
+        const float g = gv[u][i];
+        dbv[i] = g * xs;
+        dav[i] = g * bv[u][i] * (s + xs * (1.0f - s));
+      }
+      store_f32<T, VEC>(da + p * VEC, dav);
+      store_f32<T, VEC>(db + p * VEC, dbv);
+    }
+  }
+}
+
+inline unsigned grid_for(int64_t npack) {
+  return (unsigned)((npack + (int64_t)kUnroll * kBlock - 1) / ((int64_t)kUnroll * kBlock));
+}
+
+}  // namespace
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" int eg_swiglu_fwd(const void* a, const void* b, void* c, int64_t n, int dtype,
+                             void* stream) {
+  clear_error();
+  if (n < 0) { set_error("eg_swiglu_fwd: negative size"); return 1; }
+  if (n == 0) return 0;
+  if (!a || !b || !c) { set_error("eg_swiglu_fwd: null pointer"); return 1; }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_swiglu_fwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    if (n % V == 0 && aligned16(a) && aligned16(b) && aligned16(c)) {
+      const int64_t np = n / V;
+      if (grid_for(np) == 0 || (int64_t)grid_for(np) > 0x7fffffffLL) { set_error("eg_swiglu_fwd: too large"); return 1; }
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, V>), dim3(grid_for(np)), dim3(kBlock), 0, st,
+                         (const T*)a, (const T*)b, (T*)c, np);
+    } else {
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, 1>), dim3(grid_for(n)), dim3(kBlock), 0, st,
+                         (const T*)a, (const T*)b, (T*)c, n);
+    }
+    return check_launch("eg_swiglu_fwd");
+  });
+}
+
+extern "C" int eg_swiglu_bwd(const void* dc, const void* a, const void* b, void* da, void* db,
+                             int64_t n, int dtype, void* stream) {
+  clear_error();
+  if (n < 0) { set_error("eg_swiglu_bwd: negative size"); return 1; }
+  if (n == 0) return 0;
+  if (!dc || !a || !b || !da || !db) { set_error("eg_swiglu_bwd: null pointer"); return 1; }
+  if (da == db) { set_error("eg_swiglu_bwd: da and db must not alias each other"); return 1; }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_swiglu_bwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    if (n % V == 0 && aligned16(dc) && aligned16(a) && aligned16(b) && aligned16(da) &&
+        aligned16(db)) {
+      const int64_t np = n / V;
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, V>), dim3(grid_for(np)), dim3(kBlock), 0, st,
+                         (const T*)dc, (const T*)a, (const T*)b, (T*)da, (T*)db, np);
+    } else {
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, 1>), dim3(grid_for(n)), dim3(kBlock), 0, st,
+                         (const T*)dc, (const T*)a, (const T*)b, (T*)da, (T*)db, n);
+    }
+    return check_launch("eg_swiglu_bwd");
+  });
+}

@@ -1,0 +1,265 @@
+"""Declarations of the six autograd-pair operators this library implements.
+
+Argument names, activity, output and gradient names follow the reference's
+declarations exactly, so a candidate module written against them is the same
+drop-in the reference's harness looks up:
+
+* softmax    src/evograd/ops/level1/softmax/__init__.py:69-92
+* rmsnorm    src/evograd/ops/level1/rmsnorm/__init__.py:72-130
+* layernorm  src/evograd/ops/level1/layernorm/__init__.py:124-171
+* swiglu     src/evograd/ops/level1/swiglu/__init__.py:61-97
+* rope       src/evograd/ops/level1/rope/__init__.py:98-162
+* causal_attention: the reference has no standalone declaration; its semantics
+  are F.scaled_dot_product_attention(q, k, v, is_causal=True) inside
+  src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-108. It is
+  declared here the way an external ``--declaration path.py:op`` would be
+  (src/evograd/opdecl/verify_cli.py:35-38).
+
+Differences from the reference declarations, all deliberate:
+
+* Tolerances are the stricter gate of this build: fp32 (1e-5, 1e-5),
+  fp16 (1e-2, 1e-2), bf16 (2e-2, 2e-2), flat for every output and gradient (the
+  reference uses fp32 2e-5, fp16 5e-2, bf16 8e-2, src/evograd/ops/_common.py:13-17,
+  and widens bf16 parameter gradients by sqrt(rows/8)).
+* ``reference_dtype="float32"``: the oracle runs reduced-precision cases in fp32
+  and casts back (the promotion of src/evograd/opdecl/oracle.py:70-110), so a
+  comparison measures the kernel's error, not the oracle's own bf16 rounding.
+* Each declaration also lists the BASELINE configuration(s) of this build as
+  ``benchmark`` workloads (label "baseline").
+
+``forward``/``runtime_forward`` are "module:function" strings naming the
+CPU-checkable restatement in the repository's ``oracle`` package, which only
+tests and the benchmark's CPU baseline import; ``make_inputs`` names the seeded
+input recipe in ``evograd_amd.inputs``.
+"""
+
+from __future__ import annotations
+
+from .opdecl import Active, Inactive, OpDecl, Workload, declare_op
+
+TOLERANCES = {
+    "float32": (1e-5, 1e-5),
+    "float16": (1e-2, 1e-2),
+    "bfloat16": (2e-2, 2e-2),
+}
+
+
+def _w2(shapes, dtypes, row="rows", col="cols", label=""):
+    return tuple(
+        Workload(dims={row: r, col: c}, dtype=dt, label=label)
+        for (r, c) in shapes
+        for dt in dtypes
+    )
+
+
+# ------------------------------------------------------------------ softmax
+SOFTMAX = declare_op(
+    name="softmax",
+    forward="oracle.forward_refs:softmax_forward_ref",
+    dims=("rows", "cols"),
+    args=(Active("x", "[rows, cols]"),),
+    output=Active("y", "[rows, cols]"),
+    forward_semantics="Numerically stable softmax over the last dimension in fp32.",
+    backward_semantics="Return dx = y * (dy - sum(dy*y, dim=-1, keepdim=True)).",
+    reference_dtype="float32",
+    correctness=(
+        _w2(((8, 512), (16, 1024)), ("float32",))
+        + _w2(((32, 4096), (64, 2048)), ("float16", "bfloat16"))
+        # ragged widths (scalar path), a single row and a vocabulary-wide row
+        # (two-read path)
+        + _w2(((17, 1000), (5, 127), (1, 4096), (3, 131072)), ("float32", "bfloat16"))
+    ),
+    benchmark=_w2(((4096, 4096),), ("float32",), label="baseline"),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_softmax_inputs",
+)
+
+# ------------------------------------------------------------------ rmsnorm
+RMSNORM = declare_op(
+    name="rmsnorm",
+    forward="oracle.forward_refs:rmsnorm_forward_ref",
+    runtime_forward="oracle.forward_refs:rmsnorm_runtime_ref",
+    dims=("rows", "hidden"),
+    args=(
+        Active("x", "[rows, hidden]"),
+        Active("weight", "[hidden]"),
+        Inactive("eps", default=1e-5),
+    ),
+    output=Active("y", "[rows, hidden]"),
+    forward_semantics=(
+        "rrms = rsqrt(mean(x^2, -1) + eps) in fp32; y = ((x * rrms) * weight) cast to "
+        "x's dtype."
+    ),
+    backward_semantics=(
+        "xhat = x * rrms, g = dy * weight: dx = (g - xhat * mean(g * xhat, -1)) * rrms; "
+        "dweight = sum(dy * xhat, dim=0); fp32 accumulation."
+    ),
+    reference_dtype="float32",
+    correctness=(
+        Workload(dims=dict(rows=8, hidden=64), dtype="float32"),
+        Workload(dims=dict(rows=17, hidden=128), dtype="float32"),
+        Workload(dims=dict(rows=32, hidden=256), dtype="float16"),
+        Workload(dims=dict(rows=64, hidden=512), dtype="float16"),
+        Workload(dims=dict(rows=32, hidden=256), dtype="bfloat16"),
+        Workload(dims=dict(rows=64, hidden=512), dtype="bfloat16"),
+        Workload(dims=dict(rows=128, hidden=4096), dtype="bfloat16"),
+        # coverage: single and ragged row counts, non-power-of-two widths,
+        # more rows than backward workgroups, the widest Llama hidden
+        Workload(dims=dict(rows=1, hidden=4096), dtype="bfloat16"),
+        Workload(dims=dict(rows=17, hidden=127), dtype="float32"),
+        Workload(dims=dict(rows=17, hidden=513), dtype="float16"),
+        Workload(dims=dict(rows=17, hidden=1000), dtype="bfloat16"),
+        Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16"),
+        Workload(dims=dict(rows=1024, hidden=8192), dtype="bfloat16"),
+    ),
+    benchmark=(
+        Workload(dims=dict(rows=16384, hidden=4096), dtype="bfloat16", label="baseline",
+                 extra={"eps": 1e-6}),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_rmsnorm_inputs",
+)
+
+# ---------------------------------------------------------------- layernorm
+LAYERNORM = declare_op(
+    name="layernorm",
+    forward="oracle.forward_refs:layernorm_forward_ref",
+    runtime_forward="oracle.forward_refs:layernorm_runtime_ref",
+    dims=("rows", "hidden"),
+    args=(
+        Active("x", "[rows, hidden]"),
+        Active("weight", "[hidden]"),
+        Active("bias", "[hidden]"),
+        Inactive("eps", default=1e-5),
+    ),
+    output=Active("y", "[rows, hidden]"),
+    forward_semantics="Row-wise LayerNorm over the last dimension, statistics in fp32.",
+    backward_semantics=(
+        "Return dx, dweight, dbias from dy, saved state and eps; dtypes follow x, weight "
+        "and bias."
+    ),
+    reference_dtype="float32",
+    correctness=(
+        Workload(dims=dict(rows=8, hidden=64), dtype="float32"),
+        Workload(dims=dict(rows=17, hidden=128), dtype="float32"),
+        Workload(dims=dict(rows=32, hidden=256), dtype="float16"),
+        Workload(dims=dict(rows=64, hidden=512), dtype="float16"),
+        Workload(dims=dict(rows=32, hidden=256), dtype="bfloat16"),
+        Workload(dims=dict(rows=64, hidden=512), dtype="bfloat16"),
+        Workload(dims=dict(rows=128, hidden=4096), dtype="bfloat16"),
+        Workload(dims=dict(rows=1024, hidden=8192), dtype="bfloat16"),
+        Workload(dims=dict(rows=17, hidden=1000), dtype="bfloat16"),
+        Workload(dims=dict(rows=17, hidden=127), dtype="float32"),
+        Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16"),
+    ),
+    benchmark=(
+        Workload(dims=dict(rows=16384, hidden=4096), dtype="bfloat16", label="baseline"),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_layernorm_inputs",
+)
+
+# ------------------------------------------------------------------- swiglu
+SWIGLU = declare_op(
+    name="swiglu",
+    forward="oracle.forward_refs:swiglu_forward_ref",
+    dims=("rows", "cols"),
+    args=(Active("a", "[rows, cols]"), Active("b", "[rows, cols]")),
+    output=Active("c", "[rows, cols]"),
+    forward_semantics="Element-wise c = silu(a) * b, with SiLU evaluated in fp32.",
+    backward_semantics=(
+        "With s=sigmoid(a): db = dc*(a*s), da = dc*b*((a*s)*(1-s)+s). Preserve input dtypes."
+    ),
+    reference_dtype="float32",
+    correctness=(
+        _w2(((8, 64), (17, 128)), ("float32",))
+        + _w2(((32, 256), (64, 512)), ("float16", "bfloat16"))
+        + _w2(((17, 255), (17, 1001), (1, 512)), ("float32", "bfloat16"))
+    ),
+    benchmark=_w2(((16384, 14336),), ("bfloat16",), label="baseline"),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_swiglu_inputs",
+    backward_may_overwrite=("a", "b"),
+)
+
+# --------------------------------------------------------------------- rope
+ROPE = declare_op(
+    name="rope",
+    forward="oracle.forward_refs:rope_forward_ref",
+    dims=("B", "n_heads", "T", "head_dim"),
+    args=(
+        Active("x", "[B, n_heads, T, head_dim]"),
+        Inactive("cos", "[T, head_dim]", note="rotary cosine table, duplicated halves"),
+        Inactive("sin", "[T, head_dim]", note="rotary sine table, same layout as cos"),
+    ),
+    output=Active("y", "[B, n_heads, T, head_dim]"),
+    forward_semantics=(
+        "Half-rotated (GPT-NeoX / Llama) RoPE: y = [x1, x2]*[cos, cos] + [-x2, x1]*[sin, sin] "
+        "in fp32, cast back to x's dtype."
+    ),
+    backward_semantics="dx = [dy1, dy2]*[cos, cos] + [dy2, -dy1]*[sin, sin].",
+    reference_dtype="float32",
+    correctness=tuple(
+        Workload(dims=dict(B=b, n_heads=h, T=t, head_dim=d), dtype=dt)
+        for b, h, t, d in ((1, 4, 16, 64), (2, 8, 128, 128), (1, 32, 129, 128), (1, 3, 7, 10))
+        for dt in ("float32", "float16", "bfloat16")
+    ),
+    benchmark=(
+        # the q half of the joint q/k configuration; the k half has n_heads=8
+        Workload(dims=dict(B=8, n_heads=32, T=4096, head_dim=128), dtype="bfloat16",
+                 label="baseline", extra={"theta": 10000.0, "table_dtype": "float32",
+                                          "k_heads": 8}),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_rope_inputs",
+    memory_inputs=("x",),
+)
+
+# --------------------------------------------------------- causal attention
+CAUSAL_ATTENTION = declare_op(
+    name="causal_attention",
+    forward="oracle.forward_refs:causal_attention_forward_ref",
+    runtime_forward="oracle.forward_refs:causal_attention_runtime_ref",
+    dims=("B", "H", "S", "D"),
+    args=(
+        Active("q", "[B, H, S, D]"),
+        Active("k", "[B, H, S, D]"),
+        Active("v", "[B, H, S, D]"),
+    ),
+    output=Active("o", "[B, H, S, D]"),
+    forward_semantics=(
+        "o = softmax(q @ k^T / sqrt(D) + causal mask) @ v, the semantics of "
+        "F.scaled_dot_product_attention(q, k, v, is_causal=True); fp32 accumulation."
+    ),
+    backward_semantics="Return dq, dk, dv; P is recomputed from the saved logsumexp.",
+    reference_dtype="float32",
+    correctness=tuple(
+        Workload(dims=dict(B=b, H=h, S=s, D=d), dtype=dt)
+        for b, h, s, d in (
+            (1, 1, 1, 128),
+            (1, 2, 64, 64),
+            (2, 4, 128, 128),
+            (1, 2, 129, 128),
+            (1, 3, 200, 64),
+            (1, 4, 1024, 128),
+        )
+        for dt in ("bfloat16", "float16")
+    ),
+    benchmark=(
+        Workload(dims=dict(B=4, H=32, S=4096, D=128), dtype="bfloat16", label="baseline"),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_attention_inputs",
+)
+
+OPS: dict[str, OpDecl] = {
+    op.name: op for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION)
+}
+
+
+def get_op(name: str) -> OpDecl:
+    """Look up a declaration by name (src/evograd/ops/__init__.py:90-99)."""
+    try:
+        return OPS[name]
+    except KeyError:
+        raise KeyError(f"unknown op {name!r}; known: {sorted(OPS)}") from None

@@ -1,0 +1,158 @@
+"""Deterministic seeded synthetic inputs per declared workload.
+
+Restates src/evograd/opdecl/inputs.py:40-75 and the declarations' ``make_inputs``
+recipes (seeds and distributions), so a case means the same tensors here as in
+the reference's harness on the same device type.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .opdecl import Active, OpDecl, Workload, bind_shape
+
+DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16,
+          "float64": torch.float64}
+
+# Llama-3's rotary base (src/evograd/opdecl/models.py:259-261); the BASELINE RoPE
+# configuration overrides it with theta=10000 through the workload's ``extra``.
+LLAMA3_ROPE_THETA = 500000.0
+
+
+def resolve_dtype(name: str) -> torch.dtype:
+    try:
+        return DTYPES[name]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {name!r}") from None
+
+
+def case_seed(workload: Workload) -> int:
+    """Generic per-case seed (inputs.py:40-49)."""
+    seed = 0
+    for name in sorted(workload.dims):
+        seed = seed * 131 + int(workload.dims[name])
+    return seed * 131 + sum(map(ord, workload.dtype))
+
+
+def make_softmax_inputs(op, workload, device="cuda"):
+    """softmax/__init__.py:44-51: seed rows*100003+cols, x then dy ~ N(0,1)."""
+    rows, cols = workload.dims["rows"], workload.dims["cols"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100003 + cols)
+    x = torch.randn((rows, cols), device=device, dtype=dt)
+    dy = torch.randn((rows, cols), device=device, dtype=dt)
+    return {"x": x, "dy": dy}
+
+
+def make_rmsnorm_inputs(op, workload, device="cuda"):
+    """rmsnorm/__init__.py:20-32: seed rows*100000+hidden; x; weight = 1 + 0.1 N(0,1)
+    drawn in fp32 then cast; dy. eps 1e-5 unless the workload says otherwise."""
+    rows, hidden = workload.dims["rows"], workload.dims["hidden"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100000 + hidden)
+    x = torch.randn((rows, hidden), device=device, dtype=dt)
+    weight = (1.0 + 0.1 * torch.randn((hidden,), device=device, dtype=torch.float32)).to(dt)
+    dy = torch.randn((rows, hidden), device=device, dtype=dt)
+    return {"x": x, "weight": weight, "eps": float(workload.extra.get("eps", 1e-5)), "dy": dy}
+
+
+def make_layernorm_inputs(op, workload, device="cuda"):
+    """layernorm/__init__.py:16-24: seed rows*100000+hidden; x, weight, bias, dy ~ N(0,1)."""
+    rows, hidden = workload.dims["rows"], workload.dims["hidden"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100000 + hidden)
+    x = torch.randn((rows, hidden), device=device, dtype=dt)
+    weight = torch.randn((hidden,), device=device, dtype=dt)
+    bias = torch.randn((hidden,), device=device, dtype=dt)
+    dy = torch.randn((rows, hidden), device=device, dtype=dt)
+    return {"x": x, "weight": weight, "bias": bias,
+            "eps": float(workload.extra.get("eps", 1e-5)), "dy": dy}
+
+
+def make_swiglu_inputs(op, workload, device="cuda"):
+    """swiglu/__init__.py:44-52: seed rows*100003+cols; a, b, dc ~ N(0,1)."""
+    rows, cols = workload.dims["rows"], workload.dims["cols"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100003 + cols)
+    a = torch.randn((rows, cols), device=device, dtype=dt)
+    b = torch.randn((rows, cols), device=device, dtype=dt)
+    dc = torch.randn((rows, cols), device=device, dtype=dt)
+    return {"a": a, "b": b, "dc": dc}
+
+
+def rope_tables(tokens: int, head_dim: int, theta: float, dtype, device):
+    """cos/sin [tokens, head_dim] with duplicated halves (rope/__init__.py:47-59):
+    angle[t, i] = t * theta^(-2i/head_dim), i < head_dim/2."""
+    positions = torch.arange(tokens, device=device, dtype=torch.float32)[:, None]
+    inv_freq = theta ** (
+        -torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim
+    )
+    freqs = positions * inv_freq[None, :]
+    angles = torch.cat((freqs, freqs), dim=-1)
+    return angles.cos().to(dtype), angles.sin().to(dtype)
+
+
+def make_rope_inputs(op, workload, device="cuda"):
+    """rope/__init__.py:30-62: seed T*100003 + heads*1009 + head_dim; x = 0.5 N(0,1);
+    tables at Llama-3's theta cast to x's dtype; dy = 0.5 N(0,1). A workload's
+    ``extra`` may set theta, table_dtype and x_scale (the BASELINE case uses
+    theta 10000, fp32 tables and unit-variance x)."""
+    d = workload.dims
+    B, H, T, D = d["B"], d["n_heads"], d["T"], d["head_dim"]
+    if D % 2:
+        raise ValueError(f"rope needs an even head_dim, got {D}")
+    dt = resolve_dtype(workload.dtype)
+    scale = float(workload.extra.get("x_scale", 0.5 if workload.label != "baseline" else 1.0))
+    torch.manual_seed(T * 100003 + H * 1009 + D)
+    x = torch.randn((B, H, T, D), device=device, dtype=dt) * scale
+    theta = float(workload.extra.get("theta", LLAMA3_ROPE_THETA))
+    tdt = resolve_dtype(workload.extra.get("table_dtype", workload.dtype))
+    cos, sin = rope_tables(T, D, theta, tdt, device)
+    dy = torch.randn((B, H, T, D), device=device, dtype=dt) * scale
+    return {"x": x, "cos": cos, "sin": sin, "dy": dy}
+
+
+def make_attention_inputs(op, workload, device="cuda"):
+    """Generic seed (inputs.py:40-49); q, k, v, do ~ N(0,1) as the BASELINE
+    attention configuration specifies."""
+    d = workload.dims
+    shape = (d["B"], d["H"], d["S"], d["D"])
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(case_seed(workload))
+    q = torch.randn(shape, device=device, dtype=dt)
+    k = torch.randn(shape, device=device, dtype=dt)
+    v = torch.randn(shape, device=device, dtype=dt)
+    do = torch.randn(shape, device=device, dtype=dt)
+    return {"q": q, "k": k, "v": v, "do": do}
+
+
+RECIPES = {
+    "make_softmax_inputs": make_softmax_inputs,
+    "make_rmsnorm_inputs": make_rmsnorm_inputs,
+    "make_layernorm_inputs": make_layernorm_inputs,
+    "make_swiglu_inputs": make_swiglu_inputs,
+    "make_rope_inputs": make_rope_inputs,
+    "make_attention_inputs": make_attention_inputs,
+}
+
+
+def make_case_inputs(op: OpDecl, workload: Workload, device: str = "cuda") -> dict:
+    """All primals plus the upstream gradient keyed by declared names (inputs.py:52-75)."""
+    if op.make_inputs is not None:
+        _, _, fn = op.make_inputs.partition(":")
+        return RECIPES[fn](op, workload, device)
+    torch.manual_seed(case_seed(workload))
+    values: dict = {}
+    dt = resolve_dtype(workload.dtype)
+    for arg in op.args:
+        if isinstance(arg, Active):
+            values[arg.name] = torch.randn(bind_shape(arg.shape, workload.dims), device=device,
+                                           dtype=dt) * 0.5
+        elif arg.is_tensor:
+            values[arg.name] = torch.zeros(bind_shape(arg.shape, workload.dims), device=device,
+                                           dtype=dt)
+        else:
+            values[arg.name] = arg.default
+    values[op.upstream_grad_name] = torch.randn(
+        bind_shape(op.output.shape, workload.dims), device=device, dtype=dt) * 0.5
+    return values

@@ -1,0 +1,158 @@
+/*
+ * evograd_hip.h — C ABI of libevograd_hip.so, the gfx950 (MI355X) kernels behind
+ * evograd's autograd-pair hot path.
+ *
+ * The reference (akumdam2/evograd) has no native code: each operator's pair is a
+ * Python module exposing
+ *     <op>_forward_with_saved(*declared args) -> (y, saved)
+ *     <op>_backward_from_saved(dy, saved, **scalar inactive args) -> grads
+ * found by src/evograd/opdecl/bind.py:28-47 (lookup_pair) and called by
+ * src/evograd/opdecl/verify.py:118-143 and src/evograd/bench/harness.py:216-349.
+ * Every entry point below is one kernel launch sequence that such a module calls.
+ * The citation on each names the reference computation it replaces.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers to contiguous row-major tensors. The caller
+ *     owns every buffer: outputs, saved state and workspace are allocated by the
+ *     caller (in the Python modules: torch.empty on the caching allocator).
+ *     The library never allocates, frees or synchronises.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the
+ *     legacy default stream).
+ *   - Return 0 on success. A non-zero return means nothing was launched (or the
+ *     launch itself failed); eg_last_error() then describes why. The message
+ *     buffer is thread-local.
+ *   - `dtype` is one of eg_dtype. Reductions always accumulate in fp32.
+ *   - Results are deterministic: no atomics; every reduction has a fixed order.
+ */
+#ifndef EVOGRAD_HIP_H
+#define EVOGRAD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  EG_F32 = 0,
+  EG_F16 = 1,
+  EG_BF16 = 2,
+} eg_dtype;
+
+/* ABI version of this header; bumped on any signature change. */
+int eg_abi_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* eg_last_error(void);
+
+/* ---------------------------------------------------------------- softmax
+ * Replaces softmax_forward_ref (src/evograd/ops/level1/softmax/forward_ref.py:6-7):
+ *   y = softmax(x.float(), dim=-1).to(x.dtype), x and y [rows, cols].
+ * Saved state is y itself. */
+int eg_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
+                   void* stream);
+
+/* Replaces the autograd backward of softmax_forward_ref, declared at
+ * src/evograd/ops/level1/softmax/__init__.py:78:
+ *   dx = y * (dy - sum(dy * y, -1)), accumulated in fp32. */
+int eg_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_t cols,
+                   int dtype, void* stream);
+
+/* ---------------------------------------------------------------- rmsnorm
+ * Replaces rmsnorm_forward_ref (src/evograd/ops/level1/rmsnorm/forward_ref.py:6-21):
+ *   rstd = rsqrt(mean(x^2, -1) + eps); y = ((x * rstd) * weight).to(x.dtype)
+ * x, y [rows, hidden] (dtype); weight [hidden] (dtype); rstd [rows] fp32 (saved). */
+int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd, int64_t rows,
+                   int64_t hidden, float eps, int dtype, void* stream);
+
+/* Bytes of fp32 workspace eg_rmsnorm_bwd needs for its per-block dweight partials. */
+size_t eg_rmsnorm_workspace_bytes(int64_t rows, int64_t hidden);
+
+/* Replaces the autograd backward of rmsnorm_forward_ref, declared at
+ * src/evograd/ops/level1/rmsnorm/__init__.py:85-86:
+ *   xhat = x * rstd, g = dy * weight
+ *   dx = (g - xhat * mean(g * xhat, -1)) * rstd
+ *   dweight = sum_rows(dy * xhat)   (two stages: per-block partials, fixed-order sum) */
+int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const float* rstd,
+                   void* dx, void* dweight, void* workspace, int64_t rows, int64_t hidden,
+                   int dtype, void* stream);
+
+/* -------------------------------------------------------------- layernorm
+ * Replaces layernorm_forward_ref (src/evograd/ops/level1/layernorm/forward_ref.py:6-23):
+ *   mean = mean(x, -1); var = mean((x - mean)^2, -1); rstd = rsqrt(var + eps)
+ *   y = ((x - mean) * rstd * weight + bias).to(x.dtype)
+ * mean, rstd [rows] fp32 are saved. */
+int eg_layernorm_fwd(const void* x, const void* weight, const void* bias, void* y,
+                     float* mean, float* rstd, int64_t rows, int64_t hidden, float eps,
+                     int dtype, void* stream);
+
+/* Bytes of fp32 workspace eg_layernorm_bwd needs (dweight and dbias partials). */
+size_t eg_layernorm_workspace_bytes(int64_t rows, int64_t hidden);
+
+/* Replaces the autograd backward of layernorm_forward_ref
+ * (src/evograd/ops/level1/layernorm/__init__.py:124-171 declares dx, dweight, dbias):
+ *   xhat = (x - mean) * rstd, g = dy * weight
+ *   dx = rstd * (g - mean(g, -1) - xhat * mean(g * xhat, -1))
+ *   dweight = sum_rows(dy * xhat), dbias = sum_rows(dy)   (two-stage, fixed order) */
+int eg_layernorm_bwd(const void* dy, const void* x, const void* weight, const float* mean,
+                     const float* rstd, void* dx, void* dweight, void* dbias,
+                     void* workspace, int64_t rows, int64_t hidden, int dtype,
+                     void* stream);
+
+/* ----------------------------------------------------------------- swiglu
+ * Replaces swiglu_forward_ref (src/evograd/ops/level1/swiglu/forward_ref.py:6-9):
+ *   c = silu(a.float()).to(a.dtype) * b    (the silu is rounded to dtype first)
+ * a, b, c hold n elements. */
+int eg_swiglu_fwd(const void* a, const void* b, void* c, int64_t n, int dtype,
+                  void* stream);
+
+/* Replaces the autograd backward declared at
+ * src/evograd/ops/level1/swiglu/__init__.py:70-73, sigmoid recomputed from a:
+ *   s = sigmoid(a); db = dc * a * s; da = dc * b * (s + a * s * (1 - s))
+ * da may alias a and db may alias b (backward_may_overwrite, :96): each element
+ * is read before it is written, by the same thread. */
+int eg_swiglu_bwd(const void* dc, const void* a, const void* b, void* da, void* db,
+                  int64_t n, int dtype, void* stream);
+
+/* ------------------------------------------------------------------- rope
+ * Replaces rope_forward_ref (src/evograd/ops/level1/rope/forward_ref.py:28-47),
+ * half-rotated layout, for up to two tensors in one launch (q and k of a GQA layer):
+ *   y = x * cos + rotate_half(x) * sin, rotate_half(x) = [-x2, x1], in fp32.
+ * q [batch, heads_q, tokens, head_dim], k [batch, heads_k, tokens, head_dim]
+ * (k, k_out may be NULL with heads_k = 0); cos, sin [tokens, head_dim] of
+ * table_dtype (EG_F32 or the same dtype as q). `inverse` = 1 applies the
+ * transpose rotation (sin negated): the backward declared at
+ * src/evograd/ops/level1/rope/__init__.py:124-130. Out-of-place only. */
+int eg_rope(const void* q, const void* k, void* q_out, void* k_out, const void* cos,
+            const void* sin, int64_t batch, int64_t heads_q, int64_t heads_k,
+            int64_t tokens, int64_t head_dim, int dtype, int table_dtype, int inverse,
+            void* stream);
+
+/* ------------------------------------------------------ causal attention
+ * Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True) as used by
+ * src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:107:
+ *   o = softmax(q k^T * scale + causal mask) v
+ * q, k, v, o [batch, heads, seq, head_dim] (EG_BF16 or EG_F16); lse [batch, heads, seq]
+ * fp32 = logsumexp of the scaled, masked scores (saved). head_dim must be 64 or 128. */
+int eg_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float scale,
+                int dtype, void* stream);
+
+/* Bytes of workspace eg_attn_bwd needs (delta = rowsum(do * o) fp32 and a
+ * partial-dq accumulator). */
+size_t eg_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t seq,
+                               int64_t head_dim);
+
+/* Backward of the above: P is recomputed from q, k and lse; produces dq, dk, dv
+ * of q's dtype. */
+int eg_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                const void* o, const float* lse, void* dq, void* dk, void* dv,
+                void* workspace, int64_t batch, int64_t heads, int64_t seq,
+                int64_t head_dim, float scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EVOGRAD_HIP_H */

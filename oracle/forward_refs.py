@@ -1,0 +1,114 @@
+"""Trusted forwards, restated from the reference (test infrastructure only).
+
+Each function is the mathematics the reference's oracle differentiates; the
+citation names the file it restates.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def softmax_forward_ref(x: torch.Tensor) -> torch.Tensor:
+    """src/evograd/ops/level1/softmax/forward_ref.py:6-7."""
+    return torch.softmax(x.float(), dim=-1).to(x.dtype)
+
+
+def rmsnorm_forward_ref(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """src/evograd/ops/level1/rmsnorm/forward_ref.py:6-21."""
+    if x.ndim != 2:
+        raise ValueError(f"expected x to be 2D, got shape {tuple(x.shape)}")
+    if weight.ndim != 1 or weight.shape[0] != x.shape[1]:
+        raise ValueError("weight must be 1D with length hidden")
+    x32 = x.float()
+    ms = torch.mean(x32 * x32, dim=-1, keepdim=True)
+    x_hat = x32 * torch.rsqrt(ms + eps)
+    return (x_hat * weight.float()).to(x.dtype)
+
+
+def rmsnorm_runtime_ref(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """src/evograd/ops/level1/rmsnorm/forward_ref.py:24-34 (the fused spelling timed
+    as the eager baseline)."""
+    return F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
+
+
+def layernorm_forward_ref(x, weight, bias, eps: float = 1e-5):
+    """src/evograd/ops/level1/layernorm/forward_ref.py:6-23."""
+    if x.ndim != 2:
+        raise ValueError(f"expected x to be 2D, got shape {tuple(x.shape)}")
+    if weight.ndim != 1 or bias.ndim != 1:
+        raise ValueError("weight and bias must be 1D tensors")
+    x32 = x.float()
+    mean = torch.mean(x32, dim=-1, keepdim=True)
+    var = torch.mean((x32 - mean) ** 2, dim=-1, keepdim=True)
+    x_hat = (x32 - mean) * torch.rsqrt(var + eps)
+    return (x_hat * weight.float() + bias.float()).to(x.dtype)
+
+
+def layernorm_runtime_ref(x, weight, bias, eps: float = 1e-5):
+    """src/evograd/ops/level1/layernorm/forward_ref.py:26-42."""
+    return F.layer_norm(x, (x.shape[-1],), weight=weight, bias=bias, eps=eps)
+
+
+def swiglu_forward_ref(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """src/evograd/ops/level1/swiglu/forward_ref.py:6-9."""
+    if a.shape != b.shape:
+        raise ValueError(f"a and b must have the same shape, got {a.shape} and {b.shape}")
+    return F.silu(a.float()).to(a.dtype) * b
+
+
+def _rotate_half(x):
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def rope_forward_ref(x, cos, sin):
+    """src/evograd/ops/level1/rope/forward_ref.py:28-47 (half-rotated layout)."""
+    if x.ndim != 4:
+        raise ValueError(f"rope expects [batch, heads, tokens, head_dim], got {tuple(x.shape)}")
+    c = cos[None, None].float()
+    s = sin[None, None].float()
+    x32 = x.float()
+    return (x32 * c + _rotate_half(x32) * s).to(x.dtype)
+
+
+def causal_attention_forward_ref(q, k, v):
+    """Causal SDPA written out: softmax(q k^T / sqrt(D) + mask) v, the semantics of
+    F.scaled_dot_product_attention(q, k, v, is_causal=True) at
+    src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:107. Scores and
+    probabilities in fp32; the result is cast to q's dtype."""
+    S, D = q.shape[-2], q.shape[-1]
+    scale = 1.0 / (D ** 0.5)
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) * scale
+    mask = torch.ones(S, S, dtype=torch.bool, device=q.device).triu_(1)
+    s = s.masked_fill(mask, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, v.float()).to(q.dtype)
+
+
+def causal_attention_runtime_ref(q, k, v):
+    """The eager PyTorch call the reference makes (llama3_decoder_layer/forward_ref.py:107)."""
+    return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+
+
+def causal_attention_lse_ref(q, k):
+    """logsumexp over keys of the scaled, causally masked scores, fp32 [B, H, S]:
+    the statistic the attention forward saves."""
+    S, D = q.shape[-2], q.shape[-1]
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) * (1.0 / D ** 0.5)
+    mask = torch.ones(S, S, dtype=torch.bool, device=q.device).triu_(1)
+    return torch.logsumexp(s.masked_fill(mask, float("-inf")), dim=-1)
+
+
+FORWARDS = {
+    "softmax_forward_ref": softmax_forward_ref,
+    "rmsnorm_forward_ref": rmsnorm_forward_ref,
+    "rmsnorm_runtime_ref": rmsnorm_runtime_ref,
+    "layernorm_forward_ref": layernorm_forward_ref,
+    "layernorm_runtime_ref": layernorm_runtime_ref,
+    "swiglu_forward_ref": swiglu_forward_ref,
+    "rope_forward_ref": rope_forward_ref,
+    "causal_attention_forward_ref": causal_attention_forward_ref,
+    "causal_attention_runtime_ref": causal_attention_runtime_ref,
+}

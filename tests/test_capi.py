@@ -1,0 +1,67 @@
+"""The C-ABI library builds, loads and exports exactly what include/evograd_hip.h
+declares; the Python binding declares the same set. No kernel is launched."""
+
+import os
+import re
+
+import pytest
+import torch
+
+from evograd_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "evograd_hip.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(eg_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    syms = header_symbols()
+    assert syms == set(_lib.SIGNATURES), syms ^ set(_lib.SIGNATURES)
+
+
+def test_binding_arity_matches_header():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), (name, params, args)
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_library_loads_and_exports_every_symbol():
+    lib = _lib.load()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+    assert lib.eg_abi_version() == _lib.ABI_VERSION
+    assert lib.eg_last_error() is not None
+    # size queries are pure host arithmetic
+    assert lib.eg_rmsnorm_workspace_bytes(16384, 4096) == 512 * 4096 * 4
+    assert lib.eg_layernorm_workspace_bytes(3, 64) == 2 * 3 * 64 * 4
+    assert lib.eg_rmsnorm_workspace_bytes(0, 64) == 0
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_host_side_validation_errors_without_gpu():
+    """Argument errors are reported before any launch (no device needed)."""
+    with pytest.raises(RuntimeError, match="negative"):
+        _lib.call("eg_softmax_fwd", None, None, -1, 4, _lib.EG_F32, None)
+    with pytest.raises(RuntimeError, match="even"):
+        _lib.call("eg_rope", None, None, None, None, None, None, 1, 1, 0, 4, 5, 0, 0, 0, None)
+    with pytest.raises(RuntimeError, match="dtype"):
+        _lib.call("eg_swiglu_fwd", 16, 16, 16, 8, 7, None)
+    # empty inputs are a no-op, not an error
+    _lib.call("eg_softmax_fwd", None, None, 0, 0, _lib.EG_F32, None)
+
+
+def test_pairs_refuse_cpu_tensors():
+    from evograd_amd.pairs import rmsnorm, softmax
+
+    with pytest.raises(RuntimeError, match="GPU"):
+        softmax.softmax_forward_with_saved(torch.zeros(2, 4))
+    with pytest.raises(RuntimeError, match="GPU"):
+        rmsnorm.rmsnorm_forward_with_saved(torch.zeros(2, 4), torch.ones(4))

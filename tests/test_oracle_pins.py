@@ -1,0 +1,311 @@
+"""Pins for every function of the oracle package (CPU, fp64 where it matters).
+
+The reference ships no golden vectors for these operators (its tests pin the
+oracle only on a toy op, tests/test_opdecl_torch.py:119-130), so each restated
+forward is pinned by what the mathematics fixes — closed forms, invariants,
+special cases, brute force — and each oracle gradient by central finite
+differences of the forward in fp64. Each check is chosen so that a plausible
+slip (dropped eps, wrong rotation convention, missing causal mask, transposed
+operand, wrong sign) fails at least one of them.
+"""
+
+import math
+
+import pytest
+import torch
+
+from evograd_amd import decls
+from evograd_amd.opdecl import Workload
+from oracle import forward_refs as fr
+from evograd_amd.inputs import case_seed, make_case_inputs, rope_tables
+from oracle.oracle import oracle
+
+torch.set_grad_enabled(True)
+
+
+def _fd_check(op, inputs, h=1e-3, tol=1e-3):
+    """<grad_i, v_i> == d/dt <dy, f(x + t v)> at t=0 for a random direction v on
+    every Active input (central differences). The restated forwards evaluate in
+    fp32 internally (``x.float()``, as the reference's do), so the step and the
+    tolerance are sized for fp32 rounding; a wrong term or sign misses by O(1)."""
+    fwd = fr.FORWARDS[op.forward.split(":")[1]]
+    y, grads = oracle(op, inputs, use_reference_dtype=False)
+    gen = torch.Generator().manual_seed(7)
+    actives = op.active_args()
+    dirs = {a.name: torch.randn(inputs[a.name].shape, generator=gen, dtype=torch.float64)
+            for a in actives}
+    dy = inputs[op.upstream_grad_name]
+
+    def f(t):
+        args = []
+        for a in op.args:
+            v = inputs.get(a.name, getattr(a, "default", None))
+            if a.name in dirs:
+                v = v + t * dirs[a.name]
+            args.append(v)
+        return (fwd(*args) * dy).sum().item()
+
+    numeric = (f(h) - f(-h)) / (2 * h)
+    analytic = sum((grads[a.grad_name] * dirs[a.name]).sum().item() for a in actives)
+    assert abs(numeric - analytic) <= tol * max(1.0, abs(analytic)), (op.name, numeric, analytic)
+
+
+def _f64(inputs):
+    return {k: (v.double() if torch.is_tensor(v) and v.is_floating_point() else v)
+            for k, v in inputs.items()}
+
+
+# ------------------------------------------------------------------ softmax
+def test_softmax_forward_closed_forms():
+    x = torch.tensor([[0.0, math.log(2.0)], [5.0, 5.0]], dtype=torch.float64)
+    y = fr.softmax_forward_ref(x)
+    assert torch.allclose(y, torch.tensor([[1 / 3, 2 / 3], [0.5, 0.5]], dtype=torch.float64))
+    x = torch.randn(6, 33, dtype=torch.float64)
+    y = fr.softmax_forward_ref(x)
+    assert torch.allclose(y.sum(-1), torch.ones(6, dtype=torch.float64))
+    assert torch.allclose(fr.softmax_forward_ref(x + 3.5), y)  # shift invariance
+    hot = torch.zeros(1, 9, dtype=torch.float64)
+    hot[0, 4] = 200.0
+    assert torch.allclose(fr.softmax_forward_ref(hot), torch.nn.functional.one_hot(
+        torch.tensor([4]), 9).double())
+    assert fr.softmax_forward_ref(x.float()).dtype == torch.float32
+
+
+def test_softmax_gradient_fd_and_rowsum():
+    inputs = _f64(make_case_inputs(decls.SOFTMAX, Workload(dims=dict(rows=4, cols=37),
+                                                           dtype="float32"), "cpu"))
+    _fd_check(decls.SOFTMAX, inputs)
+    _, g = oracle(decls.SOFTMAX, inputs, use_reference_dtype=False)
+    # dx is orthogonal to the all-ones direction (softmax is shift invariant)
+    assert torch.allclose(g["dx"].sum(-1), torch.zeros(4, dtype=torch.float64), atol=1e-6)
+
+
+# ------------------------------------------------------------------ rmsnorm
+def test_rmsnorm_forward_closed_forms():
+    w = torch.tensor([1.0, 2.0, -0.5, 3.0], dtype=torch.float64)
+    x = torch.full((2, 4), 3.0, dtype=torch.float64)
+    x[1] = -0.25
+    y = fr.rmsnorm_forward_ref(x, w, eps=0.0)
+    assert torch.allclose(y, torch.stack([w, -w]))
+    # eps enters inside the rsqrt: mean(x^2) = 9, rstd = 1/sqrt(9 + eps)
+    y = fr.rmsnorm_forward_ref(x[:1], w, eps=7.0)
+    assert torch.allclose(y, 3.0 * w / 4.0)
+    x = torch.randn(5, 64, dtype=torch.float64)
+    y = fr.rmsnorm_forward_ref(x, torch.ones(64, dtype=torch.float64), eps=0.0)
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(5, dtype=torch.float64))
+    assert torch.allclose(fr.rmsnorm_forward_ref(4 * x, w.repeat(16), 0.0),
+                          fr.rmsnorm_forward_ref(x, w.repeat(16), 0.0))
+
+
+def test_rmsnorm_gradient_fd_and_brute_force_dweight():
+    inputs = _f64(make_case_inputs(decls.RMSNORM, Workload(dims=dict(rows=5, hidden=24),
+                                                           dtype="float32"), "cpu"))
+    _fd_check(decls.RMSNORM, inputs)
+    _, g = oracle(decls.RMSNORM, inputs, use_reference_dtype=False)
+    x, dy, eps = inputs["x"], inputs["dy"], inputs["eps"]
+    dw = torch.zeros(24, dtype=torch.float64)
+    for r in range(5):
+        xh = x[r] / math.sqrt(float((x[r] ** 2).mean()) + eps)
+        dw += dy[r] * xh
+    assert torch.allclose(g["dweight"], dw)
+
+
+# ---------------------------------------------------------------- layernorm
+def test_layernorm_forward_closed_forms():
+    x = torch.randn(4, 50, dtype=torch.float64) * 3 + 2
+    one, zero = torch.ones(50, dtype=torch.float64), torch.zeros(50, dtype=torch.float64)
+    y = fr.layernorm_forward_ref(x, one, zero, eps=0.0)
+    assert torch.allclose(y.mean(-1), torch.zeros(4, dtype=torch.float64), atol=1e-6)
+    assert torch.allclose(y.var(-1, unbiased=False), torch.ones(4, dtype=torch.float64))
+    b = torch.randn(50, dtype=torch.float64)
+    assert torch.allclose(fr.layernorm_forward_ref(x, zero, b), b.expand(4, 50))
+    assert torch.allclose(fr.layernorm_forward_ref(x + 10, one, zero, 0.0), y, atol=1e-5)
+    # biased variance with eps inside the rsqrt: row [1, 3] -> var 1
+    r = fr.layernorm_forward_ref(torch.tensor([[1.0, 3.0]], dtype=torch.float64),
+                                 torch.ones(2, dtype=torch.float64),
+                                 torch.zeros(2, dtype=torch.float64), eps=3.0)
+    assert torch.allclose(r, torch.tensor([[-0.5, 0.5]], dtype=torch.float64))
+
+
+def test_layernorm_gradient_fd_and_sums():
+    inputs = _f64(make_case_inputs(decls.LAYERNORM, Workload(dims=dict(rows=6, hidden=20),
+                                                             dtype="float32"), "cpu"))
+    _fd_check(decls.LAYERNORM, inputs)
+    _, g = oracle(decls.LAYERNORM, inputs, use_reference_dtype=False)
+    assert torch.allclose(g["dbias"], inputs["dy"].sum(0))
+    # with unit weight, dx of each row sums to zero (shift invariance)
+    inputs["weight"] = torch.ones_like(inputs["weight"])
+    _, g = oracle(decls.LAYERNORM, inputs, use_reference_dtype=False)
+    assert torch.allclose(g["dx"].sum(-1), torch.zeros(6, dtype=torch.float64), atol=1e-5)
+
+
+# ------------------------------------------------------------------- swiglu
+def test_swiglu_closed_forms():
+    a = torch.tensor([0.0, 1.0, 40.0, -40.0], dtype=torch.float64)
+    b = torch.tensor([3.0, 2.0, 0.5, 7.0], dtype=torch.float64)
+    c = fr.swiglu_forward_ref(a, b)
+    expect = torch.tensor([0.0, 2.0 / (1 + math.exp(-1.0)), 20.0, 0.0], dtype=torch.float64)
+    assert torch.allclose(c, expect, atol=1e-6)
+    inputs = {"a": torch.zeros(3, dtype=torch.float64), "b": torch.tensor([1.0, -2.0, 4.0],
+              dtype=torch.float64), "dc": torch.tensor([2.0, 1.0, 0.5], dtype=torch.float64)}
+    _, g = oracle(decls.SWIGLU, inputs, use_reference_dtype=False)
+    assert torch.allclose(g["da"], inputs["dc"] * inputs["b"] / 2)  # silu'(0) = 1/2
+    assert torch.allclose(g["db"], torch.zeros(3, dtype=torch.float64))
+
+
+def test_swiglu_rounds_silu_before_the_product():
+    # bf16: silu(a) is rounded to bf16 first, then the bf16 product rounds again
+    a = torch.tensor([0.3359375], dtype=torch.bfloat16)
+    b = torch.tensor([3.015625], dtype=torch.bfloat16)
+    s = torch.nn.functional.silu(a.float()).to(torch.bfloat16)
+    assert fr.swiglu_forward_ref(a, b).item() == (s * b).item()
+
+
+def test_swiglu_gradient_fd():
+    inputs = _f64(make_case_inputs(decls.SWIGLU, Workload(dims=dict(rows=3, cols=11),
+                                                          dtype="float32"), "cpu"))
+    _fd_check(decls.SWIGLU, inputs)
+
+
+# --------------------------------------------------------------------- rope
+def test_rope_tables_closed_form():
+    cos, sin = rope_tables(5, 8, 10000.0, torch.float64, "cpu")
+    for t in range(5):
+        for i in range(4):
+            ang = t * 10000.0 ** (-2 * i / 8)
+            assert abs(cos[t, i] - math.cos(ang)) < 1e-6
+            assert abs(cos[t, i + 4] - math.cos(ang)) < 1e-6
+            assert abs(sin[t, i] - math.sin(ang)) < 1e-6
+
+
+def test_rope_forward_half_rotation_convention():
+    # head_dim 4: pairs are (0, 2) and (1, 3) — not the interleaved (0, 1), (2, 3)
+    x = torch.tensor([1.0, 2.0, 3.0, 4.0], dtype=torch.float64).view(1, 1, 1, 4)
+    c = torch.tensor([[0.6, 0.8, 0.6, 0.8]], dtype=torch.float64)
+    s = torch.tensor([[0.8, 0.6, 0.8, 0.6]], dtype=torch.float64)
+    y = fr.rope_forward_ref(x, c, s).view(4)
+    expect = [1 * 0.6 - 3 * 0.8, 2 * 0.8 - 4 * 0.6, 3 * 0.6 + 1 * 0.8, 4 * 0.8 + 2 * 0.6]
+    assert torch.allclose(y, torch.tensor(expect, dtype=torch.float64))
+
+
+def test_rope_norm_preservation_identity_and_inverse():
+    x = torch.randn(2, 3, 9, 16, dtype=torch.float64)
+    cos, sin = rope_tables(9, 16, 10000.0, torch.float64, "cpu")
+    y = fr.rope_forward_ref(x, cos, sin)
+    pair = lambda t: t[..., :8] ** 2 + t[..., 8:] ** 2  # noqa: E731
+    assert torch.allclose(pair(y), pair(x), atol=1e-6)  # each (i, i+half) pair keeps its norm
+    assert torch.allclose(y[:, :, 0], x[:, :, 0], atol=1e-6)  # position 0 is the identity
+    back = fr.rope_forward_ref(y, cos, -sin)
+    assert torch.allclose(back, x, atol=1e-6)
+
+
+def test_rope_gradient_is_inverse_rotation():
+    w = Workload(dims=dict(B=1, n_heads=2, T=7, head_dim=12), dtype="float32")
+    inputs = _f64(make_case_inputs(decls.ROPE, w, "cpu"))
+    _fd_check(decls.ROPE, inputs)
+    _, g = oracle(decls.ROPE, inputs, use_reference_dtype=False)
+    assert set(g) == {"dx"}
+    assert torch.allclose(g["dx"], fr.rope_forward_ref(inputs["dy"], inputs["cos"], -inputs["sin"]))
+
+
+# --------------------------------------------------------- causal attention
+def _attn_brute(q, k, v):
+    B, H, S, D = q.shape
+    o = torch.zeros_like(q)
+    lse = torch.zeros(B, H, S, dtype=q.dtype)
+    for b in range(B):
+        for h in range(H):
+            for t in range(S):
+                sc = [float(q[b, h, t] @ k[b, h, j]) / math.sqrt(D) for j in range(t + 1)]
+                m = max(sc)
+                e = [math.exp(s - m) for s in sc]
+                z = sum(e)
+                lse[b, h, t] = m + math.log(z)
+                for j in range(t + 1):
+                    o[b, h, t] += e[j] / z * v[b, h, j]
+    return o, lse
+
+
+def test_attention_forward_brute_force_and_lse():
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 6, 8, generator=g, dtype=torch.float64) for _ in range(3))
+    o_ref, lse_ref = _attn_brute(q, k, v)
+    assert torch.allclose(fr.causal_attention_forward_ref(q, k, v).double(), o_ref)
+    assert torch.allclose(fr.causal_attention_lse_ref(q, k).double(), lse_ref)
+    sdpa = fr.causal_attention_runtime_ref(q, k, v)
+    assert torch.allclose(sdpa, o_ref)
+
+
+def test_attention_special_cases():
+    v = torch.randn(1, 1, 5, 4, dtype=torch.float64)
+    q = torch.zeros(1, 1, 5, 4, dtype=torch.float64)
+    k = torch.randn(1, 1, 5, 4, dtype=torch.float64)
+    o = fr.causal_attention_forward_ref(q, k, v).double()
+    prefix_mean = torch.cumsum(v, 2) / torch.arange(1, 6, dtype=torch.float64).view(1, 1, 5, 1)
+    assert torch.allclose(o, prefix_mean)  # uniform scores -> prefix mean of v
+    lse = fr.causal_attention_lse_ref(q, k).double()
+    assert torch.allclose(lse.view(5), torch.log(torch.arange(1, 6, dtype=torch.float64)))
+    one = torch.randn(1, 3, 1, 8, dtype=torch.float64)
+    assert torch.allclose(fr.causal_attention_forward_ref(one, one * 2, one * 3).double(),
+                          one * 3)  # S = 1 -> o = v
+    # causality: changing a later key/value leaves earlier outputs unchanged
+    q2, k2, v2 = (torch.randn(1, 1, 6, 4, dtype=torch.float64) for _ in range(3))
+    base = fr.causal_attention_forward_ref(q2, k2, v2).double()
+    k3, v3 = k2.clone(), v2.clone()
+    k3[..., 4, :] += 5
+    v3[..., 4, :] -= 5
+    moved = fr.causal_attention_forward_ref(q2, k3, v3).double()
+    assert torch.allclose(moved[..., :4, :], base[..., :4, :])
+    assert not torch.allclose(moved[..., 4:, :], base[..., 4:, :])
+
+
+def test_attention_gradient_fd():
+    w = Workload(dims=dict(B=1, H=2, S=5, D=4), dtype="float32")
+    inputs = _f64(make_case_inputs(decls.CAUSAL_ATTENTION, w, "cpu"))
+    _fd_check(decls.CAUSAL_ATTENTION, inputs)
+
+
+# ------------------------------------------------------- oracle machinery
+def test_oracle_promotes_and_casts_back():
+    w = Workload(dims=dict(rows=4, hidden=32), dtype="bfloat16")
+    inputs = make_case_inputs(decls.RMSNORM, w, "cpu")
+    y, g = oracle(decls.RMSNORM, inputs)
+    assert y.dtype == torch.bfloat16
+    assert g["dx"].dtype == torch.bfloat16 and g["dweight"].dtype == torch.bfloat16
+    assert list(g) == ["dx", "dweight"]
+    # promoted oracle == fp32 computation rounded once
+    x32 = {k: (v.float() if torch.is_tensor(v) else v) for k, v in inputs.items()}
+    y32, g32 = oracle(decls.RMSNORM, x32)
+    assert torch.equal(y, y32.bfloat16())
+    assert torch.equal(g["dx"], g32["dx"].bfloat16())
+    # Inactive tensors get no gradient; dtype of tables untouched by the result
+    wr = Workload(dims=dict(B=1, n_heads=1, T=3, head_dim=4), dtype="bfloat16")
+    _, gr = oracle(decls.ROPE, make_case_inputs(decls.ROPE, wr, "cpu"))
+    assert list(gr) == ["dx"] and gr["dx"].dtype == torch.bfloat16
+
+
+def test_oracle_missing_input_raises():
+    with pytest.raises(ValueError):
+        oracle(decls.SOFTMAX, {"dy": torch.zeros(2, 2)})
+
+
+# ------------------------------------------------------------------- inputs
+def test_inputs_are_deterministic_and_follow_recipes():
+    w = Workload(dims=dict(rows=8, cols=16), dtype="float32")
+    a = make_case_inputs(decls.SOFTMAX, w, "cpu")
+    b = make_case_inputs(decls.SOFTMAX, w, "cpu")
+    assert torch.equal(a["x"], b["x"]) and torch.equal(a["dy"], b["dy"])
+    torch.manual_seed(8 * 100003 + 16)
+    assert torch.equal(a["x"], torch.randn(8, 16))
+    r = make_case_inputs(decls.RMSNORM, Workload(dims=dict(rows=4, hidden=4096),
+                                                 dtype="float32"), "cpu")
+    assert abs(float(r["weight"].mean()) - 1.0) < 0.01 and r["eps"] == 1e-5
+    wb = decls.RMSNORM.benchmark[0]
+    assert wb.extra["eps"] == 1e-6
+    rr = make_case_inputs(decls.ROPE, Workload(dims=dict(B=1, n_heads=2, T=3, head_dim=4),
+                                               dtype="bfloat16",
+                                               extra={"theta": 10000.0,
+                                                      "table_dtype": "float32"}), "cpu")
+    assert rr["cos"].dtype == torch.float32 and rr["x"].dtype == torch.bfloat16
+    assert case_seed(Workload(dims=dict(B=1, H=1, S=1, D=1), dtype="x")) == (
+        ((((1 * 131 + 1) * 131 + 1) * 131 + 1) * 131) + ord("x"))
