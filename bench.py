@@ -122,6 +122,9 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
                   for a, spec in zip(args, op.args)]
 
         def autograd_fn():
+            for lf in leaves:
+                if torch.is_tensor(lf):
+                    lf.grad = None
             y = bound(*leaves)
             y.backward(dy)
 
@@ -139,9 +142,6 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     full_ms = time_regions(lambda: bwd_call(fwd()[1]), reps=steps, warmup=warmup, flush=flush)
     ag = None
     if autograd_fn is not None:
-        for lf in leaves:
-            if torch.is_tensor(lf):
-                lf.grad = None
         ag = summarize(time_regions(autograd_fn, reps=steps, warmup=warmup, flush=flush))
     work = algorithmic_work(name, w, k_heads)
     sf, sb, sfull = summarize(fwd_ms), summarize(bwd_ms), summarize(full_ms)
