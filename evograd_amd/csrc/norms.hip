@@ -15,9 +15,9 @@
 // Each thread owns a fixed set of columns for the whole walk, so it keeps its
 // weight values and its dweight (and dbias) accumulators in registers; the next
 // row's loads are issued before the current row is reduced. At the end every
-// workgroup writes one fp32 partial row to the workspace [G, hidden], and a second
-// kernel sums the G partials per column in a fixed order. No atomics: the result
-// is bit-identical from run to run.
+// workgroup writes one fp32 partial row to the workspace [G, hidden], and two
+// small kernels sum the G partials per column in a fixed order. No atomics: the
+// result is bit-identical from run to run.
 #include "eg_common.hpp"
 
 #include <initializer_list>
@@ -273,29 +273,83 @@ __global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
 }
 
 // ------------------------------------------------- stage 2: column sums
-// out[c] = sum_{g=0..G-1} partial[g, c], combined in a fixed order: 4 row
-// groups per column (g = grp, grp+4, ...) summed in order, then the 4 group sums
-// added in group order. blockIdx.y selects one of up to two (partial, out) pairs.
-template <typename T>
-__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ p0,
-                                                     T* __restrict__ o0,
-                                                     const float* __restrict__ p1,
-                                                     T* __restrict__ o1, int G, int hidden) {
-  __shared__ float lds[4][64];
-  const float* p = blockIdx.y == 0 ? p0 : p1;
-  T* o = blockIdx.y == 0 ? o0 : o1;
-  const int cx = threadIdx.x & 63;
-  const int grp = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + cx;
-  float s = 0.f;
-  if (c < hidden)
-    for (int g = grp; g < G; g += 4) s += p[(int64_t)g * hidden + c];
-  lds[grp][cx] = s;
-  __syncthreads();
-  if (grp == 0 && c < hidden) {
-    const float t = ((lds[0][cx] + lds[1][cx]) + lds[2][cx]) + lds[3][cx];
-    o[c] = from_f32<T>(t);
+// out[p][c] = sum_{g=0..G-1} partial[p][g][c] in a fixed two-level order:
+// level 1 sums runs of kRun consecutive partial rows (g ascending) into
+// level1[p][G1][c], level 2 sums the G1 run totals in ascending order and casts.
+// One wave per (256-column tile, run): every lane keeps kRun independent 16-byte
+// loads in flight, so the 8 MB of partials at 16384 x 4096 stream at full rate.
+constexpr int kRun = 16;
+
+inline int64_t level1_rows(int64_t G) { return (G + kRun - 1) / kRun; }
+
+template <int RUN>
+__device__ __forceinline__ void sum_rows4(const float* __restrict__ p, int64_t stride, int rows,
+                                          int c, int hidden, float (&acc)[4]) {
+  acc[0] = acc[1] = acc[2] = acc[3] = 0.f;
+  if (c + 3 < hidden && (hidden & 3) == 0) {
+    float4 v[RUN];
+#pragma unroll
+    for (int g = 0; g < RUN; ++g)
+      if (g < rows) v[g] = *reinterpret_cast<const float4*>(p + g * stride + c);
+#pragma unroll
+    for (int g = 0; g < RUN; ++g)
+      if (g < rows) { acc[0] += v[g].x; acc[1] += v[g].y; acc[2] += v[g].z; acc[3] += v[g].w; }
+  } else {
+    for (int g = 0; g < rows; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (c + i < hidden) acc[i] += p[g * stride + c + i];
   }
+}
+
+__global__ __launch_bounds__(64) void colsum_stage1(const float* __restrict__ partial,
+                                                    float* __restrict__ level1, int G, int G1,
+                                                    int hidden) {
+  const int c = (blockIdx.x * 64 + threadIdx.x) * 4;
+  if (c >= hidden) return;
+  const int g0 = blockIdx.y * kRun;
+  const int rows = min(kRun, G - g0);
+  const float* p = partial + ((int64_t)blockIdx.z * G + g0) * hidden;
+  float acc[4];
+  sum_rows4<kRun>(p, hidden, rows, c, hidden, acc);
+  float* o = level1 + ((int64_t)blockIdx.z * G1 + blockIdx.y) * hidden;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (c + i < hidden) o[c + i] = acc[i];
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void colsum_stage2(const float* __restrict__ level1, T* __restrict__ o0,
+                                                    T* __restrict__ o1, int G1, int hidden) {
+  const int c = (blockIdx.x * 64 + threadIdx.x) * 4;
+  if (c >= hidden) return;
+  const float* p = level1 + (int64_t)blockIdx.y * G1 * hidden;
+  T* o = blockIdx.y == 0 ? o0 : o1;
+  float tot[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int g0 = 0; g0 < G1; g0 += kRun) {
+    float acc[4];
+    sum_rows4<kRun>(p + (int64_t)g0 * hidden, hidden, min(kRun, G1 - g0), c, hidden, acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (c + i < hidden) o[c + i] = from_f32<T>(tot[i]);
+}
+
+// Sums `nparams` stacked [G, hidden] partial arrays starting at `partial`, using
+// the level-1 buffer `level1` ([nparams, G1, hidden]).
+template <typename T>
+int launch_colsum(const float* partial, float* level1, T* o0, T* o1, int nparams, int G,
+                  int hidden, hipStream_t st, const char* what) {
+  const int G1 = (int)level1_rows(G);
+  const unsigned gx = (unsigned)((hidden + 255) / 256);
+  hipLaunchKernelGGL(colsum_stage1, dim3(gx, (unsigned)G1, (unsigned)nparams), dim3(64), 0, st,
+                     partial, level1, G, G1, hidden);
+  if (int rc = check_launch(what)) return rc;
+  hipLaunchKernelGGL((colsum_stage2<T>), dim3(gx, (unsigned)nparams), dim3(64), 0, st, level1, o0,
+                     o1, G1, hidden);
+  return check_launch(what);
 }
 
 // ------------------------------------------------------------- dispatch
@@ -384,13 +438,20 @@ bool vec_ok(int hidden, std::initializer_list<const void*> ptrs) {
 
 using namespace eg;
 
-extern "C" size_t eg_rmsnorm_workspace_bytes(int64_t rows, int64_t hidden) {
+// Workspace: nparams x [G, hidden] partials followed by nparams x [G1, hidden]
+// level-1 run totals, fp32.
+static size_t norm_workspace_bytes(int64_t rows, int64_t hidden, int nparams) {
   if (rows <= 0 || hidden <= 0) return 0;
-  return (size_t)partial_blocks(rows) * (size_t)hidden * sizeof(float);
+  const int64_t G = partial_blocks(rows);
+  return (size_t)nparams * (size_t)(G + level1_rows(G)) * (size_t)hidden * sizeof(float);
+}
+
+extern "C" size_t eg_rmsnorm_workspace_bytes(int64_t rows, int64_t hidden) {
+  return norm_workspace_bytes(rows, hidden, 1);
 }
 
 extern "C" size_t eg_layernorm_workspace_bytes(int64_t rows, int64_t hidden) {
-  return 2 * eg_rmsnorm_workspace_bytes(rows, hidden);
+  return norm_workspace_bytes(rows, hidden, 2);
 }
 
 extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd,
@@ -450,9 +511,8 @@ extern "C" int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight,
     if (!ok) { set_error("eg_rmsnorm_bwd: hidden=%d too wide", h); return 1; }
     if (int rc = check_launch("eg_rmsnorm_bwd")) return rc;
     const int G = (int)partial_blocks(rows);
-    hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((h + 63) / 64), 1), dim3(256), 0, st,
-                       part, (T*)dweight, part, (T*)dweight, G, h);
-    return check_launch("eg_rmsnorm_bwd(colsum)");
+    return launch_colsum<T>(part, part + (int64_t)G * h, (T*)dweight, (T*)dweight, 1, G, h, st,
+                            "eg_rmsnorm_bwd(colsum)");
   });
 }
 
@@ -518,8 +578,7 @@ extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weigh
     if (!ok) { set_error("eg_layernorm_bwd: hidden=%d too wide", h); return 1; }
     if (int rc = check_launch("eg_layernorm_bwd")) return rc;
     const int G = (int)partial_blocks(rows);
-    hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((h + 63) / 64), 2), dim3(256), 0, st,
-                       pw, (T*)dweight, pb, (T*)dbias, G, h);
-    return check_launch("eg_layernorm_bwd(colsum)");
+    return launch_colsum<T>(pw, pw + 2 * (int64_t)G * h, (T*)dweight, (T*)dbias, 2, G, h, st,
+                            "eg_layernorm_bwd(colsum)");
   });
 }
