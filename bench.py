@@ -251,6 +251,72 @@ def cpu_model() -> str:
     return "unknown"
 
 
+# ---------------------------------------------------------- profiling mode
+COPY_BYTES = 256 << 20
+
+
+def profile_run(name: str, steps: int) -> dict:
+    """Workload for rocprofv3: ``steps`` x (cache flush, forward, backward) of one
+    operator at its BASELINE configuration, then ``steps`` plain copies of
+    COPY_BYTES (a torch elementwise kernel reading and writing COPY_BYTES each),
+    whose FETCH_SIZE/WRITE_SIZE readings calibrate the counters for the op's
+    kernels."""
+    import torch
+
+    from evograd_amd import decls, pair_module
+    from evograd_amd.bind import backward_inactive_kwargs, lookup_pair
+    from evograd_amd.harness import CacheFlusher
+    from evograd_amd.inputs import make_case_inputs
+
+    op = decls.get_op(name)
+    mod = pair_module(name)
+    w = op.benchmark[0]
+    inputs = make_case_inputs(op, w, "cuda")
+    f, b = lookup_pair(op, mod)
+    args = [inputs.get(a.name, getattr(a, "default", None)) for a in op.args]
+    kw = backward_inactive_kwargs(op, b, inputs)
+    dy = inputs[op.upstream_grad_name]
+    flush = CacheFlusher("cuda")
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    times = {"fwd": [], "bwd": [], "copy": []}
+    for _ in range(steps):
+        flush()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        _, saved = f(*args)
+        e[1].record()
+        b(dy, saved, **kw)
+        e[2].record()
+        torch.cuda.synchronize()
+        times["fwd"].append(e[0].elapsed_time(e[1]) * 1e3)
+        times["bwd"].append(e[1].elapsed_time(e[2]) * 1e3)
+    for _ in range(steps):
+        flush()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e[0].record()
+        torch.mul(src, 1.0, out=dst)
+        e[1].record()
+        torch.cuda.synchronize()
+        times["copy"].append(e[0].elapsed_time(e[1]) * 1e3)
+    return {"profile": name, "config": {"dims": w.dims, "dtype": w.dtype},
+            "copy_bytes_each_way": COPY_BYTES,
+            **{f"{k}_us_median": statistics.median(v) for k, v in times.items()}}
+
+
+def load_traffic(kernel_key: str):
+    """HBM bytes per launch of a kernel, measured by rocprofv3 FETCH_SIZE and
+    WRITE_SIZE runs and recorded under profiles/ (None when not measured)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as fh:
+            entry = json.load(fh).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+    return entry
+
+
 # --------------------------------------------------------------------- main
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -259,6 +325,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ops", default=",".join(ALL_OPS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--profile", metavar="OP",
+                    help="rocprofv3 workload: STEPS x (flush, fwd, bwd) of OP plus copy calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every operator's work shards with no or one "
@@ -276,6 +344,9 @@ def main() -> int:
 
     _lib.load()
     torch.cuda.set_device(0)
+    if args.profile:
+        print(json.dumps(profile_run(args.profile, args.steps)), flush=True)
+        return 0
     flush = CacheFlusher("cuda")
     ops = [o for o in args.ops.split(",") if o]
     if HEADLINE not in ops:
@@ -347,6 +418,10 @@ def main() -> int:
         "cpu_model": cpu_model(),
         "ops": results,
     }
+    traffic = load_traffic("rmsnorm_bwd")
+    if traffic is not None:
+        line["roofline"]["traffic"] = traffic.get("hbm_bytes_per_launch")
+        line["roofline"]["traffic_source"] = "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
     if line["cpu_baseline"] is not None:
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 1)
     print(json.dumps(line), flush=True)

@@ -14,17 +14,21 @@
 // operand A, row l%32 and k = 8*(l/32) .. +7 (16 contiguous bytes when k runs
 // along memory); for B (K x N), column l%32 and the same k; the 32 x 32 fp32
 // result C gives lane l column l%32 and, in register r, row (r/4)*8 + (l/32)*4 + r%4.
-// Every product is arranged so its result feeds the next one without a shuffle:
-// a result C (M x N) is used as the B operand of X * C, with the k index of that
-// next product permuted to match C's register order (keys 8j + 4*(l/32) + i).
-// The matching A operand is read from an LDS copy stored transposed with the same
-// permutation of each 16-wide group ([0-3, 8-11, 4-7, 12-15]), so every operand
-// fetch is one 16-byte LDS read.
+// Every product is arranged so that its result feeds the next one without a
+// shuffle: a result C (M x N) is the B operand of X * C, with the k index of that
+// product permuted to C's register order (rows 8j + 4*(l/32) + i). The matching A
+// operand is read from an LDS copy stored transposed with that permutation applied
+// to each 16-wide group ([0-3, 8-11, 4-7, 12-15]), so each operand fetch is one
+// 16-byte LDS read. Transposed tiles are 64 wide; their eight 16-byte groups are
+// XOR-swizzled by (row / 8) % 8 so that both the transposing 8-byte writes and
+// the 16-byte operand reads spread over the LDS banks.
 //
 // Kernels (all deterministic, no atomics):
 //   attn_fwd:    one workgroup = 128 query rows of one (b, h) (4 waves x 32 rows);
 //                loops over 64-key tiles up to the diagonal; online softmax in the
-//                log2 domain; S^T = K Q^T then O^T += V^T P^T.
+//                log2 domain with the running max refreshed only when it grows by
+//                more than 2^8 (exact: the reference point cancels in o = sum/l);
+//                S^T = K Q^T then O^T += V^T P^T.
 //   attn_delta:  delta = rowsum(do * o).
 //   attn_dkdv:   one workgroup = 128 keys (4 waves x 32 keys); loops over 64-row
 //                query tiles from the diagonal down; S = Q K^T, dP = dO V^T,
@@ -46,31 +50,23 @@ template <> struct MM<bf16_t> {
   static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t bits(float f) { return f32_to_bf16_bits(f); }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack2_bf16(lo, hi); }
 };
 template <> struct MM<f16_t> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
   static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t bits(float f) {
-    _Float16 h = (_Float16)f;
-    uint16_t u;
-    __builtin_memcpy(&u, &h, 2);
-    return u;
-  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack2_f16(lo, hi); }
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleThreshold = 8.0f;  // log2 units: refresh the max past 2^8 growth
 
 template <typename V>
 __device__ __forceinline__ V ld16(const uint16_t* p) {
   return *reinterpret_cast<const V*>(p);
-}
-
-__device__ __forceinline__ uint4 ld_global16(const uint16_t* p) {
-  return *reinterpret_cast<const uint4*>(p);
 }
 
 // Eight fp32 values (registers off..off+7 of a result tile) rounded and packed
@@ -78,20 +74,33 @@ __device__ __forceinline__ uint4 ld_global16(const uint16_t* p) {
 template <typename T>
 __device__ __forceinline__ typename MM<T>::v8 pack8(const f32x16& c, int off) {
   uint4 u;
-  u.x = MM<T>::bits(c[off + 0]) | (MM<T>::bits(c[off + 1]) << 16);
-  u.y = MM<T>::bits(c[off + 2]) | (MM<T>::bits(c[off + 3]) << 16);
-  u.z = MM<T>::bits(c[off + 4]) | (MM<T>::bits(c[off + 5]) << 16);
-  u.w = MM<T>::bits(c[off + 6]) | (MM<T>::bits(c[off + 7]) << 16);
+  u.x = MM<T>::pack2(c[off + 0], c[off + 1]);
+  u.y = MM<T>::pack2(c[off + 2], c[off + 3]);
+  u.z = MM<T>::pack2(c[off + 4], c[off + 5]);
+  u.w = MM<T>::pack2(c[off + 6], c[off + 7]);
   typename MM<T>::v8 r;
   __builtin_memcpy(&r, &u, 16);
   return r;
 }
 
-// Position of key (or row) `i` inside a transposed LDS tile: within each group of
-// 16 the 4-element chunks are stored in the order 0, 2, 1, 3.
-__device__ __forceinline__ int tpos(int i) {
+// Four fp32 values scaled by `f`, packed as 8 bytes.
+template <typename T>
+__device__ __forceinline__ uint2 pack4(const f32x16& c, int off, float f) {
+  uint2 u;
+  u.x = MM<T>::pack2(c[off + 0] * f, c[off + 1] * f);
+  u.y = MM<T>::pack2(c[off + 2] * f, c[off + 3] * f);
+  return u;
+}
+
+// Transposed 64-wide tile: element offset of (row, position `pos` of the
+// permuted 64 columns). The 4-element chunks of each 16-group are stored in the
+// order 0, 2, 1, 3, and the 16-byte groups are XOR-swizzled by row.
+__device__ __forceinline__ int tperm(int i) {
   const int c = (i >> 2) & 3;
   return (i & ~15) | ((((c & 1) << 1) | (c >> 1)) << 2) | (i & 3);
+}
+__device__ __forceinline__ int toff(int row, int stride, int pos) {
+  return row * stride + ((((pos >> 3) ^ (row >> 3)) & 7) << 3) + (pos & 7);
 }
 
 // Element e (0..7) of a 16-byte pack of 16-bit values.
@@ -100,50 +109,57 @@ __device__ __forceinline__ uint32_t half_of(const uint4& u, int e) {
   return (e & 1) ? (word >> 16) : (word & 0xffffu);
 }
 
-// A tile of ROWS x D elements, loaded as 4-row x 8-column blocks (one per thread
-// while combos last): regs[i] = row 4*rb + i, columns 8*cb .. 8*cb+7.
-template <int ROWS, int D>
-struct Tile4x8 {
-  static constexpr int CB = D / 8;             // column blocks
-  static constexpr int COMBOS = (ROWS / 4) * CB;
+// A 64 x D tile copied from HBM as 4-row x 8-column blocks, one block per
+// thread (D = 64 has 128 blocks: threads t and t + 128 carry the same block and
+// write the same values). Rows at or past `nrows` read as zero; the loads are
+// unconditional (clamped address + select) so no branch hides their wait.
+template <int D>
+struct Tile64 {
+  static constexpr int CB = D / 8;
+  static constexpr int COMBOS = 16 * CB;
   uint4 r[4];
-  bool active;
-  int rb, cb;
+
+  __device__ __forceinline__ int combo() const { return (int)threadIdx.x & (COMBOS - 1); }
 
   __device__ __forceinline__ void load(const uint16_t* __restrict__ src, int row0, int nrows) {
-    const int t = threadIdx.x;
-    active = t < COMBOS;
-    rb = t / CB;
-    cb = t - rb * CB;
-    if (!active) return;
+    const int t = combo();
+    const int rb = t / CB, cb = t - (t / CB) * CB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = row0 + 4 * rb + i;
-      r[i] = row < nrows ? ld_global16(src + (int64_t)row * D + 8 * cb) : make_uint4(0, 0, 0, 0);
+      const int rc = row < nrows ? row : nrows - 1;
+      const uint4 v = *reinterpret_cast<const uint4*>(src + (int64_t)rc * D + 8 * cb);
+      r[i] = row < nrows ? v : make_uint4(0, 0, 0, 0);
     }
   }
 
-  // Row-major copy: lds[row * stride + col].
   __device__ __forceinline__ void store_rows(uint16_t* lds, int stride) const {
-    if (!active) return;
+    const int t = combo();
+    const int rb = t / CB, cb = t - (t / CB) * CB;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       *reinterpret_cast<uint4*>(lds + (4 * rb + i) * stride + 8 * cb) = r[i];
   }
 
-  // Transposed copy: lds[col * stride + tpos(row)], 4 rows per 8-byte write.
+  // Transposed: column c of the source becomes LDS row c; source row i goes to
+  // permuted position tperm(i).
   __device__ __forceinline__ void store_cols(uint16_t* lds, int stride) const {
-    if (!active) return;
-    const int pos = tpos(4 * rb);
+    const int t = combo();
+    const int rb = t / CB, cb = t - (t / CB) * CB;
+    const int pos = tperm(4 * rb);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       uint2 u;
       u.x = half_of(r[0], e) | (half_of(r[1], e) << 16);
       u.y = half_of(r[2], e) | (half_of(r[3], e) << 16);
-      *reinterpret_cast<uint2*>(lds + (8 * cb + e) * stride + pos) = u;
+      *reinterpret_cast<uint2*>(lds + toff(8 * cb + e, stride, pos)) = u;
     }
   }
 };
+
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
 
 // ------------------------------------------------------------------ forward
 template <typename T, int D>
@@ -163,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
   const int bh = blockIdx.y;
   const int qb = nqb - 1 - (int)blockIdx.x;  // longest rows first
   const int q0 = qb * BM;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
   const uint16_t* qp = q + base;
@@ -171,11 +187,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
   const uint16_t* vp = v + base;
 
   const int qrow = q0 + 32 * w + l32;
+  const int qrc = qrow < S ? qrow : S - 1;
   v8 qf[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    if (qrow < S) qf[kk] = ld16<v8>(qp + (int64_t)qrow * D + kk * 16 + 8 * hh);
-    else qf[kk] = v8{};
+    const v8 t = ld16<v8>(qp + (int64_t)qrc * D + kk * 16 + 8 * hh);
+    qf[kk] = qrow < S ? t : v8{};
   }
 
   f32x16 acc[DT];
@@ -185,9 +202,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
 
   const int kv_end = min(S, q0 + BM);
   const int ntiles = (kv_end + BN - 1) / BN;
-  const int wave_last_row = q0 + 32 * w + 31;
+  const int wave_first_row = q0 + 32 * w;
 
-  Tile4x8<BN, D> kt, vt;
+  Tile64<D> kt, vt;
   kt.load(kp, 0, S);
   vt.load(vp, 0, S);
   for (int j = 0; j < ntiles; ++j) {
@@ -200,34 +217,50 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
       kt.load(kp, k0 + BN, S);
       vt.load(vp, k0 + BN, S);
     }
-    if (k0 > wave_last_row) continue;  // every key of the tile is above this wave's rows
+    if (k0 > wave_first_row + 31) continue;  // every key of the tile is above this wave's rows
 
     f32x16 s[2];
 #pragma unroll
-    for (int T2 = 0; T2 < 2; ++T2) {
-      s[T2] = f32x16{};
+    for (int T2 = 0; T2 < 2; ++T2) s[T2] = f32x16{};
 #pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk)
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+      for (int T2 = 0; T2 < 2; ++T2)
         s[T2] = MM<T>::mma(ld16<v8>(Ks + (32 * T2 + l32) * KST + kk * 16 + 8 * hh), qf[kk], s[T2]);
-    }
-    const bool diag = k0 + BN - 1 > q0 + 32 * w;
+
     float mt = -INFINITY;
+    if (k0 + BN - 1 > wave_first_row) {  // tile crosses the diagonal for this wave
 #pragma unroll
-    for (int T2 = 0; T2 < 2; ++T2)
+      for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[T2][r] * scale_log2;
-        if (diag) {
+        for (int r = 0; r < 16; ++r) {
           const int key = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
-          if (key > qrow) x = -INFINITY;
+          const float x = key > qrow ? -INFINITY : s[T2][r] * scale_log2;
+          s[T2][r] = x;
+          mt = fmaxf(mt, x);
         }
-        s[T2][r] = x;
-        mt = fmaxf(mt, x);
-      }
+    } else {
+#pragma unroll
+      for (int T2 = 0; T2 < 2; ++T2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float x = s[T2][r] * scale_log2;
+          s[T2][r] = x;
+          mt = fmaxf(mt, x);
+        }
+    }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m, mt);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    // Refresh the reference max only when some row's max grew past the
+    // threshold (always on the first tile, where m is -inf).
+    if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleThreshold) != 0) {
+      const float m_new = fmaxf(m, mt);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+      m = m_new;
+    }
+    const float m_use = m == -INFINITY ? 0.f : m;
     float ps = 0.f;
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
@@ -237,16 +270,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
         s[T2][r] = p;
         ps += p;
       }
-    lsum = lsum * alpha + ps;
-    m = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    lsum += ps;
 #pragma unroll
     for (int ms = 0; ms < BN / 16; ++ms) {
       const v8 pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
 #pragma unroll
       for (int t = 0; t < DT; ++t)
-        acc[t] = MM<T>::mma(ld16<v8>(Vt + (32 * t + l32) * VST + ms * 16 + 8 * hh), pb, acc[t]);
+        acc[t] = MM<T>::mma(ld16<v8>(Vt + toff(32 * t + l32, VST, ms * 16 + 8 * hh)), pb, acc[t]);
     }
   }
 
@@ -257,12 +287,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 u;
-        u.x = MM<T>::bits(acc[t][4 * g + 0] * inv) | (MM<T>::bits(acc[t][4 * g + 1] * inv) << 16);
-        u.y = MM<T>::bits(acc[t][4 * g + 2] * inv) | (MM<T>::bits(acc[t][4 * g + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(op + 32 * t + 8 * g + 4 * hh) = u;
-      }
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<uint2*>(op + 32 * t + 8 * g + 4 * hh) = pack4<T>(acc[t], 4 * g, inv);
     if (hh == 0) lse[(int64_t)bh * S + qrow] = (m + log2f(ltot)) * kLn2;
   }
 }
@@ -314,23 +340,21 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
   const int bh = blockIdx.y;
   const int kb = nkb - 1 - (int)blockIdx.x;
   const int k0 = kb * BK;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
   const float* lsep = lse + (int64_t)bh * S;
   const float* delp = delta + (int64_t)bh * S;
 
   const int key = k0 + 32 * w + l32;
+  const int krc = key < S ? key : S - 1;
   v8 kf[KSTEPS], vf[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    if (key < S) {
-      kf[kk] = ld16<v8>(k + base + (int64_t)key * D + kk * 16 + 8 * hh);
-      vf[kk] = ld16<v8>(v + base + (int64_t)key * D + kk * 16 + 8 * hh);
-    } else {
-      kf[kk] = v8{};
-      vf[kk] = v8{};
-    }
+    const v8 a = ld16<v8>(k + base + (int64_t)krc * D + kk * 16 + 8 * hh);
+    const v8 b = ld16<v8>(v + base + (int64_t)krc * D + kk * 16 + 8 * hh);
+    kf[kk] = key < S ? a : v8{};
+    vf[kk] = key < S ? b : v8{};
   }
   f32x16 dka[DT], dva[DT];
 #pragma unroll
@@ -340,16 +364,16 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
   const int i_end = (S + BQ - 1) / BQ;
   const int wave_first_key = k0 + 32 * w;
 
-  Tile4x8<BQ, D> qt, dt;
+  Tile64<D> qt, dt;
   float lreg = 0.f, ereg = 0.f;
   auto load_q = [&](int i) {
     qt.load(q + base, i * BQ, S);
     dt.load(dout + base, i * BQ, S);
-    const int row = i * BQ + (int)threadIdx.x;
-    if (threadIdx.x < BQ) {
-      lreg = row < S ? lsep[row] * kLog2e : INFINITY;
-      ereg = row < S ? delp[row] : 0.f;
-    }
+    const int row = i * BQ + ((int)threadIdx.x & (BQ - 1));
+    const int rc = row < S ? row : S - 1;
+    const float lv = lsep[rc], ev = delp[rc];
+    lreg = row < S ? lv * kLog2e : INFINITY;
+    ereg = row < S ? ev : 0.f;
   };
   if (i_first < i_end) load_q(i_first);
   for (int i = i_first; i < i_end; ++i) {
@@ -366,15 +390,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
 
     f32x16 s[2], dp[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      s[mt] = f32x16{};
-      dp[mt] = f32x16{};
+    for (int mt = 0; mt < 2; ++mt) { s[mt] = f32x16{}; dp[mt] = f32x16{}; }
 #pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
         s[mt] = MM<T>::mma(ld16<v8>(Qs + (32 * mt + l32) * RST + kk * 16 + 8 * hh), kf[kk], s[mt]);
         dp[mt] = MM<T>::mma(ld16<v8>(Ds + (32 * mt + l32) * RST + kk * 16 + 8 * hh), vf[kk], dp[mt]);
       }
-    }
     const bool diag = qi0 < wave_first_key + 31;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -400,8 +423,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
       const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
-        dva[t] = MM<T>::mma(ld16<v8>(Dt + (32 * t + l32) * TST + ms * 16 + 8 * hh), pb, dva[t]);
-        dka[t] = MM<T>::mma(ld16<v8>(Qt + (32 * t + l32) * TST + ms * 16 + 8 * hh), sb, dka[t]);
+        const int off = toff(32 * t + l32, TST, ms * 16 + 8 * hh);
+        dva[t] = MM<T>::mma(ld16<v8>(Dt + off), pb, dva[t]);
+        dka[t] = MM<T>::mma(ld16<v8>(Qt + off), sb, dka[t]);
       }
     }
   }
@@ -413,13 +437,8 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
     for (int t = 0; t < DT; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        uint2 a, b;
-        a.x = MM<T>::bits(dka[t][4 * g + 0] * scale) | (MM<T>::bits(dka[t][4 * g + 1] * scale) << 16);
-        a.y = MM<T>::bits(dka[t][4 * g + 2] * scale) | (MM<T>::bits(dka[t][4 * g + 3] * scale) << 16);
-        b.x = MM<T>::bits(dva[t][4 * g + 0]) | (MM<T>::bits(dva[t][4 * g + 1]) << 16);
-        b.y = MM<T>::bits(dva[t][4 * g + 2]) | (MM<T>::bits(dva[t][4 * g + 3]) << 16);
-        *reinterpret_cast<uint2*>(dkp + 32 * t + 8 * g + 4 * hh) = a;
-        *reinterpret_cast<uint2*>(dvp + 32 * t + 8 * g + 4 * hh) = b;
+        *reinterpret_cast<uint2*>(dkp + 32 * t + 8 * g + 4 * hh) = pack4<T>(dka[t], 4 * g, scale);
+        *reinterpret_cast<uint2*>(dvp + 32 * t + 8 * g + 4 * hh) = pack4<T>(dva[t], 4 * g, 1.0f);
       }
   }
 }
@@ -444,24 +463,23 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
   const int bh = blockIdx.y;
   const int qb = nqb - 1 - (int)blockIdx.x;
   const int q0 = qb * BM;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
 
   const int qrow = q0 + 32 * w + l32;
+  const int qrc = qrow < S ? qrow : S - 1;
   v8 qf[KSTEPS], df[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    if (qrow < S) {
-      qf[kk] = ld16<v8>(q + base + (int64_t)qrow * D + kk * 16 + 8 * hh);
-      df[kk] = ld16<v8>(dout + base + (int64_t)qrow * D + kk * 16 + 8 * hh);
-    } else {
-      qf[kk] = v8{};
-      df[kk] = v8{};
-    }
+    const v8 a = ld16<v8>(q + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
+    const v8 b = ld16<v8>(dout + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
+    qf[kk] = qrow < S ? a : v8{};
+    df[kk] = qrow < S ? b : v8{};
   }
-  const float l2 = qrow < S ? lse[(int64_t)bh * S + qrow] * kLog2e : INFINITY;
-  const float dl = qrow < S ? delta[(int64_t)bh * S + qrow] : 0.f;
+  const float lv = lse[(int64_t)bh * S + qrc], ev = delta[(int64_t)bh * S + qrc];
+  const float l2 = qrow < S ? lv * kLog2e : INFINITY;
+  const float dl = qrow < S ? ev : 0.f;
 
   f32x16 acc[DT];
 #pragma unroll
@@ -469,9 +487,9 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
 
   const int kv_end = min(S, q0 + BM);
   const int ntiles = (kv_end + BN - 1) / BN;
-  const int wave_last_row = q0 + 32 * w + 31;
+  const int wave_first_row = q0 + 32 * w;
 
-  Tile4x8<BN, D> kt, vt;
+  Tile64<D> kt, vt;
   kt.load(k + base, 0, S);
   vt.load(v + base, 0, S);
   for (int j = 0; j < ntiles; ++j) {
@@ -485,20 +503,19 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
       kt.load(k + base, k0 + BN, S);
       vt.load(v + base, k0 + BN, S);
     }
-    if (k0 > wave_last_row) continue;
+    if (k0 > wave_first_row + 31) continue;
 
     f32x16 s[2], dp[2];
 #pragma unroll
-    for (int T2 = 0; T2 < 2; ++T2) {
-      s[T2] = f32x16{};
-      dp[T2] = f32x16{};
+    for (int T2 = 0; T2 < 2; ++T2) { s[T2] = f32x16{}; dp[T2] = f32x16{}; }
 #pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+      for (int T2 = 0; T2 < 2; ++T2) {
         s[T2] = MM<T>::mma(ld16<v8>(Ks + (32 * T2 + l32) * RST + kk * 16 + 8 * hh), qf[kk], s[T2]);
         dp[T2] = MM<T>::mma(ld16<v8>(Vs + (32 * T2 + l32) * RST + kk * 16 + 8 * hh), df[kk], dp[T2]);
       }
-    }
-    const bool diag = k0 + BN - 1 > q0 + 32 * w;
+    const bool diag = k0 + BN - 1 > wave_first_row;
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
@@ -515,7 +532,7 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
       const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
 #pragma unroll
       for (int t = 0; t < DT; ++t)
-        acc[t] = MM<T>::mma(ld16<v8>(Kt + (32 * t + l32) * TST + ms * 16 + 8 * hh), sb, acc[t]);
+        acc[t] = MM<T>::mma(ld16<v8>(Kt + toff(32 * t + l32, TST, ms * 16 + 8 * hh)), sb, acc[t]);
     }
   }
 
@@ -524,12 +541,8 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 u;
-        u.x = MM<T>::bits(acc[t][4 * g + 0] * scale) | (MM<T>::bits(acc[t][4 * g + 1] * scale) << 16);
-        u.y = MM<T>::bits(acc[t][4 * g + 2] * scale) | (MM<T>::bits(acc[t][4 * g + 3] * scale) << 16);
-        *reinterpret_cast<uint2*>(op + 32 * t + 8 * g + 4 * hh) = u;
-      }
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<uint2*>(op + 32 * t + 8 * g + 4 * hh) = pack4<T>(acc[t], 4 * g, scale);
   }
 }
 

@@ -37,12 +37,31 @@ __device__ __forceinline__ float to_f32(bf16_t v) {
   return __uint_as_float(((uint32_t)v.bits) << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950); NaN
+// stays a quiet NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const __bf16 b = (__bf16)f;
+  uint16_t u;
+  __builtin_memcpy(&u, &b, 2);
+  return u;
+}
+
+// Two fp32 values -> packed pair of 16-bit values (one v_cvt_pk_* instruction),
+// round to nearest even; `lo` lands in bits 0..15.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t r = __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t);
+  uint32_t u;
+  __builtin_memcpy(&u, &r, 4);
+  return u;
+}
+__device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  const f16x2_t r = __builtin_convertvector((f32x2_t){lo, hi}, f16x2_t);
+  uint32_t u;
+  __builtin_memcpy(&u, &r, 4);
+  return u;
 }
 
 template <typename T> __device__ __forceinline__ T from_f32(float v);

@@ -1,0 +1,130 @@
+"""Summaries of rocprofv3 CSV output (``--output-format csv``) as short markdown.
+
+    python -m evograd_amd.profiling stats    <prefix>_kernel_stats.csv [FILTER]
+    python -m evograd_amd.profiling counters <prefix>_counter_collection.csv [FILTER]
+    python -m evograd_amd.profiling traffic  FETCH.csv WRITE.csv KERNEL_SUBSTRING [KEY]
+
+``traffic`` turns the FETCH_SIZE and WRITE_SIZE readings (KiB per dispatch,
+summed over the L2 channels) of one kernel into HBM bytes per launch, scaled by
+what the same counters read for the calibration copy that ``bench.py --profile``
+runs (a torch elementwise multiply reading and writing 256 MiB each), and prints
+the JSON entry recorded in profiles/traffic.json.
+"""
+
+from __future__ import annotations
+
+import collections
+import csv
+import json
+import re
+import statistics
+import sys
+
+COPY_KERNEL = "MulFunctor<float>"
+COPY_BYTES = 256 << 20
+
+
+def short_name(name: str) -> str:
+    """Kernel name without namespaces, argument lists and most template noise."""
+    n = re.sub(r"^void\s+", "", name)
+    n = n.replace("(anonymous namespace)::", "")
+    depth, out = 0, []
+    for ch in n:  # drop the argument list: everything from the first '(' at depth 0
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            break
+        out.append(ch)
+    n = "".join(out)
+    n = n.replace("at::native::", "at::")
+    n = n.replace("eg::bf16_t", "bf16").replace("eg::f16_t", "f16")
+    return n[:110]
+
+
+def stats(path: str, filt: str = "") -> str:
+    rows = list(csv.DictReader(open(path)))
+    lines = ["| kernel | calls | avg us | min us | max us | share % |", "|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        if filt and filt not in r["Name"]:
+            continue
+        lines.append(
+            f"| `{short_name(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+            f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} |"
+        )
+    return "\n".join(lines)
+
+
+def _counter_table(path: str):
+    """kernel name -> counter -> list of per-dispatch values."""
+    per = collections.defaultdict(lambda: collections.defaultdict(dict))
+    for r in csv.DictReader(open(path)):
+        per[r["Kernel_Name"]][r["Counter_Name"]][r["Dispatch_Id"]] = (
+            per[r["Kernel_Name"]][r["Counter_Name"]].get(r["Dispatch_Id"], 0.0)
+            + float(r["Counter_Value"])
+        )
+    return {k: {c: list(d.values()) for c, d in cs.items()} for k, cs in per.items()}
+
+
+def counters(path: str, filt: str = "") -> str:
+    table = _counter_table(path)
+    lines = ["| kernel | counter | dispatches | mean per dispatch |", "|---|---|---:|---:|"]
+    for k, cs in table.items():
+        if filt and filt not in k:
+            continue
+        for c, vals in sorted(cs.items()):
+            lines.append(f"| `{short_name(k)}` | {c} | {len(vals)} | {statistics.mean(vals):.6g} |")
+    return "\n".join(lines)
+
+
+def traffic(fetch_csv: str, write_csv: str, kernel: str, key: str = "") -> dict:
+    f, w = _counter_table(fetch_csv), _counter_table(write_csv)
+
+    def pick(table, sub, counter):
+        vals = [v for k, cs in table.items() if sub in k for v in cs.get(counter, [])]
+        if not vals:
+            raise SystemExit(f"no {counter} readings for kernels matching {sub!r}")
+        return statistics.median(vals)
+
+    copy_fetch_kib = pick(f, COPY_KERNEL, "FETCH_SIZE")
+    copy_write_kib = pick(w, COPY_KERNEL, "WRITE_SIZE")
+    fetch_scale = COPY_BYTES / (copy_fetch_kib * 1024.0)
+    write_scale = COPY_BYTES / (copy_write_kib * 1024.0)
+    kf = pick(f, kernel, "FETCH_SIZE") * 1024.0 * fetch_scale
+    kw = pick(w, kernel, "WRITE_SIZE") * 1024.0 * write_scale
+    return {
+        "kernel": kernel,
+        "key": key or kernel,
+        "fetch_bytes_per_launch": round(kf),
+        "write_bytes_per_launch": round(kw),
+        "hbm_bytes_per_launch": round(kf + kw),
+        "copy_calibration": {
+            "bytes_each_way": COPY_BYTES,
+            "fetch_kib_read": copy_fetch_kib,
+            "write_kib_read": copy_write_kib,
+            "fetch_scale": fetch_scale,
+            "write_scale": write_scale,
+        },
+    }
+
+
+def main(argv: list) -> int:
+    if len(argv) < 2:
+        print(__doc__)
+        return 2
+    cmd = argv[0]
+    if cmd == "stats":
+        print(stats(argv[1], argv[2] if len(argv) > 2 else ""))
+    elif cmd == "counters":
+        print(counters(argv[1], argv[2] if len(argv) > 2 else ""))
+    elif cmd == "traffic":
+        print(json.dumps(traffic(argv[1], argv[2], argv[3], argv[4] if len(argv) > 4 else ""), indent=1))
+    else:
+        print(__doc__)
+        return 2
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))
