@@ -124,6 +124,18 @@ __device__ __forceinline__ void store_f32_nt(T* __restrict__ p, const float (&in
   __builtin_nontemporal_store(raw, reinterpret_cast<u32x4*>(p));
 }
 
+// Streaming when NT and the pack is 16 bytes, plain otherwise.
+template <typename T, int VEC, bool NT>
+__device__ __forceinline__ void load_vec(const T* __restrict__ p, float (&out)[VEC]) {
+  if constexpr (NT && sizeof(T) * VEC == 16) load_f32_nt<T, VEC>(p, out);
+  else load_f32<T, VEC>(p, out);
+}
+template <typename T, int VEC, bool NT>
+__device__ __forceinline__ void store_vec(T* __restrict__ p, const float (&in)[VEC]) {
+  if constexpr (NT && sizeof(T) * VEC == 16) store_f32_nt<T, VEC>(p, in);
+  else store_f32<T, VEC>(p, in);
+}
+
 // ------------------------------------------------------------- reductions
 struct SumOp {
   __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }

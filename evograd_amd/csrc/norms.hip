@@ -15,9 +15,9 @@
 // Each thread owns a fixed set of columns for the whole walk, so it keeps its
 // weight values and its dweight (and dbias) accumulators in registers; the next
 // row's loads are issued before the current row is reduced. At the end every
-// workgroup writes one fp32 partial row to the workspace [G, hidden], and two
-// small kernels sum the G partials per column in a fixed order. No atomics: the
-// result is bit-identical from run to run.
+// workgroup writes one fp32 partial row to the workspace [G, hidden], and a small
+// kernel sums the G partials per column in a fixed order. No atomics: the result
+// is bit-identical from run to run.
 #include "eg_common.hpp"
 
 #include <initializer_list>
@@ -31,13 +31,13 @@ inline int64_t partial_blocks(int64_t rows) {
   return rows < kPartialBlocks ? (rows > 0 ? rows : 1) : kPartialBlocks;
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT = false>
 __device__ __forceinline__ void load_cols(const T* __restrict__ p, int n, float (&v)[ITEMS][VEC]) {
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
     if (c < n) {
-      load_f32<T, VEC>(p + c, v[it]);
+      load_vec<T, VEC, NT>(p + c, v[it]);
     } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) v[it][i] = 0.f;
@@ -45,17 +45,17 @@ __device__ __forceinline__ void load_cols(const T* __restrict__ p, int n, float 
   }
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT = false>
 __device__ __forceinline__ void store_cols(T* __restrict__ p, int n, const float (&v)[ITEMS][VEC]) {
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-    if (c < n) store_f32<T, VEC>(p + c, v[it]);
+    if (c < n) store_vec<T, VEC, NT>(p + c, v[it]);
   }
 }
 
 // ------------------------------------------------------------------ RMSNorm
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_kernel(const T* __restrict__ x,
                                                             const T* __restrict__ w,
                                                             T* __restrict__ y,
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_kernel(const T* __restrict_
   const int64_t row = blockIdx.x;
   const int64_t off = row * hidden;
   float xv[ITEMS][VEC], wv[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK>(x + off, hidden, xv);
+  load_cols<T, VEC, ITEMS, BLOCK, NT>(x + off, hidden, xv);
   load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
   float ss = 0.f;
 #pragma unroll
@@ -78,11 +78,11 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_kernel(const T* __restrict_
   for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) xv[it][i] = (xv[it][i] * rstd) * wv[it][i];
-  store_cols<T, VEC, ITEMS, BLOCK>(y + off, hidden, xv);
+  store_cols<T, VEC, ITEMS, BLOCK, NT>(y + off, hidden, xv);
   if (threadIdx.x == 0) rstd_out[row] = rstd;
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ partial,
@@ -101,8 +101,8 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
   float xv[ITEMS][VEC], gv[ITEMS][VEC];
   float r = 0.f;
   if (row < rows) {
-    load_cols<T, VEC, ITEMS, BLOCK>(x + row * hidden, hidden, xv);
-    load_cols<T, VEC, ITEMS, BLOCK>(dy + row * hidden, hidden, gv);
+    load_cols<T, VEC, ITEMS, BLOCK, NT>(x + row * hidden, hidden, xv);
+    load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + row * hidden, hidden, gv);
     r = rstd[row];
   }
   while (row < rows) {
@@ -111,8 +111,8 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
     float nx[ITEMS][VEC], ng[ITEMS][VEC];
     float nr = 0.f;
     if (nrow < rows) {
-      load_cols<T, VEC, ITEMS, BLOCK>(x + nrow * hidden, hidden, nx);
-      load_cols<T, VEC, ITEMS, BLOCK>(dy + nrow * hidden, hidden, ng);
+      load_cols<T, VEC, ITEMS, BLOCK, NT>(x + nrow * hidden, hidden, nx);
+      load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + nrow * hidden, hidden, ng);
       nr = rstd[nrow];
     }
     float dot = 0.f;
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
     for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) gv[it][i] = (gv[it][i] - xv[it][i] * dot) * r;
-    store_cols<T, VEC, ITEMS, BLOCK>(dx + row * hidden, hidden, gv);
+    store_cols<T, VEC, ITEMS, BLOCK, NT>(dx + row * hidden, hidden, gv);
     row = nrow;
     if (row < rows) {
 #pragma unroll
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
 }
 
 // ---------------------------------------------------------------- LayerNorm
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void layernorm_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b,
     T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(BLOCK) void layernorm_fwd_kernel(
   const int64_t row = blockIdx.x;
   const int64_t off = row * hidden;
   float xv[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK>(x + off, hidden, xv);
+  load_cols<T, VEC, ITEMS, BLOCK, NT>(x + off, hidden, xv);
   float s = 0.f;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it)
@@ -187,11 +187,11 @@ __global__ __launch_bounds__(BLOCK) void layernorm_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < VEC; ++i)
       xv[it][i] = ((xv[it][i] - mean) * rstd) * wv[it][i] + bv[it][i];
-  store_cols<T, VEC, ITEMS, BLOCK>(y + off, hidden, xv);
+  store_cols<T, VEC, ITEMS, BLOCK, NT>(y + off, hidden, xv);
   if (threadIdx.x == 0) { mean_out[row] = mean; rstd_out[row] = rstd; }
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
@@ -210,8 +210,8 @@ __global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
   float xv[ITEMS][VEC], gv[ITEMS][VEC];
   float mu = 0.f, r = 0.f;
   if (row < rows) {
-    load_cols<T, VEC, ITEMS, BLOCK>(x + row * hidden, hidden, xv);
-    load_cols<T, VEC, ITEMS, BLOCK>(dy + row * hidden, hidden, gv);
+    load_cols<T, VEC, ITEMS, BLOCK, NT>(x + row * hidden, hidden, xv);
+    load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + row * hidden, hidden, gv);
     mu = mean[row];
     r = rstd[row];
   }
@@ -220,8 +220,8 @@ __global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
     float nx[ITEMS][VEC], ng[ITEMS][VEC];
     float nmu = 0.f, nr = 0.f;
     if (nrow < rows) {
-      load_cols<T, VEC, ITEMS, BLOCK>(x + nrow * hidden, hidden, nx);
-      load_cols<T, VEC, ITEMS, BLOCK>(dy + nrow * hidden, hidden, ng);
+      load_cols<T, VEC, ITEMS, BLOCK, NT>(x + nrow * hidden, hidden, nx);
+      load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + nrow * hidden, hidden, ng);
       nmu = mean[nrow];
       nr = rstd[nrow];
     }
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
     for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) gv[it][i] = r * ((gv[it][i] - sg) - xv[it][i] * sgx);
-    store_cols<T, VEC, ITEMS, BLOCK>(dx + row * hidden, hidden, gv);
+    store_cols<T, VEC, ITEMS, BLOCK, NT>(dx + row * hidden, hidden, gv);
     row = nrow;
     if (row < rows) {
 #pragma unroll
@@ -273,82 +273,68 @@ __global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
 }
 
 // ------------------------------------------------- stage 2: column sums
-// out[p][c] = sum_{g=0..G-1} partial[p][g][c] in a fixed two-level order:
-// level 1 sums runs of kRun consecutive partial rows (g ascending) into
-// level1[p][G1][c], level 2 sums the G1 run totals in ascending order and casts.
-// One wave per (256-column tile, run): every lane keeps kRun independent 16-byte
-// loads in flight, so the 8 MB of partials at 16384 x 4096 stream at full rate.
-constexpr int kRun = 16;
+// out[p][c] = sum_{g=0..G-1} partial[p][g][c] in a fixed order. A workgroup owns
+// 64 columns (16 lanes x 4 columns); its 16 row groups each sum the partial rows
+// g = rg, rg + 16, ... in ascending order with all loads of a batch issued
+// together, and the 16 group totals are then added in group order through LDS.
+// blockIdx.y selects the parameter (dweight, dbias).
+constexpr int kColGroups = 16;
+constexpr int kColBatch = 16;
 
-inline int64_t level1_rows(int64_t G) { return (G + kRun - 1) / kRun; }
-
-template <int RUN>
-__device__ __forceinline__ void sum_rows4(const float* __restrict__ p, int64_t stride, int rows,
-                                          int c, int hidden, float (&acc)[4]) {
-  acc[0] = acc[1] = acc[2] = acc[3] = 0.f;
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ partial,
+                                                     T* __restrict__ o0, T* __restrict__ o1,
+                                                     int G, int hidden) {
+  __shared__ float4 lds[kColGroups][16];
+  const int q = threadIdx.x & 15;   // column quad within the tile
+  const int rg = threadIdx.x >> 4;  // row group
+  const int c = blockIdx.x * 64 + 4 * q;
+  const float* p = partial + (int64_t)blockIdx.y * G * hidden;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (c + 3 < hidden && (hidden & 3) == 0) {
-    float4 v[RUN];
+    for (int g0 = rg; g0 < G; g0 += kColGroups * kColBatch) {
+      float4 v[kColBatch];
 #pragma unroll
-    for (int g = 0; g < RUN; ++g)
-      if (g < rows) v[g] = *reinterpret_cast<const float4*>(p + g * stride + c);
+      for (int i = 0; i < kColBatch; ++i) {
+        const int g = g0 + i * kColGroups;
+        v[i] = g < G ? *reinterpret_cast<const float4*>(p + (int64_t)g * hidden + c)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
 #pragma unroll
-    for (int g = 0; g < RUN; ++g)
-      if (g < rows) { acc[0] += v[g].x; acc[1] += v[g].y; acc[2] += v[g].z; acc[3] += v[g].w; }
+      for (int i = 0; i < kColBatch; ++i) {
+        acc.x += v[i].x; acc.y += v[i].y; acc.z += v[i].z; acc.w += v[i].w;
+      }
+    }
   } else {
-    for (int g = 0; g < rows; ++g)
+    float a4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int g = rg; g < G; g += kColGroups)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (c + i < hidden) acc[i] += p[g * stride + c + i];
+        if (c + i < hidden) a4[i] += p[(int64_t)g * hidden + c + i];
+    acc = make_float4(a4[0], a4[1], a4[2], a4[3]);
+  }
+  lds[rg][q] = acc;
+  __syncthreads();
+  if (rg == 0) {
+    float4 t = lds[0][q];
+#pragma unroll
+    for (int r = 1; r < kColGroups; ++r) {
+      const float4 u = lds[r][q];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    T* o = blockIdx.y == 0 ? o0 : o1;
+    const float tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (c + i < hidden) o[c + i] = from_f32<T>(tv[i]);
   }
 }
 
-__global__ __launch_bounds__(64) void colsum_stage1(const float* __restrict__ partial,
-                                                    float* __restrict__ level1, int G, int G1,
-                                                    int hidden) {
-  const int c = (blockIdx.x * 64 + threadIdx.x) * 4;
-  if (c >= hidden) return;
-  const int g0 = blockIdx.y * kRun;
-  const int rows = min(kRun, G - g0);
-  const float* p = partial + ((int64_t)blockIdx.z * G + g0) * hidden;
-  float acc[4];
-  sum_rows4<kRun>(p, hidden, rows, c, hidden, acc);
-  float* o = level1 + ((int64_t)blockIdx.z * G1 + blockIdx.y) * hidden;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (c + i < hidden) o[c + i] = acc[i];
-}
-
 template <typename T>
-__global__ __launch_bounds__(64) void colsum_stage2(const float* __restrict__ level1, T* __restrict__ o0,
-                                                    T* __restrict__ o1, int G1, int hidden) {
-  const int c = (blockIdx.x * 64 + threadIdx.x) * 4;
-  if (c >= hidden) return;
-  const float* p = level1 + (int64_t)blockIdx.y * G1 * hidden;
-  T* o = blockIdx.y == 0 ? o0 : o1;
-  float tot[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int g0 = 0; g0 < G1; g0 += kRun) {
-    float acc[4];
-    sum_rows4<kRun>(p + (int64_t)g0 * hidden, hidden, min(kRun, G1 - g0), c, hidden, acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tot[i] += acc[i];
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (c + i < hidden) o[c + i] = from_f32<T>(tot[i]);
-}
-
-// Sums `nparams` stacked [G, hidden] partial arrays starting at `partial`, using
-// the level-1 buffer `level1` ([nparams, G1, hidden]).
-template <typename T>
-int launch_colsum(const float* partial, float* level1, T* o0, T* o1, int nparams, int G,
-                  int hidden, hipStream_t st, const char* what) {
-  const int G1 = (int)level1_rows(G);
-  const unsigned gx = (unsigned)((hidden + 255) / 256);
-  hipLaunchKernelGGL(colsum_stage1, dim3(gx, (unsigned)G1, (unsigned)nparams), dim3(64), 0, st,
-                     partial, level1, G, G1, hidden);
-  if (int rc = check_launch(what)) return rc;
-  hipLaunchKernelGGL((colsum_stage2<T>), dim3(gx, (unsigned)nparams), dim3(64), 0, st, level1, o0,
-                     o1, G1, hidden);
+int launch_colsum(const float* partial, T* o0, T* o1, int nparams, int G, int hidden,
+                  hipStream_t st, const char* what) {
+  hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((hidden + 63) / 64), (unsigned)nparams),
+                     dim3(256), 0, st, partial, o0, o1, G, hidden);
   return check_launch(what);
 }
 
@@ -370,7 +356,7 @@ template <typename T, int VEC>
 struct RmsFwd {
   const T *x, *w; T* y; float* rstd; int64_t rows; int hidden; float eps; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
                        dim3(BLOCK), 0, st, x, w, y, rstd, hidden, eps);
     return true;
   }
@@ -381,7 +367,7 @@ struct RmsBwd {
   const T *dy, *x, *w; const float* rstd; T* dx; float* part; int64_t rows; int hidden;
   hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, VEC, ITEMS, BLOCK>),
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>),
                        dim3((unsigned)partial_blocks(rows)), dim3(BLOCK), 0, st, dy, x, w, rstd,
                        dx, part, rows, hidden);
     return true;
@@ -393,7 +379,7 @@ struct LnFwd {
   const T *x, *w, *b; T* y; float *mean, *rstd; int64_t rows; int hidden; float eps;
   hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((layernorm_fwd_kernel<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+    hipLaunchKernelGGL((layernorm_fwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
                        dim3(BLOCK), 0, st, x, w, b, y, mean, rstd, hidden, eps);
     return true;
   }
@@ -404,7 +390,7 @@ struct LnBwd {
   const T *dy, *x, *w; const float *mean, *rstd; T* dx; float *pw, *pb; int64_t rows;
   int hidden; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((layernorm_bwd_kernel<T, VEC, ITEMS, BLOCK>),
+    hipLaunchKernelGGL((layernorm_bwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>),
                        dim3((unsigned)partial_blocks(rows)), dim3(BLOCK), 0, st, dy, x, w, mean,
                        rstd, dx, pw, pb, rows, hidden);
     return true;
@@ -438,12 +424,11 @@ bool vec_ok(int hidden, std::initializer_list<const void*> ptrs) {
 
 using namespace eg;
 
-// Workspace: nparams x [G, hidden] partials followed by nparams x [G1, hidden]
-// level-1 run totals, fp32.
+// Workspace: nparams x [G, hidden] fp32 partials.
 static size_t norm_workspace_bytes(int64_t rows, int64_t hidden, int nparams) {
   if (rows <= 0 || hidden <= 0) return 0;
   const int64_t G = partial_blocks(rows);
-  return (size_t)nparams * (size_t)(G + level1_rows(G)) * (size_t)hidden * sizeof(float);
+  return (size_t)nparams * (size_t)G * (size_t)hidden * sizeof(float);
 }
 
 extern "C" size_t eg_rmsnorm_workspace_bytes(int64_t rows, int64_t hidden) {
@@ -511,8 +496,7 @@ extern "C" int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight,
     if (!ok) { set_error("eg_rmsnorm_bwd: hidden=%d too wide", h); return 1; }
     if (int rc = check_launch("eg_rmsnorm_bwd")) return rc;
     const int G = (int)partial_blocks(rows);
-    return launch_colsum<T>(part, part + (int64_t)G * h, (T*)dweight, (T*)dweight, 1, G, h, st,
-                            "eg_rmsnorm_bwd(colsum)");
+    return launch_colsum<T>(part, (T*)dweight, (T*)dweight, 1, G, h, st, "eg_rmsnorm_bwd(colsum)");
   });
 }
 
@@ -578,7 +562,6 @@ extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weigh
     if (!ok) { set_error("eg_layernorm_bwd: hidden=%d too wide", h); return 1; }
     if (int rc = check_launch("eg_layernorm_bwd")) return rc;
     const int G = (int)partial_blocks(rows);
-    return launch_colsum<T>(pw, pw + 2 * (int64_t)G * h, (T*)dweight, (T*)dbias, 2, G, h, st,
-                            "eg_layernorm_bwd(colsum)");
+    return launch_colsum<T>(pw, (T*)dweight, (T*)dbias, 2, G, h, st, "eg_layernorm_bwd(colsum)");
   });
 }

@@ -18,16 +18,16 @@
 namespace eg {
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kRopeBlock = 256;
 
-template <typename T, typename TT, int VEC>
-__global__ __launch_bounds__(kBlock) void rope_kernel(
+template <typename T, typename TT, int VEC, bool NT>
+__global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo, T* __restrict__ ko,
     const TT* __restrict__ cosv, const TT* __restrict__ sinv, int heads_q, int heads_k,
     int tokens, int head_dim, int hpg, int groups_q, int groups_k, float sgn) {
   const int half = head_dim >> 1;
   const int cpr = half / VEC;  // chunks per row
-  const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t idx = (int64_t)blockIdx.x * kRopeBlock + threadIdx.x;
   const int t = (int)(idx / cpr);
   if (t >= tokens) return;
   const int ch = (int)(idx - (int64_t)t * cpr);
@@ -58,16 +58,16 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(
   for (int h = h0; h < h1; ++h) {
     const int64_t off = off0 + (int64_t)(h - h0) * row_stride;
     float x1[VEC], x2[VEC];
-    load_f32<T, VEC>(src + off, x1);
-    load_f32<T, VEC>(src + off + half, x2);
+    load_vec<T, VEC, NT>(src + off, x1);
+    load_vec<T, VEC, NT>(src + off + half, x2);
     float y1[VEC], y2[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       y1[i] = x1[i] * c1[i] + x2[i] * s1[i];
       y2[i] = x2[i] * c2[i] + x1[i] * s2[i];
     }
-    store_f32<T, VEC>(dst + off, y1);
-    store_f32<T, VEC>(dst + off + half, y2);
+    store_vec<T, VEC, NT>(dst + off, y1);
+    store_vec<T, VEC, NT>(dst + off + half, y2);
   }
 }
 
@@ -75,23 +75,25 @@ inline bool aligned_to(const void* p, size_t n) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) % n) == 0;
 }
 
+// Heads per group: enough groups to fill the chip, few enough to amortise the
+// table loads over several rows.
+constexpr int kHeadsPerGroup = 4;
+
 template <typename T, typename TT, int VEC>
 int launch_rope(const void* q, const void* k, void* qo, void* ko, const void* cosv,
                 const void* sinv, int64_t batch, int64_t hq, int64_t hk, int64_t tokens,
                 int64_t head_dim, float sgn, hipStream_t st) {
-  // Heads per group: enough groups to fill the chip, few enough to amortise the
-  // table loads over several rows.
-  const int hpg = 4;
+  const int hpg = kHeadsPerGroup;
   const int gq = (int)((hq + hpg - 1) / hpg);
   const int gk = (int)((hk + hpg - 1) / hpg);
   const int64_t gy = batch * (gq + gk);
   const int64_t threads = tokens * (head_dim / 2 / VEC);
-  const int64_t gx = (threads + kBlock - 1) / kBlock;
+  const int64_t gx = (threads + kRopeBlock - 1) / kRopeBlock;
   if (gy > 65535 || gx > 0x7fffffffLL) {
     set_error("eg_rope: grid too large (batch*groups=%lld)", (long long)gy);
     return 1;
   }
-  hipLaunchKernelGGL((rope_kernel<T, TT, VEC>), dim3((unsigned)gx, (unsigned)gy), dim3(kBlock),
+  hipLaunchKernelGGL((rope_kernel<T, TT, VEC, VEC * sizeof(T) == 16>), dim3((unsigned)gx, (unsigned)gy), dim3(kRopeBlock),
                      0, st, (const T*)q, (const T*)k, (T*)qo, (T*)ko, (const TT*)cosv,
                      (const TT*)sinv, (int)hq, (int)hk, (int)tokens, (int)head_dim, hpg, gq, gk,
                      sgn);

@@ -14,14 +14,14 @@
 namespace eg {
 namespace {
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __device__ __forceinline__ void load_row(const T* __restrict__ row, int cols, float fill,
                                          float (&v)[ITEMS][VEC]) {
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
     if (c < cols) {
-      load_f32<T, VEC>(row + c, v[it]);
+      load_vec<T, VEC, NT>(row + c, v[it]);
     } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) v[it][i] = fill;
@@ -29,23 +29,23 @@ __device__ __forceinline__ void load_row(const T* __restrict__ row, int cols, fl
   }
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __device__ __forceinline__ void store_row(T* __restrict__ row, int cols,
                                           const float (&v)[ITEMS][VEC]) {
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-    if (c < cols) store_f32<T, VEC>(row + c, v[it]);
+    if (c < cols) store_vec<T, VEC, NT>(row + c, v[it]);
   }
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void softmax_fwd_reg(const T* __restrict__ x,
                                                          T* __restrict__ y, int cols) {
   __shared__ float lds[BLOCK / kWave];
   const int64_t off = (int64_t)blockIdx.x * cols;
   float v[ITEMS][VEC];
-  load_row<T, VEC, ITEMS, BLOCK>(x + off, cols, -INFINITY, v);
+  load_row<T, VEC, ITEMS, BLOCK, NT>(x + off, cols, -INFINITY, v);
   float m = -INFINITY;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it)
@@ -66,18 +66,18 @@ __global__ __launch_bounds__(BLOCK) void softmax_fwd_reg(const T* __restrict__ x
   for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) v[it][i] *= inv;
-  store_row<T, VEC, ITEMS, BLOCK>(y + off, cols, v);
+  store_row<T, VEC, ITEMS, BLOCK, NT>(y + off, cols, v);
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK>
+template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void softmax_bwd_reg(const T* __restrict__ y,
                                                          const T* __restrict__ dy,
                                                          T* __restrict__ dx, int cols) {
   __shared__ float lds[BLOCK / kWave];
   const int64_t off = (int64_t)blockIdx.x * cols;
   float yv[ITEMS][VEC], gv[ITEMS][VEC];
-  load_row<T, VEC, ITEMS, BLOCK>(y + off, cols, 0.f, yv);
-  load_row<T, VEC, ITEMS, BLOCK>(dy + off, cols, 0.f, gv);
+  load_row<T, VEC, ITEMS, BLOCK, NT>(y + off, cols, 0.f, yv);
+  load_row<T, VEC, ITEMS, BLOCK, NT>(dy + off, cols, 0.f, gv);
   float d = 0.f;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it)
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(BLOCK) void softmax_bwd_reg(const T* __restrict__ y
   for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) gv[it][i] = yv[it][i] * (gv[it][i] - d);
-  store_row<T, VEC, ITEMS, BLOCK>(dx + off, cols, gv);
+  store_row<T, VEC, ITEMS, BLOCK, NT>(dx + off, cols, gv);
 }
 
 // ---- wide rows: online (max, sum) in one read, then a second read to write.
@@ -170,7 +170,7 @@ template <typename T, int VEC>
 struct FwdLaunch {
   const T* x; T* y; int64_t rows; int cols; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((softmax_fwd_reg<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+    hipLaunchKernelGGL((softmax_fwd_reg<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
                        dim3(BLOCK), 0, st, x, y, cols);
     return true;
   }
@@ -180,7 +180,7 @@ template <typename T, int VEC>
 struct BwdLaunch {
   const T* y; const T* dy; T* dx; int64_t rows; int cols; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((softmax_bwd_reg<T, VEC, ITEMS, BLOCK>), dim3((unsigned)rows),
+    hipLaunchKernelGGL((softmax_bwd_reg<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
                        dim3(BLOCK), 0, st, y, dy, dx, cols);
     return true;
   }

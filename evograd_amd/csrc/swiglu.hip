@@ -9,35 +9,35 @@
 //   s = sigmoid(a); db = dc * (a * s); da = dc * b * (s + a * s * (1 - s))
 // evaluated in fp32 and rounded once.
 //
-// Each thread moves UNROLL 16-byte packs per tensor, all loads issued before any
-// math, so a wave keeps UNROLL * 16 B * 64 lanes per stream in flight.
+// The 16-byte path streams with non-temporal loads and stores (about 15% more
+// bandwidth than plain ones on MI355X) and keeps few packs per thread; ragged
+// sizes take a scalar path.
 #include "eg_common.hpp"
 
 namespace eg {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kSwigluBlock = 256;
 
 __device__ __forceinline__ float sigmoidf_(float a) { return 1.0f / (1.0f + expf(-a)); }
 
-template <typename T, int VEC>
-__global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(const T* __restrict__ a,
+template <typename T, int VEC, int kUnroll, bool NT>
+__global__ __launch_bounds__(kSwigluBlock) void swiglu_fwd_kernel(const T* __restrict__ a,
                                                             const T* __restrict__ b,
                                                             T* __restrict__ c, int64_t npack) {
-  const int64_t base = (int64_t)blockIdx.x * kUnroll * kBlock + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kUnroll * kSwigluBlock + threadIdx.x;
   float av[kUnroll][VEC], bv[kUnroll][VEC];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + (int64_t)u * kBlock;
+    const int64_t p = base + (int64_t)u * kSwigluBlock;
     if (p < npack) {
-      load_f32<T, VEC>(a + p * VEC, av[u]);
-      load_f32<T, VEC>(b + p * VEC, bv[u]);
+      load_vec<T, VEC, NT>(a + p * VEC, av[u]);
+      load_vec<T, VEC, NT>(b + p * VEC, bv[u]);
     }
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + (int64_t)u * kBlock;
+    const int64_t p = base + (int64_t)u * kSwigluBlock;
     if (p < npack) {
       float cv[VEC];
 #pragma unroll
@@ -46,31 +46,31 @@ __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(const T* __restrict_
         const float silu = round_to<T>(x / (1.0f + expf(-x)));
         cv[i] = silu * bv[u][i];
       }
-      store_f32<T, VEC>(c + p * VEC, cv);
+      store_vec<T, VEC, NT>(c + p * VEC, cv);
     }
   }
 }
 
-template <typename T, int VEC>
-__global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(const T* __restrict__ dc,
+template <typename T, int VEC, int kUnroll, bool NT>
+__global__ __launch_bounds__(kSwigluBlock) void swiglu_bwd_kernel(const T* __restrict__ dc,
                                                             const T* a, const T* b, T* da,
                                                             T* db, int64_t npack) {
   // a/da and b/db may alias (in-place backward): no __restrict__ on them. Every
   // element is loaded before the same thread stores to it.
-  const int64_t base = (int64_t)blockIdx.x * kUnroll * kBlock + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kUnroll * kSwigluBlock + threadIdx.x;
   float gv[kUnroll][VEC], av[kUnroll][VEC], bv[kUnroll][VEC];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + (int64_t)u * kBlock;
+    const int64_t p = base + (int64_t)u * kSwigluBlock;
     if (p < npack) {
-      load_f32<T, VEC>(dc + p * VEC, gv[u]);
-      load_f32<T, VEC>(a + p * VEC, av[u]);
-      load_f32<T, VEC>(b + p * VEC, bv[u]);
+      load_vec<T, VEC, NT>(dc + p * VEC, gv[u]);
+      load_vec<T, VEC, NT>(a + p * VEC, av[u]);
+      load_vec<T, VEC, NT>(b + p * VEC, bv[u]);
     }
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + (int64_t)u * kBlock;
+    const int64_t p = base + (int64_t)u * kSwigluBlock;
     if (p < npack) {
       float dav[VEC], dbv[VEC];
 #pragma unroll
@@ -82,14 +82,22 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(const T* __restrict_
         dbv[i] = g * xs;
         dav[i] = g * bv[u][i] * (s + xs * (1.0f - s));
       }
-      store_f32<T, VEC>(da + p * VEC, dav);
-      store_f32<T, VEC>(db + p * VEC, dbv);
+      store_vec<T, VEC, NT>(da + p * VEC, dav);
+      store_vec<T, VEC, NT>(db + p * VEC, dbv);
     }
   }
 }
 
-inline unsigned grid_for(int64_t npack) {
-  return (unsigned)((npack + (int64_t)kUnroll * kBlock - 1) / ((int64_t)kUnroll * kBlock));
+// Launch shapes of the 16-byte path (streaming hints), measured on MI355X at
+// [16384, 14336] bf16: the forward moves most bytes with one pack per tensor per
+// thread, the backward (three reads, two writes) with four. The scalar path
+// unrolls 4 to keep some loads in flight.
+constexpr int kUnrollFwd = 1;
+constexpr int kUnrollBwd = 4;
+constexpr int kUnrollScalar = 4;
+
+inline int64_t grid_for(int64_t npack, int unroll) {
+  return (npack + (int64_t)unroll * kSwigluBlock - 1) / ((int64_t)unroll * kSwigluBlock);
 }
 
 }  // namespace
@@ -101,6 +109,7 @@ extern "C" int eg_swiglu_fwd(const void* a, const void* b, void* c, int64_t n, i
                              void* stream) {
   clear_error();
   if (n < 0) { set_error("eg_swiglu_fwd: negative size"); return 1; }
+  if (n > ((int64_t)1 << 40)) { set_error("eg_swiglu_fwd: size out of range"); return 1; }
   if (n == 0) return 0;
   if (!a || !b || !c) { set_error("eg_swiglu_fwd: null pointer"); return 1; }
   hipStream_t st = as_stream(stream);
@@ -109,11 +118,12 @@ extern "C" int eg_swiglu_fwd(const void* a, const void* b, void* c, int64_t n, i
     constexpr int V = 16 / sizeof(T);
     if (n % V == 0 && aligned16(a) && aligned16(b) && aligned16(c)) {
       const int64_t np = n / V;
-      if (grid_for(np) == 0 || (int64_t)grid_for(np) > 0x7fffffffLL) { set_error("eg_swiglu_fwd: too large"); return 1; }
-      hipLaunchKernelGGL((swiglu_fwd_kernel<T, V>), dim3(grid_for(np)), dim3(kBlock), 0, st,
-                         (const T*)a, (const T*)b, (T*)c, np);
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, V, kUnrollFwd, true>),
+                         dim3((unsigned)grid_for(np, kUnrollFwd)), dim3(kSwigluBlock), 0, st, (const T*)a,
+                         (const T*)b, (T*)c, np);
     } else {
-      hipLaunchKernelGGL((swiglu_fwd_kernel<T, 1>), dim3(grid_for(n)), dim3(kBlock), 0, st,
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, 1, kUnrollScalar, false>),
+                         dim3((unsigned)grid_for(n, kUnrollScalar)), dim3(kSwigluBlock), 0, st,
                          (const T*)a, (const T*)b, (T*)c, n);
     }
     return check_launch("eg_swiglu_fwd");
@@ -124,6 +134,7 @@ extern "C" int eg_swiglu_bwd(const void* dc, const void* a, const void* b, void*
                              int64_t n, int dtype, void* stream) {
   clear_error();
   if (n < 0) { set_error("eg_swiglu_bwd: negative size"); return 1; }
+  if (n > ((int64_t)1 << 40)) { set_error("eg_swiglu_bwd: size out of range"); return 1; }
   if (n == 0) return 0;
   if (!dc || !a || !b || !da || !db) { set_error("eg_swiglu_bwd: null pointer"); return 1; }
   if (da == db) { set_error("eg_swiglu_bwd: da and db must not alias each other"); return 1; }
@@ -134,10 +145,12 @@ extern "C" int eg_swiglu_bwd(const void* dc, const void* a, const void* b, void*
     if (n % V == 0 && aligned16(dc) && aligned16(a) && aligned16(b) && aligned16(da) &&
         aligned16(db)) {
       const int64_t np = n / V;
-      hipLaunchKernelGGL((swiglu_bwd_kernel<T, V>), dim3(grid_for(np)), dim3(kBlock), 0, st,
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, V, kUnrollBwd, true>),
+                         dim3((unsigned)grid_for(np, kUnrollBwd)), dim3(kSwigluBlock), 0, st,
                          (const T*)dc, (const T*)a, (const T*)b, (T*)da, (T*)db, np);
     } else {
-      hipLaunchKernelGGL((swiglu_bwd_kernel<T, 1>), dim3(grid_for(n)), dim3(kBlock), 0, st,
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, 1, kUnrollScalar, false>),
+                         dim3((unsigned)grid_for(n, kUnrollScalar)), dim3(kSwigluBlock), 0, st,
                          (const T*)dc, (const T*)a, (const T*)b, (T*)da, (T*)db, n);
     }
     return check_launch("eg_swiglu_bwd");

@@ -40,8 +40,8 @@ def test_library_loads_and_exports_every_symbol():
     assert lib.eg_abi_version() == _lib.ABI_VERSION
     assert lib.eg_last_error() is not None
     # size queries are pure host arithmetic
-    assert lib.eg_rmsnorm_workspace_bytes(16384, 4096) == (512 + 32) * 4096 * 4
-    assert lib.eg_layernorm_workspace_bytes(3, 64) == 2 * (3 + 1) * 64 * 4
+    assert lib.eg_rmsnorm_workspace_bytes(16384, 4096) == 512 * 4096 * 4
+    assert lib.eg_layernorm_workspace_bytes(3, 64) == 2 * 3 * 64 * 4
     assert lib.eg_rmsnorm_workspace_bytes(0, 64) == 0
 
 
