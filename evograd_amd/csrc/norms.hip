@@ -8,8 +8,9 @@
 // Layout: x, y, dy, dx are [rows, hidden] row-major in HBM; weight/bias [hidden];
 // the saved statistics (rstd, and mean for LayerNorm) are fp32 [rows].
 //
-// Forward: one workgroup per row, the row held in registers (16-byte packs),
-// statistics reduced by wave butterflies and one LDS exchange.
+// Forward: one wave per row when the row is 1..8 packs per lane (RMSNorm), else
+// one workgroup per row; the row is held in registers (16-byte packs) and its
+// statistics reduced by wave butterflies (and one LDS exchange for workgroups).
 //
 // Backward: G = min(rows, kPartialBlocks) workgroups walk the rows with stride G.
 // Each thread owns a fixed set of columns for the whole walk, so it keeps its
@@ -148,6 +149,60 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
     if (c < hidden) store_f32<float, VEC>(pp + c, acc[it]);
   }
+}
+
+// --------------------------------------------- RMSNorm forward, one wave per row
+// For rows of ITEMS x 64 lanes x VEC elements (hidden 512..4096 in bf16) a wave
+// owns a whole row: the statistic is reduced with wave butterflies only, so no
+// workgroup barrier sits between a row's loads and its stores, and the waves of a
+// CU drift independently, keeping many rows of loads in flight. (The same shape
+// for the backward, with per-lane dweight sums, measured slower than the
+// workgroup kernel below and is not used.)
+template <typename T, int VEC>
+__device__ __forceinline__ Pack<T, VEC> ld_pack(const T* __restrict__ p) {
+  static_assert(sizeof(T) * VEC == 16, "16-byte packs");
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  Pack<T, VEC> pk;
+  __builtin_memcpy(&pk, &raw, 16);
+  return pk;
+}
+
+template <typename T, int VEC, int ITEMS>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
+                                                        const T* __restrict__ w,
+                                                        T* __restrict__ y,
+                                                        float* __restrict__ rstd_out, int64_t rows,
+                                                        float eps) {
+  constexpr int H = ITEMS * kWave * VEC;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * H;
+  Pack<T, VEC> xp[ITEMS];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) xp[it] = ld_pack<T, VEC>(xr + (it * kWave + lane) * VEC);
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float v = to_f32(xp[it].v[i]);
+      ss += v * v;
+    }
+  ss = wave_reduce(ss, SumOp());
+  const float r = rsqrtf(ss / (float)H + eps);
+  T* yr = y + row * H;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * kWave + lane) * VEC;
+    const Pack<T, VEC> wp = *reinterpret_cast<const Pack<T, VEC>*>(w + c);
+    float o[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) o[i] = (to_f32(xp[it].v[i]) * r) * to_f32(wp.v[i]);
+    store_f32_nt<T, VEC>(yr + c, o);
+  }
+  if (lane == 0) rstd_out[row] = r;
 }
 
 // ---------------------------------------------------------------- LayerNorm
@@ -452,7 +507,21 @@ extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float*
     constexpr int V = 16 / sizeof(T);
     const int h = (int)hidden;
     bool ok;
-    if (vec_ok<T>(h, {x, weight, y})) {
+    const int waves_items = h / (kWave * V);
+    if (vec_ok<T>(h, {x, weight, y}) && h % (kWave * V) == 0 &&
+        (waves_items == 1 || waves_items == 2 || waves_items == 4 || waves_items == 8)) {
+      const unsigned grid = (unsigned)((rows + 3) / 4);
+      const T* xp = (const T*)x;
+      const T* wp = (const T*)weight;
+      T* yp = (T*)y;
+      switch (waves_items) {
+        case 1: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        case 2: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        case 4: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        default: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 8>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+      }
+      ok = true;
+    } else if (vec_ok<T>(h, {x, weight, y})) {
       RmsFwd<T, V> f{(const T*)x, (const T*)weight, (T*)y, rstd, rows, h, eps, st};
       ok = pick_norm_config((h + V - 1) / V, f);
     } else {
