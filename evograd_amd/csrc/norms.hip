@@ -8,17 +8,25 @@
 // Layout: x, y, dy, dx are [rows, hidden] row-major in HBM; weight/bias [hidden];
 // the saved statistics (rstd, and mean for LayerNorm) are fp32 [rows].
 //
-// Forward: one wave per row when the row is 1..8 packs per lane (RMSNorm), else
-// one workgroup per row; the row is held in registers (16-byte packs) and its
-// statistics reduced by wave butterflies (and one LDS exchange for workgroups).
+// Ring kernels (every backward, the LayerNorm forward, and the RMSNorm forward
+// for widths the one-wave kernel does not take): a fixed grid of G workgroups
+// walks the rows with stride G. A thread owns the same columns on every row
+// (16-byte packs), so weight, bias and the dweight/dbias sums stay in its
+// registers. Each workgroup keeps DEPTH rows of loads in flight: a ring slot is
+// refilled with the row DEPTH*G further on as soon as its data is in registers,
+// before the current row's reduction. Row statistics are reduced with wave
+// butterflies and one barrier per sum, through two alternating LDS slots (a
+// slot is rewritten only after the next barrier, so no second barrier is needed).
 //
-// Backward: G = min(rows, kPartialBlocks) workgroups walk the rows with stride G.
-// Each thread owns a fixed set of columns for the whole walk, so it keeps its
-// weight values and its dweight (and dbias) accumulators in registers; the next
-// row's loads are issued before the current row is reduced. At the end every
-// workgroup writes one fp32 partial row to the workspace [G, hidden], and a small
-// kernel sums the G partials per column in a fixed order. No atomics: the result
-// is bit-identical from run to run.
+// The backward writes one fp32 partial row per workgroup ([G, hidden] per
+// parameter); the column-sum kernel adds the G partials of each column in a
+// fixed order. No atomics: results are bit-identical from run to run, and G is a
+// constant (not the device's CU count), so the summation order is the same on
+// every device.
+//
+// RMSNorm forward for hidden = 64 x VEC x {1, 2, 4, 8}: one wave per row, the
+// statistic reduced by wave butterflies only, so no barrier sits between a row's
+// loads and its stores.
 #include "eg_common.hpp"
 
 #include <initializer_list>
@@ -26,148 +34,192 @@
 namespace eg {
 namespace {
 
-constexpr int kPartialBlocks = 512;
+// Workgroups of the backward ring per 512 threads of workgroup width: one
+// 512-thread workgroup per CU of an MI355X (256 CUs) for RMSNorm, 1.5 for
+// LayerNorm (two partial rows per workgroup, measured best at that count).
+constexpr int64_t kRmsBwdBlocks = 256;
+constexpr int64_t kLnBwdBlocks = 384;
+constexpr int64_t kFwdBlocks = 512;
 
-inline int64_t partial_blocks(int64_t rows) {
-  return rows < kPartialBlocks ? (rows > 0 ? rows : 1) : kPartialBlocks;
+inline int64_t ring_blocks(int64_t rows, int64_t per512, int block) {
+  const int64_t g = per512 * (block < 512 ? 512 / block : 1);
+  return rows < g ? (rows > 0 ? rows : 1) : g;
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK, bool NT = false>
-__device__ __forceinline__ void load_cols(const T* __restrict__ p, int n, float (&v)[ITEMS][VEC]) {
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-    if (c < n) {
-      load_vec<T, VEC, NT>(p + c, v[it]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) v[it][i] = 0.f;
-    }
+// Workgroup width for a row of npack packs: (BLOCK, ITEMS) with BLOCK * ITEMS >= npack.
+template <typename F>
+bool pick_ring(int64_t npack, F&& f) {
+  if (npack <= 64) return f.template go<64, 1>();
+  if (npack <= 128) return f.template go<128, 1>();
+  if (npack <= 256) return f.template go<256, 1>();
+  if (npack <= 512) return f.template go<512, 1>();
+  if (npack <= 1024) return f.template go<512, 2>();
+  if (npack <= 2048) return f.template go<1024, 2>();
+  if (npack <= 4096) return f.template go<1024, 4>();
+  if (npack <= 8192) return f.template go<1024, 8>();
+  return false;
+}
+
+inline int ring_block_for(int64_t npack) {
+  if (npack <= 64) return 64;
+  if (npack <= 128) return 128;
+  if (npack <= 256) return 256;
+  if (npack <= 512) return 512;
+  if (npack <= 1024) return 512;
+  return 1024;
+}
+
+// Rows in flight per workgroup: deeper for narrow rows, one for very wide ones.
+template <int ITEMS> constexpr int ring_depth() { return ITEMS == 1 ? 4 : ITEMS == 2 ? 2 : 1; }
+
+// ------------------------------------------------------------- pack access
+template <typename T, int VEC>
+__device__ __forceinline__ Pack<T, VEC> ld_raw(const T* __restrict__ p) {
+  if constexpr (sizeof(T) * VEC == 16) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    Pack<T, VEC> pk;
+    __builtin_memcpy(&pk, &raw, 16);
+    return pk;
+  } else {
+    return *reinterpret_cast<const Pack<T, VEC>*>(p);
   }
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK, bool NT = false>
-__device__ __forceinline__ void store_cols(T* __restrict__ p, int n, const float (&v)[ITEMS][VEC]) {
+template <typename T, int VEC>
+__device__ __forceinline__ void unpack(const Pack<T, VEC>& pk, float (&f)[VEC]) {
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-    if (c < n) store_vec<T, VEC, NT>(p + c, v[it]);
-  }
+  for (int i = 0; i < VEC; ++i) f[i] = to_f32(pk.v[i]);
 }
 
-// ------------------------------------------------------------------ RMSNorm
-template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
-__global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_kernel(const T* __restrict__ x,
-                                                            const T* __restrict__ w,
-                                                            T* __restrict__ y,
-                                                            float* __restrict__ rstd_out,
-                                                            int hidden, float eps) {
-  __shared__ float lds[BLOCK / kWave];
-  const int64_t row = blockIdx.x;
-  const int64_t off = row * hidden;
-  float xv[ITEMS][VEC], wv[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK, NT>(x + off, hidden, xv);
-  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
-  float ss = 0.f;
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) ss += xv[it][i] * xv[it][i];
-  ss = block_reduce<BLOCK>(ss, SumOp(), lds);
-  const float rstd = rsqrtf(ss / (float)hidden + eps);
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) xv[it][i] = (xv[it][i] * rstd) * wv[it][i];
-  store_cols<T, VEC, ITEMS, BLOCK, NT>(y + off, hidden, xv);
-  if (threadIdx.x == 0) rstd_out[row] = rstd;
+template <typename T, int VEC>
+__device__ __forceinline__ void st_vec(T* __restrict__ p, const float (&f)[VEC]) {
+  store_vec<T, VEC, true>(p, f);
 }
 
-template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
-__global__ __launch_bounds__(BLOCK) void rmsnorm_bwd_kernel(
-    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
-    const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ partial,
-    int64_t rows, int hidden) {
-  __shared__ float lds[BLOCK / kWave];
-  const int64_t G = gridDim.x;
-  float wv[ITEMS][VEC], acc[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
+// Sums of N values over the workgroup with one barrier per call: per-wave
+// butterflies, then the wave totals added in wave order from one of two
+// alternating LDS slots. Every thread ends with the totals.
+template <int BLOCK, int N>
+struct SlotSum {
+  static constexpr int NW = BLOCK / kWave;
+  float (*slot)[N][NW];  // [2][N][NW] in LDS
+  int par;
+  __device__ __forceinline__ void operator()(float (&v)[N]) {
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it)
+    for (int i = 0; i < N; ++i) v[i] = wave_reduce(v[i], SumOp());
+    if constexpr (NW > 1) {
+      const int lane = threadIdx.x & (kWave - 1);
+      const int wid = threadIdx.x / kWave;
+      if (lane == 0)
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[it][i] = 0.f;
-  const float inv_h = 1.0f / (float)hidden;
-
-  int64_t row = blockIdx.x;
-  float xv[ITEMS][VEC], gv[ITEMS][VEC];
-  float r = 0.f;
-  if (row < rows) {
-    load_cols<T, VEC, ITEMS, BLOCK, NT>(x + row * hidden, hidden, xv);
-    load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + row * hidden, hidden, gv);
-    r = rstd[row];
-  }
-  while (row < rows) {
-    // Prefetch the next row of this workgroup while the current one reduces.
-    const int64_t nrow = row + G;
-    float nx[ITEMS][VEC], ng[ITEMS][VEC];
-    float nr = 0.f;
-    if (nrow < rows) {
-      load_cols<T, VEC, ITEMS, BLOCK, NT>(x + nrow * hidden, hidden, nx);
-      load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + nrow * hidden, hidden, ng);
-      nr = rstd[nrow];
-    }
-    float dot = 0.f;
+        for (int i = 0; i < N; ++i) slot[par][i][wid] = v[i];
+      __syncthreads();
 #pragma unroll
-    for (int it = 0; it < ITEMS; ++it)
+      for (int i = 0; i < N; ++i) {
+        float t = slot[par][i][0];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        const float xh = xv[it][i] * r;
-        acc[it][i] += gv[it][i] * xh;
-        const float g = gv[it][i] * wv[it][i];
-        xv[it][i] = xh;
-        gv[it][i] = g;
-        dot += g * xh;
+        for (int q = 1; q < NW; ++q) t += slot[par][i][q];
+        v[i] = t;
       }
-    dot = block_reduce<BLOCK>(dot, SumOp(), lds) * inv_h;
+      par ^= 1;
+    }
+  }
+};
+
+// --------------------------------------------------------------- forward
+template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN>
+__global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
+                                                       const T* __restrict__ w,
+                                                       const T* __restrict__ b,
+                                                       T* __restrict__ y,
+                                                       float* __restrict__ mean_out,
+                                                       float* __restrict__ rstd_out,
+                                                       int64_t rows, int hidden, float eps) {
+  __shared__ float slots[2][1][BLOCK / kWave];
+  SlotSum<BLOCK, 1> bsum{slots, 0};
+  const int64_t G = gridDim.x;
+  const float inv_h = 1.0f / (float)hidden;
+  int col[ITEMS];
+  bool live[ITEMS];
+  float wv[ITEMS][VEC], bv[ITEMS][VEC];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    col[it] = (it * BLOCK + (int)threadIdx.x) * VEC;
+    live[it] = col[it] < hidden;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { wv[it][i] = 0.f; bv[it][i] = 0.f; }
+    if (live[it]) {
+      unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(w + col[it]), wv[it]);
+      if (LN) unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(b + col[it]), bv[it]);
+    }
+  }
+  Pack<T, VEC> xb[DEPTH][ITEMS];
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k) {
+    const int64_t row = blockIdx.x + k * G;
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it)
+      if (row < rows && live[it]) xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
+  }
+  for (int64_t base = blockIdx.x; base < rows; base += DEPTH * G) {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) gv[it][i] = (gv[it][i] - xv[it][i] * dot) * r;
-    store_cols<T, VEC, ITEMS, BLOCK, NT>(dx + row * hidden, hidden, gv);
-    row = nrow;
-    if (row < rows) {
+    for (int k = 0; k < DEPTH; ++k) {
+      const int64_t row = base + k * G;
+      if (row >= rows) break;
+      float xv[ITEMS][VEC];
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) xv[it][i] = 0.f;
+        if (live[it]) unpack<T, VEC>(xb[k][it], xv[it]);
+      }
+      const int64_t nrow = row + DEPTH * G;
+      if (nrow < rows)
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it)
+          if (live[it]) xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
+      float mean = 0.f;
+      if (LN) {
+        float s[1] = {0.f};
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) s[0] += xv[it][i];
+        bsum(s);
+        mean = s[0] * inv_h;
+      }
+      float q[1] = {0.f};
 #pragma unroll
       for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) { xv[it][i] = nx[it][i]; gv[it][i] = ng[it][i]; }
-      r = nr;
+        for (int i = 0; i < VEC; ++i) {
+          // Padding columns hold x = 0 and must not add (0 - mean)^2.
+          const float d = live[it] && (col[it] + i < hidden) ? xv[it][i] - mean : 0.f;
+          q[0] += d * d;
+        }
+      bsum(q);
+      const float rstd = rsqrtf(q[0] * inv_h + eps);
+      T* yr = y + row * hidden;
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it) {
+        if (!live[it]) continue;
+        float o[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          o[i] = LN ? ((xv[it][i] - mean) * rstd) * wv[it][i] + bv[it][i]
+                    : (xv[it][i] * rstd) * wv[it][i];
+        st_vec<T, VEC>(yr + col[it], o);
+      }
+      if (threadIdx.x == 0) {
+        rstd_out[row] = rstd;
+        if (LN) mean_out[row] = mean;
+      }
     }
   }
-  float* pp = partial + (int64_t)blockIdx.x * hidden;
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-    if (c < hidden) store_f32<float, VEC>(pp + c, acc[it]);
-  }
 }
 
-// --------------------------------------------- RMSNorm forward, one wave per row
-// For rows of ITEMS x 64 lanes x VEC elements (hidden 512..4096 in bf16) a wave
-// owns a whole row: the statistic is reduced with wave butterflies only, so no
-// workgroup barrier sits between a row's loads and its stores, and the waves of a
-// CU drift independently, keeping many rows of loads in flight. (The same shape
-// for the backward, with per-lane dweight sums, measured slower than the
-// workgroup kernel below and is not used.)
-template <typename T, int VEC>
-__device__ __forceinline__ Pack<T, VEC> ld_pack(const T* __restrict__ p) {
-  static_assert(sizeof(T) * VEC == 16, "16-byte packs");
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  Pack<T, VEC> pk;
-  __builtin_memcpy(&pk, &raw, 16);
-  return pk;
-}
-
+// RMSNorm forward, one wave per row, for rows of ITEMS x 64 lanes x VEC elements.
 template <typename T, int VEC, int ITEMS>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
                                                         const T* __restrict__ w,
@@ -181,7 +233,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
   const T* xr = x + row * H;
   Pack<T, VEC> xp[ITEMS];
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) xp[it] = ld_pack<T, VEC>(xr + (it * kWave + lane) * VEC);
+  for (int it = 0; it < ITEMS; ++it) xp[it] = ld_raw<T, VEC>(xr + (it * kWave + lane) * VEC);
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it)
@@ -200,254 +252,209 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
     float o[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) o[i] = (to_f32(xp[it].v[i]) * r) * to_f32(wp.v[i]);
-    store_f32_nt<T, VEC>(yr + c, o);
+    st_vec<T, VEC>(yr + c, o);
   }
   if (lane == 0) rstd_out[row] = r;
 }
 
-// ---------------------------------------------------------------- LayerNorm
-template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
-__global__ __launch_bounds__(BLOCK) void layernorm_fwd_kernel(
-    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ b,
-    T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
-    int hidden, float eps) {
-  __shared__ float lds[BLOCK / kWave];
-  const int64_t row = blockIdx.x;
-  const int64_t off = row * hidden;
-  float xv[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK, NT>(x + off, hidden, xv);
-  float s = 0.f;
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) s += xv[it][i];
-  const float mean = block_reduce<BLOCK>(s, SumOp(), lds) / (float)hidden;
-  float q = 0.f;
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      const float d = (c + i < hidden) ? xv[it][i] - mean : 0.f;
-      q += d * d;
-    }
-  }
-  const float var = block_reduce<BLOCK>(q, SumOp(), lds) / (float)hidden;
-  const float rstd = rsqrtf(var + eps);
-  float wv[ITEMS][VEC], bv[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
-  load_cols<T, VEC, ITEMS, BLOCK>(b, hidden, bv);
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i)
-      xv[it][i] = ((xv[it][i] - mean) * rstd) * wv[it][i] + bv[it][i];
-  store_cols<T, VEC, ITEMS, BLOCK, NT>(y + off, hidden, xv);
-  if (threadIdx.x == 0) { mean_out[row] = mean; rstd_out[row] = rstd; }
-}
-
-template <typename T, int VEC, int ITEMS, int BLOCK, bool NT>
-__global__ __launch_bounds__(BLOCK) void layernorm_bwd_kernel(
+// -------------------------------------------------------------- backward
+// RMSNorm:   xhat = x * rstd, g = dy * w, dx = (g - xhat * mean(g * xhat)) * rstd
+// LayerNorm: xhat = (x - mean) * rstd, dx = rstd * (g - mean(g) - xhat * mean(g * xhat))
+// dweight += dy * xhat, dbias += dy (per thread, per owned column).
+template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN>
+__global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
     float* __restrict__ partial_w, float* __restrict__ partial_b, int64_t rows, int hidden) {
-  __shared__ float lds[2 * (BLOCK / kWave)];
+  constexpr int NS = LN ? 2 : 1;
+  __shared__ float slots[2][NS][BLOCK / kWave];
+  SlotSum<BLOCK, NS> bsum{slots, 0};
   const int64_t G = gridDim.x;
-  float wv[ITEMS][VEC], accw[ITEMS][VEC], accb[ITEMS][VEC];
-  load_cols<T, VEC, ITEMS, BLOCK>(w, hidden, wv);
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) { accw[it][i] = 0.f; accb[it][i] = 0.f; }
   const float inv_h = 1.0f / (float)hidden;
-
-  int64_t row = blockIdx.x;
-  float xv[ITEMS][VEC], gv[ITEMS][VEC];
-  float mu = 0.f, r = 0.f;
-  if (row < rows) {
-    load_cols<T, VEC, ITEMS, BLOCK, NT>(x + row * hidden, hidden, xv);
-    load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + row * hidden, hidden, gv);
-    mu = mean[row];
-    r = rstd[row];
+  int col[ITEMS];
+  bool live[ITEMS];
+  float wv[ITEMS][VEC], aw[ITEMS][VEC], ab[ITEMS][VEC];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    col[it] = (it * BLOCK + (int)threadIdx.x) * VEC;
+    live[it] = col[it] < hidden;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { wv[it][i] = 0.f; aw[it][i] = 0.f; ab[it][i] = 0.f; }
+    if (live[it]) unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(w + col[it]), wv[it]);
   }
-  while (row < rows) {
-    const int64_t nrow = row + G;
-    float nx[ITEMS][VEC], ng[ITEMS][VEC];
-    float nmu = 0.f, nr = 0.f;
-    if (nrow < rows) {
-      load_cols<T, VEC, ITEMS, BLOCK, NT>(x + nrow * hidden, hidden, nx);
-      load_cols<T, VEC, ITEMS, BLOCK, NT>(dy + nrow * hidden, hidden, ng);
-      nmu = mean[nrow];
-      nr = rstd[nrow];
-    }
-    float sg = 0.f, sgx = 0.f;
+  Pack<T, VEC> xb[DEPTH][ITEMS], gb[DEPTH][ITEMS];
+  float rb[DEPTH], mb[DEPTH];
 #pragma unroll
-    for (int it = 0; it < ITEMS; ++it) {
-      const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        // Padding columns load zeros for x but must also give xhat = 0.
-        const float xh = (c + i < hidden) ? (xv[it][i] - mu) * r : 0.f;
-        accw[it][i] += gv[it][i] * xh;
-        accb[it][i] += gv[it][i];
-        const float g = gv[it][i] * wv[it][i];
-        xv[it][i] = xh;
-        gv[it][i] = g;
-        sg += g;
-        sgx += g * xh;
-      }
-    }
-    block_reduce2<BLOCK>(sg, sgx, lds);
-    sg *= inv_h;
-    sgx *= inv_h;
-#pragma unroll
-    for (int it = 0; it < ITEMS; ++it)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) gv[it][i] = r * ((gv[it][i] - sg) - xv[it][i] * sgx);
-    store_cols<T, VEC, ITEMS, BLOCK, NT>(dx + row * hidden, hidden, gv);
-    row = nrow;
+  for (int k = 0; k < DEPTH; ++k) {
+    const int64_t row = blockIdx.x + k * G;
+    rb[k] = 0.f;
+    mb[k] = 0.f;
     if (row < rows) {
 #pragma unroll
       for (int it = 0; it < ITEMS; ++it)
+        if (live[it]) {
+          xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
+          gb[k][it] = ld_raw<T, VEC>(dy + row * hidden + col[it]);
+        }
+      rb[k] = rstd[row];
+      if (LN) mb[k] = mean[row];
+    }
+  }
+  for (int64_t base = blockIdx.x; base < rows; base += DEPTH * G) {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) { xv[it][i] = nx[it][i]; gv[it][i] = ng[it][i]; }
-      mu = nmu;
-      r = nr;
+    for (int k = 0; k < DEPTH; ++k) {
+      const int64_t row = base + k * G;
+      if (row >= rows) break;
+      const float r = rb[k], mu = mb[k];
+      float xh[ITEMS][VEC], g[ITEMS][VEC];
+      float s[NS];
+#pragma unroll
+      for (int j = 0; j < NS; ++j) s[j] = 0.f;
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it) {
+        float xv[VEC], gv[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) { xv[i] = 0.f; gv[i] = 0.f; }
+        if (live[it]) { unpack<T, VEC>(xb[k][it], xv); unpack<T, VEC>(gb[k][it], gv); }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          // Padding columns (dy = 0 there) must also give xhat = 0 for LayerNorm.
+          const bool in = live[it] && (col[it] + i < hidden);
+          const float h = LN ? (in ? (xv[i] - mu) * r : 0.f) : xv[i] * r;
+          aw[it][i] += gv[i] * h;
+          if (LN) ab[it][i] += gv[i];
+          const float gg = gv[i] * wv[it][i];
+          s[0] += gg * h;
+          if (LN) s[1] += gg;
+          xh[it][i] = h;
+          g[it][i] = gg;
+        }
+      }
+      const int64_t nrow = row + DEPTH * G;
+      if (nrow < rows) {
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it)
+          if (live[it]) {
+            xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
+            gb[k][it] = ld_raw<T, VEC>(dy + nrow * hidden + col[it]);
+          }
+        rb[k] = rstd[nrow];
+        if (LN) mb[k] = mean[nrow];
+      }
+      bsum(s);
+      const float dgx = s[0] * inv_h;
+      const float dg = LN ? s[1] * inv_h : 0.f;
+      T* dxr = dx + row * hidden;
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it) {
+        if (!live[it]) continue;
+        float o[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          o[i] = LN ? r * ((g[it][i] - dg) - xh[it][i] * dgx) : (g[it][i] - xh[it][i] * dgx) * r;
+        st_vec<T, VEC>(dxr + col[it], o);
+      }
     }
   }
   float* pw = partial_w + (int64_t)blockIdx.x * hidden;
-  float* pb = partial_b + (int64_t)blockIdx.x * hidden;
+  float* pb = LN ? partial_b + (int64_t)blockIdx.x * hidden : nullptr;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
-    if (c < hidden) {
-      store_f32<float, VEC>(pw + c, accw[it]);
-      store_f32<float, VEC>(pb + c, accb[it]);
+    if (!live[it]) continue;
+    if (col[it] + VEC <= hidden) {
+      store_f32<float, VEC>(pw + col[it], aw[it]);
+      if (LN) store_f32<float, VEC>(pb + col[it], ab[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        if (col[it] + i < hidden) {
+          pw[col[it] + i] = aw[it][i];
+          if (LN) pb[col[it] + i] = ab[it][i];
+        }
     }
   }
 }
 
 // ------------------------------------------------- stage 2: column sums
-// out[p][c] = sum_{g=0..G-1} partial[p][g][c] in a fixed order. A workgroup owns
-// 64 columns (16 lanes x 4 columns); its 16 row groups each sum the partial rows
-// g = rg, rg + 16, ... in ascending order with all loads of a batch issued
-// together, and the 16 group totals are then added in group order through LDS.
-// blockIdx.y selects the parameter (dweight, dbias).
-constexpr int kColGroups = 16;
-constexpr int kColBatch = 16;
-
+// out[c] = sum_{g=0..G-1} partial[g][c]. A wave owns 4 adjacent columns; lane l
+// adds the partial rows l, l + 64, l + 128, ... in ascending order (batches of 8
+// loads issued together), then the 64 lane totals are combined by a butterfly.
+// The order is fixed, so the result is bit-identical on every run.
+// blockIdx.y selects the parameter (0: p0 -> o0, 1: p1 -> o1).
 template <typename T>
-__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ partial,
+__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ p0,
+                                                     const float* __restrict__ p1,
                                                      T* __restrict__ o0, T* __restrict__ o1,
                                                      int G, int hidden) {
-  __shared__ float4 lds[kColGroups][16];
-  const int q = threadIdx.x & 15;   // column quad within the tile
-  const int rg = threadIdx.x >> 4;  // row group
-  const int c = blockIdx.x * 64 + 4 * q;
-  const float* p = partial + (int64_t)blockIdx.y * G * hidden;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (c + 3 < hidden && (hidden & 3) == 0) {
-    for (int g0 = rg; g0 < G; g0 += kColGroups * kColBatch) {
-      float4 v[kColBatch];
+  constexpr int kBatch = 8;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int c = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * 4;
+  if (c >= hidden) return;  // whole wave leaves together
+  const float* p = blockIdx.y == 0 ? p0 : p1;
+  T* o = blockIdx.y == 0 ? o0 : o1;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((hidden & 3) == 0) {
+    for (int g0 = lane; g0 < G; g0 += kWave * kBatch) {
+      float4 v[kBatch];
 #pragma unroll
-      for (int i = 0; i < kColBatch; ++i) {
-        const int g = g0 + i * kColGroups;
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = g0 + kWave * i;
         v[i] = g < G ? *reinterpret_cast<const float4*>(p + (int64_t)g * hidden + c)
                      : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
-      for (int i = 0; i < kColBatch; ++i) {
-        acc.x += v[i].x; acc.y += v[i].y; acc.z += v[i].z; acc.w += v[i].w;
+      for (int i = 0; i < kBatch; ++i) {
+        acc[0] += v[i].x; acc[1] += v[i].y; acc[2] += v[i].z; acc[3] += v[i].w;
       }
     }
   } else {
-    float a4[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int g = rg; g < G; g += kColGroups)
+    for (int g = lane; g < G; g += kWave)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (c + i < hidden) a4[i] += p[(int64_t)g * hidden + c + i];
-    acc = make_float4(a4[0], a4[1], a4[2], a4[3]);
+        if (c + i < hidden) acc[i] += p[(int64_t)g * hidden + c + i];
   }
-  lds[rg][q] = acc;
-  __syncthreads();
-  if (rg == 0) {
-    float4 t = lds[0][q];
 #pragma unroll
-    for (int r = 1; r < kColGroups; ++r) {
-      const float4 u = lds[r][q];
-      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
-    }
-    T* o = blockIdx.y == 0 ? o0 : o1;
-    const float tv[4] = {t.x, t.y, t.z, t.w};
+  for (int i = 0; i < 4; ++i) acc[i] = wave_reduce(acc[i], SumOp());
+  if (lane == 0)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (c + i < hidden) o[c + i] = from_f32<T>(tv[i]);
-  }
+      if (c + i < hidden) o[c + i] = from_f32<T>(acc[i]);
 }
 
 template <typename T>
-int launch_colsum(const float* partial, T* o0, T* o1, int nparams, int G, int hidden,
-                  hipStream_t st, const char* what) {
-  hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((hidden + 63) / 64), (unsigned)nparams),
-                     dim3(256), 0, st, partial, o0, o1, G, hidden);
+int launch_colsum(const float* p0, const float* p1, T* o0, T* o1, int nparams, int G,
+                  int hidden, hipStream_t st, const char* what) {
+  const int quads = (hidden + 3) / 4;
+  hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((quads + 3) / 4), (unsigned)nparams),
+                     dim3(256), 0, st, p0, p1, o0, o1, G, hidden);
   return check_launch(what);
 }
 
 // ------------------------------------------------------------- dispatch
-template <typename F>
-bool pick_norm_config(int64_t npack, F&& f) {
-  if (npack <= 64) return f.template go<64, 1>();
-  if (npack <= 128) return f.template go<128, 1>();
-  if (npack <= 256) return f.template go<256, 1>();
-  if (npack <= 512) return f.template go<512, 1>();
-  if (npack <= 1024) return f.template go<512, 2>();
-  if (npack <= 2048) return f.template go<1024, 2>();
-  if (npack <= 4096) return f.template go<1024, 4>();
-  if (npack <= 8192) return f.template go<1024, 8>();
-  return false;
-}
-
-template <typename T, int VEC>
-struct RmsFwd {
-  const T *x, *w; T* y; float* rstd; int64_t rows; int hidden; float eps; hipStream_t st;
-  template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
-                       dim3(BLOCK), 0, st, x, w, y, rstd, hidden, eps);
-    return true;
-  }
-};
-
-template <typename T, int VEC>
-struct RmsBwd {
-  const T *dy, *x, *w; const float* rstd; T* dx; float* part; int64_t rows; int hidden;
-  hipStream_t st;
-  template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>),
-                       dim3((unsigned)partial_blocks(rows)), dim3(BLOCK), 0, st, dy, x, w, rstd,
-                       dx, part, rows, hidden);
-    return true;
-  }
-};
-
-template <typename T, int VEC>
-struct LnFwd {
+template <typename T, int VEC, bool LN>
+struct FwdRing {
   const T *x, *w, *b; T* y; float *mean, *rstd; int64_t rows; int hidden; float eps;
   hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((layernorm_fwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
-                       dim3(BLOCK), 0, st, x, w, b, y, mean, rstd, hidden, eps);
+    const int64_t G = ring_blocks(rows, kFwdBlocks, BLOCK);
+    hipLaunchKernelGGL((norm_fwd_ring<T, VEC, ITEMS, BLOCK, ring_depth<ITEMS>(), LN>),
+                       dim3((unsigned)G), dim3(BLOCK), 0, st, x, w, b, y, mean, rstd, rows,
+                       hidden, eps);
     return true;
   }
 };
 
-template <typename T, int VEC>
-struct LnBwd {
+template <typename T, int VEC, bool LN>
+struct BwdRing {
   const T *dy, *x, *w; const float *mean, *rstd; T* dx; float *pw, *pb; int64_t rows;
   int hidden; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((layernorm_bwd_kernel<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>),
-                       dim3((unsigned)partial_blocks(rows)), dim3(BLOCK), 0, st, dy, x, w, mean,
-                       rstd, dx, pw, pb, rows, hidden);
+    // LayerNorm carries two partial sums per column: half the ring depth.
+    constexpr int D = LN ? (ring_depth<ITEMS>() > 1 ? ring_depth<ITEMS>() / 2 : 1)
+                         : ring_depth<ITEMS>();
+    const int64_t G = ring_blocks(rows, LN ? kLnBwdBlocks : kRmsBwdBlocks, BLOCK);
+    hipLaunchKernelGGL((norm_bwd_ring<T, VEC, ITEMS, BLOCK, D, LN>), dim3((unsigned)G),
+                       dim3(BLOCK), 0, st, dy, x, w, mean, rstd, dx, pw, pb, rows, hidden);
     return true;
   }
 };
@@ -474,24 +481,37 @@ bool vec_ok(int hidden, std::initializer_list<const void*> ptrs) {
   return true;
 }
 
+// Partial rows of the backward for a given dtype width (must match the launch).
+int64_t bwd_blocks(int64_t rows, int64_t hidden, bool ln, bool vec, int elem) {
+  const int64_t npack = vec ? (hidden + (16 / elem) - 1) / (16 / elem) : hidden;
+  return ring_blocks(rows, ln ? kLnBwdBlocks : kRmsBwdBlocks, ring_block_for(npack));
+}
+
 }  // namespace
 }  // namespace eg
 
 using namespace eg;
 
-// Workspace: nparams x [G, hidden] fp32 partials.
-static size_t norm_workspace_bytes(int64_t rows, int64_t hidden, int nparams) {
+// Workspace: nparams x [G, hidden] fp32 partials. G depends on the workgroup
+// width, which depends on the dtype; the size returned covers the widest case
+// (the 16-bit vector path has the narrowest workgroups, hence the largest G).
+static size_t norm_workspace_bytes(int64_t rows, int64_t hidden, bool ln) {
   if (rows <= 0 || hidden <= 0) return 0;
-  const int64_t G = partial_blocks(rows);
-  return (size_t)nparams * (size_t)G * (size_t)hidden * sizeof(float);
+  int64_t G = 0;
+  for (int elem : {2, 4})
+    for (bool vec : {true, false}) {
+      const int64_t g = bwd_blocks(rows, hidden, ln, vec, elem);
+      if (g > G) G = g;
+    }
+  return (size_t)(ln ? 2 : 1) * (size_t)G * (size_t)hidden * sizeof(float);
 }
 
 extern "C" size_t eg_rmsnorm_workspace_bytes(int64_t rows, int64_t hidden) {
-  return norm_workspace_bytes(rows, hidden, 1);
+  return norm_workspace_bytes(rows, hidden, false);
 }
 
 extern "C" size_t eg_layernorm_workspace_bytes(int64_t rows, int64_t hidden) {
-  return norm_workspace_bytes(rows, hidden, 2);
+  return norm_workspace_bytes(rows, hidden, true);
 }
 
 extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd,
@@ -506,27 +526,26 @@ extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float*
     using T = scalar_t;
     constexpr int V = 16 / sizeof(T);
     const int h = (int)hidden;
-    bool ok;
-    const int waves_items = h / (kWave * V);
+    const T* xp = (const T*)x;
+    const T* wp = (const T*)weight;
+    T* yp = (T*)y;
+    bool ok = true;
+    const int wave_items = h / (kWave * V);
     if (vec_ok<T>(h, {x, weight, y}) && h % (kWave * V) == 0 &&
-        (waves_items == 1 || waves_items == 2 || waves_items == 4 || waves_items == 8)) {
+        (wave_items == 1 || wave_items == 2 || wave_items == 4 || wave_items == 8)) {
       const unsigned grid = (unsigned)((rows + 3) / 4);
-      const T* xp = (const T*)x;
-      const T* wp = (const T*)weight;
-      T* yp = (T*)y;
-      switch (waves_items) {
+      switch (wave_items) {
         case 1: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
         case 2: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
         case 4: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
         default: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 8>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
       }
-      ok = true;
     } else if (vec_ok<T>(h, {x, weight, y})) {
-      RmsFwd<T, V> f{(const T*)x, (const T*)weight, (T*)y, rstd, rows, h, eps, st};
-      ok = pick_norm_config((h + V - 1) / V, f);
+      FwdRing<T, V, false> f{xp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
+      ok = pick_ring((h + V - 1) / V, f);
     } else {
-      RmsFwd<T, 1> f{(const T*)x, (const T*)weight, (T*)y, rstd, rows, h, eps, st};
-      ok = pick_norm_config(h, f);
+      FwdRing<T, 1, false> f{xp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
+      ok = pick_ring(h, f);
     }
     if (!ok) { set_error("eg_rmsnorm_fwd: hidden=%d too wide", h); return 1; }
     return check_launch("eg_rmsnorm_fwd");
@@ -554,18 +573,22 @@ extern "C" int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight,
     constexpr int V = 16 / sizeof(T);
     const int h = (int)hidden;
     float* part = (float*)workspace;
+    const bool vec = vec_ok<T>(h, {dy, x, weight, dx});
     bool ok;
-    if (vec_ok<T>(h, {dy, x, weight, dx})) {
-      RmsBwd<T, V> f{(const T*)dy, (const T*)x, (const T*)weight, rstd, (T*)dx, part, rows, h, st};
-      ok = pick_norm_config((h + V - 1) / V, f);
+    if (vec) {
+      BwdRing<T, V, false> f{(const T*)dy, (const T*)x, (const T*)weight, nullptr, rstd, (T*)dx,
+                             part, nullptr, rows, h, st};
+      ok = pick_ring((h + V - 1) / V, f);
     } else {
-      RmsBwd<T, 1> f{(const T*)dy, (const T*)x, (const T*)weight, rstd, (T*)dx, part, rows, h, st};
-      ok = pick_norm_config(h, f);
+      BwdRing<T, 1, false> f{(const T*)dy, (const T*)x, (const T*)weight, nullptr, rstd, (T*)dx,
+                             part, nullptr, rows, h, st};
+      ok = pick_ring(h, f);
     }
     if (!ok) { set_error("eg_rmsnorm_bwd: hidden=%d too wide", h); return 1; }
     if (int rc = check_launch("eg_rmsnorm_bwd")) return rc;
-    const int G = (int)partial_blocks(rows);
-    return launch_colsum<T>(part, (T*)dweight, (T*)dweight, 1, G, h, st, "eg_rmsnorm_bwd(colsum)");
+    const int G = (int)bwd_blocks(rows, h, false, vec, (int)sizeof(T));
+    return launch_colsum<T>(part, part, (T*)dweight, (T*)dweight, 1, G, h, st,
+                            "eg_rmsnorm_bwd(colsum)");
   });
 }
 
@@ -586,11 +609,11 @@ extern "C" int eg_layernorm_fwd(const void* x, const void* weight, const void* b
     const int h = (int)hidden;
     bool ok;
     if (vec_ok<T>(h, {x, weight, bias, y})) {
-      LnFwd<T, V> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
-      ok = pick_norm_config((h + V - 1) / V, f);
+      FwdRing<T, V, true> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
+      ok = pick_ring((h + V - 1) / V, f);
     } else {
-      LnFwd<T, 1> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
-      ok = pick_norm_config(h, f);
+      FwdRing<T, 1, true> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
+      ok = pick_ring(h, f);
     }
     if (!ok) { set_error("eg_layernorm_fwd: hidden=%d too wide", h); return 1; }
     return check_launch("eg_layernorm_fwd");
@@ -618,19 +641,21 @@ extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weigh
     using T = scalar_t;
     constexpr int V = 16 / sizeof(T);
     const int h = (int)hidden;
+    const bool vec = vec_ok<T>(h, {dy, x, weight, dx});
+    const int G = (int)bwd_blocks(rows, h, true, vec, (int)sizeof(T));
     float* pw = (float*)workspace;
-    float* pb = pw + partial_blocks(rows) * (int64_t)h;
+    float* pb = pw + (int64_t)G * h;
     bool ok;
-    if (vec_ok<T>(h, {dy, x, weight, dx})) {
-      LnBwd<T, V> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
-      ok = pick_norm_config((h + V - 1) / V, f);
+    if (vec) {
+      BwdRing<T, V, true> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
+      ok = pick_ring((h + V - 1) / V, f);
     } else {
-      LnBwd<T, 1> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
-      ok = pick_norm_config(h, f);
+      BwdRing<T, 1, true> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
+      ok = pick_ring(h, f);
     }
     if (!ok) { set_error("eg_layernorm_bwd: hidden=%d too wide", h); return 1; }
     if (int rc = check_launch("eg_layernorm_bwd")) return rc;
-    const int G = (int)partial_blocks(rows);
-    return launch_colsum<T>(pw, (T*)dweight, (T*)dbias, 2, G, h, st, "eg_layernorm_bwd(colsum)");
+    return launch_colsum<T>(pw, pb, (T*)dweight, (T*)dbias, 2, G, h, st,
+                            "eg_layernorm_bwd(colsum)");
   });
 }
