@@ -5,36 +5,47 @@
 // src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:107:
 //   o = softmax(q k^T * scale + causal mask) v,   lse = logsumexp(q k^T * scale + mask)
 // Backward recomputes P = exp(q k^T * scale - lse) and, with delta = rowsum(do * o):
-//   dv = P^T do,  dS = P * (do v^T - delta),  dq = scale * dS k,  dk = scale * dS^T q.
+//   dv = P^T do,  dS = P * (dP - delta) with dP = do v^T,  dq = scale * dS k,
+//   dk = scale * dS^T q.
 //
 // Layout: q, k, v, o, do, dq, dk, dv are [B, H, S, D] row-major (D contiguous);
 // lse and delta are fp32 [B, H, S].
 //
 // MFMA: v_mfma_f32_32x32x16_{bf16,f16}. Lane l of a wave holds, for an M x K
-// operand A, row l%32 and k = 8*(l/32) .. +7 (16 contiguous bytes when k runs
-// along memory); for B (K x N), column l%32 and the same k; the 32 x 32 fp32
-// result C gives lane l column l%32 and, in register r, row (r/4)*8 + (l/32)*4 + r%4.
-// Every product is arranged so that its result feeds the next one without a
-// shuffle: a result C (M x N) is the B operand of X * C, with the k index of that
-// product permuted to C's register order (rows 8j + 4*(l/32) + i). The matching A
-// operand is read from an LDS copy stored transposed with that permutation applied
-// to each 16-wide group ([0-3, 8-11, 4-7, 12-15]), so each operand fetch is one
-// 16-byte LDS read. Transposed tiles are 64 wide; their eight 16-byte groups are
-// XOR-swizzled by (row / 8) % 8 so that both the transposing 8-byte writes and
-// the 16-byte operand reads spread over the LDS banks.
+// operand A, row l%32 and k = 8*(l/32) .. +7; for B (K x N), column l%32 and the
+// same k; the 32 x 32 fp32 result C gives lane l column l%32 and, in register r,
+// row (r/4)*8 + (l/32)*4 + r%4. Every product is arranged so that its result is
+// the B operand of the next one without a shuffle: the k order of that product is
+// permuted to C's register order (rows 8j + 4*(l/32) + i), and its A operand is
+// read from LDS in the same order.
+//
+// LDS tiles are row-major ([rows][D], 16-byte chunks XOR-swizzled per row) and
+// are filled by direct buffer->LDS loads (no VGPR staging). One tile serves both
+// operand shapes:
+//   rows as A (k along D): one 16-byte ds_read_b128 per lane;
+//   transposed as A (rows = D index, k along the tile's rows): two
+//   ds_read_b64_tr_b16, each giving a lane 4 consecutive tile rows of one column.
+// gfx950 LDS serves 256 bytes per cycle; the swizzle 4*(r%4) + (r/4)%4 puts the
+// 16 rows of a b128 read in 16 distinct bank groups and the 4 rows of a
+// transpose read in 4 distinct 64-byte quarters (conflict-free at D = 128).
 //
 // Kernels (all deterministic, no atomics):
-//   attn_fwd:    one workgroup = 128 query rows of one (b, h) (4 waves x 32 rows);
-//                loops over 64-key tiles up to the diagonal; online softmax in the
-//                log2 domain with the running max refreshed only when it grows by
-//                more than 2^8 (exact: the reference point cancels in o = sum/l);
-//                S^T = K Q^T then O^T += V^T P^T.
-//   attn_delta:  delta = rowsum(do * o).
-//   attn_dkdv:   one workgroup = 128 keys (4 waves x 32 keys); loops over 64-row
-//                query tiles from the diagonal down; S = Q K^T, dP = dO V^T,
-//                dV^T += dO^T P, dK^T += Q^T dS.
-//   attn_dq:     one workgroup = 128 query rows; loops over 64-key tiles;
-//                S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
+//   attn_fwd:   workgroup = 4 waves x 32 query rows; double-buffered 64-key K and
+//               V tiles; online softmax in the log2 domain, the running max
+//               refreshed only when it grows by more than 2^8 (exact: the
+//               reference point cancels in o = sum / l); S^T = K Q^T, O^T += V^T P^T.
+//   attn_delta: delta = rowsum(do * o).
+//   attn_dkdv:  workgroup = NW waves x 32 keys (K, V in registers); double-buffered
+//               32-row Q and dO tiles from the diagonal down; S = Q K^T,
+//               dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
+//   attn_dq:    workgroup = 4 waves x 32 query rows; double-buffered 64-key K, V
+//               tiles; S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
+// The dQ pass recomputes S and dP (7 products executed where the causal
+// FLOP convention counts 5) so that no atomics are needed.
+//
+// Workgroup order: workgroup i runs on XCD i % 8 and every block of one (b, h)
+// is mapped to the same XCD, so K/V (or Q/dO) tiles of a head are shared in
+// that XCD's L2; the blocks with the most work are dispatched first.
 #include "eg_common.hpp"
 
 #include <initializer_list>
@@ -43,6 +54,8 @@ namespace eg {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+#define EG_LDS __attribute__((address_space(3)))
 
 template <typename T> struct MM;
 template <> struct MM<bf16_t> {
@@ -64,11 +77,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: refresh the max past 2^8 growth
 
-template <typename V>
-__device__ __forceinline__ V ld16(const uint16_t* p) {
-  return *reinterpret_cast<const V*>(p);
-}
-
 // Eight fp32 values (registers off..off+7 of a result tile) rounded and packed
 // as one MFMA operand.
 template <typename T>
@@ -83,106 +91,128 @@ __device__ __forceinline__ typename MM<T>::v8 pack8(const f32x16& c, int off) {
   return r;
 }
 
-// Four fp32 values scaled by `f`, packed as 8 bytes.
+// Writes the rows of a transposed 32 x 32 result (lane = row of the output, its
+// registers = 32 consecutive columns in C's order), scaled, as 8-byte stores.
 template <typename T>
-__device__ __forceinline__ uint2 pack4(const f32x16& c, int off, float f) {
-  uint2 u;
-  u.x = MM<T>::pack2(c[off + 0] * f, c[off + 1] * f);
-  u.y = MM<T>::pack2(c[off + 2] * f, c[off + 3] * f);
-  return u;
+__device__ __forceinline__ void store_rows(uint16_t* __restrict__ row, const f32x16& c, int t,
+                                           int hh, float f) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint2 u;
+    u.x = MM<T>::pack2(c[4 * g + 0] * f, c[4 * g + 1] * f);
+    u.y = MM<T>::pack2(c[4 * g + 2] * f, c[4 * g + 3] * f);
+    *reinterpret_cast<uint2*>(row + 32 * t + 8 * g + 4 * hh) = u;
+  }
 }
 
-// Transposed 64-wide tile: element offset of (row, position `pos` of the
-// permuted 64 columns). The 4-element chunks of each 16-group are stored in the
-// order 0, 2, 1, 3, and the 16-byte groups are XOR-swizzled by row.
-__device__ __forceinline__ int tperm(int i) {
-  const int c = (i >> 2) & 3;
-  return (i & ~15) | ((((c & 1) << 1) | (c >> 1)) << 2) | (i & 3);
-}
-__device__ __forceinline__ int toff(int row, int stride, int pos) {
-  return row * stride + ((((pos >> 3) ^ (row >> 3)) & 7) << 3) + (pos & 7);
-}
-
-// Element e (0..7) of a 16-byte pack of 16-bit values.
-__device__ __forceinline__ uint32_t half_of(const uint4& u, int e) {
-  const uint32_t word = (e >> 1) == 0 ? u.x : (e >> 1) == 1 ? u.y : (e >> 1) == 2 ? u.z : u.w;
-  return (e & 1) ? (word >> 16) : (word & 0xffffu);
-}
-
-// A 64 x D tile copied from HBM as 4-row x 8-column blocks, one block per
-// thread (D = 64 has 128 blocks: threads t and t + 128 carry the same block and
-// write the same values). Rows at or past `nrows` read as zero; the loads are
-// unconditional (clamped address + select) so no branch hides their wait.
 template <int D>
-struct Tile64 {
-  static constexpr int CB = D / 8;
-  static constexpr int COMBOS = 16 * CB;
-  uint4 r[4];
-
-  __device__ __forceinline__ int combo() const { return (int)threadIdx.x & (COMBOS - 1); }
-
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ src, int row0, int nrows) {
-    const int t = combo();
-    const int rb = t / CB, cb = t - (t / CB) * CB;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = row0 + 4 * rb + i;
-      const int rc = row < nrows ? row : nrows - 1;
-      const uint4 v = *reinterpret_cast<const uint4*>(src + (int64_t)rc * D + 8 * cb);
-      r[i] = row < nrows ? v : make_uint4(0, 0, 0, 0);
-    }
-  }
-
-  __device__ __forceinline__ void store_rows(uint16_t* lds, int stride) const {
-    const int t = combo();
-    const int rb = t / CB, cb = t - (t / CB) * CB;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4*>(lds + (4 * rb + i) * stride + 8 * cb) = r[i];
-  }
-
-  // Transposed: column c of the source becomes LDS row c; source row i goes to
-  // permuted position tperm(i).
-  __device__ __forceinline__ void store_cols(uint16_t* lds, int stride) const {
-    const int t = combo();
-    const int rb = t / CB, cb = t - (t / CB) * CB;
-    const int pos = tperm(4 * rb);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      uint2 u;
-      u.x = half_of(r[0], e) | (half_of(r[1], e) << 16);
-      u.y = half_of(r[2], e) | (half_of(r[3], e) << 16);
-      *reinterpret_cast<uint2*>(lds + toff(8 * cb + e, stride, pos)) = u;
-    }
-  }
-};
+__device__ __forceinline__ int swz(int row) {
+  return (((row & 3) << 2) | ((row >> 2) & 3)) & (D / 8 - 1);
+}
+template <int D>
+__device__ __forceinline__ int toff(int row, int chunk) {
+  return row * D + ((chunk ^ swz<D>(row)) << 3);
+}
 
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
+// A operand from the rows of a tile (row `row`, k = D columns 16kk + 8hh ..+7).
+template <typename V, int D>
+__device__ __forceinline__ V rd_rows(const uint16_t* lds, int row, int kk, int hh) {
+  return *reinterpret_cast<const V*>(lds + toff<D>(row, 2 * kk + hh));
+}
+
+// A operand of a transposed tile: rows = D index dd0 + l%32, k = 16 tile rows
+// from r16 in the permuted order r16 + 4hh + {0..3}, r16 + 8 + 4hh + {0..3}.
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j%4 of
+// the 8 bytes addressed by lanes 4i + j/4 (i = 0..3), so lane j points at row
+// 4hh + j/4, columns 4*(j%4) .. +3 and receives column j of rows +0..3.
+template <typename V, int D>
+__device__ __forceinline__ V rd_tr(const uint16_t* lds, int r16, int dd0, int lane) {
+  const int m = lane & 15, gs = (lane >> 4) & 1, hh = lane >> 5;
+  const int col = dd0 + 16 * gs + 4 * (m & 3);
+  const int chunk = col >> 3, sub = col & 7;
+  const int r0 = r16 + 4 * hh + (m >> 2);
+  const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EG_LDS i16x4*)(lds + toff<D>(r0, chunk) + sub));
+  const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EG_LDS i16x4*)(lds + toff<D>(r0 + 8, chunk) + sub));
+  V r;
+  __builtin_memcpy(&r, &a, 8);
+  __builtin_memcpy(reinterpret_cast<char*>(&r) + 8, &b, 8);
+  return r;
+}
+
+// Copies rows [row0, row0 + ROWS) of a [nrows, D] slice into a swizzled LDS tile
+// with 16-byte buffer->LDS loads. Each lane's offset inside the tile is fixed;
+// the buffer resource starts at row0 and ends at the slice's last row, so rows
+// past the slice are never fetched (their LDS rows keep earlier, finite values).
+template <int ROWS, int D, int NW>
+struct TileLoader {
+  static constexpr int CPR = D / 8;
+  static constexpr int ITER = ROWS * CPR / (64 * NW);
+  static_assert(ITER >= 1 && ITER * 64 * NW == ROWS * CPR, "tile must split evenly over the waves");
+  int voff[ITER];
+  __device__ __forceinline__ void init() {
+    const int w = wave_id(), lane = threadIdx.x & 63;
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int p = (it * NW + w) * 64 + lane;
+      const int r = p / CPR;
+      const int c = (p % CPR) ^ swz<D>(r);
+      voff[it] = (r * D + c * 8) * 2;
+    }
+  }
+  __device__ __forceinline__ void load(const uint16_t* slice, int row0, int nrows,
+                                       uint16_t* lds) const {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(slice + (int64_t)row0 * D), (short)0, (nrows - row0) * D * 2,
+        0x00020000);
+    const int w = wave_id();
+#pragma unroll
+    for (int it = 0; it < ITER; ++it)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (EG_LDS void*)(lds + (it * NW + w) * 64 * 8), 16,
+                                               voff[it], 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int NT>
+__device__ __forceinline__ void zero_lds(void* p, int bytes) {
+  uint4* z = reinterpret_cast<uint4*>(p);
+  for (int e = threadIdx.x; e < bytes / 16; e += NT) z[e] = make_uint4(0, 0, 0, 0);
+}
+
+// Workgroup i -> (head, block index): XCD i % 8 holds heads xcd, xcd + 8, ...;
+// block index 0 is dispatched first for every head.
+__device__ __forceinline__ void block_coords(int BH, int& bh, int& blk) {
+  const int i = blockIdx.x;
+  const int xcd = i % 8, rest = i / 8;
+  const int groups = (BH + 7) / 8;
+  bh = xcd + 8 * (rest % groups);
+  blk = rest / groups;
+}
+
 // ------------------------------------------------------------------ forward
-template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int S,
-    float scale_log2, int nqb) {
+    float scale_log2, int nqb, int BH) {
   using v8 = typename MM<T>::v8;
-  constexpr int BM = 128, BN = 64;
-  constexpr int KSTEPS = D / 16;
-  constexpr int DT = D / 32;
-  constexpr int KST = D + 8;   // K row stride (elements)
-  constexpr int VST = BN + 8;  // V^T row stride
-  __shared__ __align__(16) uint16_t Ks[BN * KST];
-  __shared__ __align__(16) uint16_t Vt[D * VST];
+  constexpr int BM = 32 * NW, BN = 64;
+  constexpr int KSTEPS = D / 16, DT = D / 32;
+  __shared__ __align__(16) uint16_t Ks[2][BN * D];
+  __shared__ __align__(16) uint16_t Vs[2][BN * D];
 
-  const int bh = blockIdx.y;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest rows first
-  const int q0 = qb * BM;
+  int bh, blk;
+  block_coords(BH, bh, blk);
+  if (bh >= BH) return;
+  const int q0 = (nqb - 1 - blk) * BM;  // longest rows first
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
-  const uint16_t* qp = q + base;
   const uint16_t* kp = k + base;
   const uint16_t* vp = v + base;
 
@@ -190,66 +220,61 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
   const int qrc = qrow < S ? qrow : S - 1;
   v8 qf[KSTEPS];
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) {
-    const v8 t = ld16<v8>(qp + (int64_t)qrc * D + kk * 16 + 8 * hh);
-    qf[kk] = qrow < S ? t : v8{};
-  }
+  for (int kk = 0; kk < KSTEPS; ++kk)
+    qf[kk] = *reinterpret_cast<const v8*>(q + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
 
   f32x16 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
   float m = -INFINITY, lsum = 0.f;
-
   const int kv_end = min(S, q0 + BM);
   const int ntiles = (kv_end + BN - 1) / BN;
   const int wave_first_row = q0 + 32 * w;
 
-  Tile64<D> kt, vt;
-  kt.load(kp, 0, S);
-  vt.load(vp, 0, S);
+  zero_lds<NW * 64>(Ks, sizeof(Ks));
+  zero_lds<NW * 64>(Vs, sizeof(Vs));
+  __syncthreads();
+  TileLoader<BN, D, NW> ld;
+  ld.init();
+  ld.load(kp, 0, S, Ks[0]);
+  ld.load(vp, 0, S, Vs[0]);
   for (int j = 0; j < ntiles; ++j) {
+    wait_loads();
     __syncthreads();
-    kt.store_rows(Ks, KST);
-    vt.store_cols(Vt, VST);
-    __syncthreads();
-    const int k0 = j * BN;
+    const int buf = j & 1;
     if (j + 1 < ntiles) {
-      kt.load(kp, k0 + BN, S);
-      vt.load(vp, k0 + BN, S);
+      ld.load(kp, (j + 1) * BN, S, Ks[buf ^ 1]);
+      ld.load(vp, (j + 1) * BN, S, Vs[buf ^ 1]);
     }
+    const int k0 = j * BN;
     if (k0 > wave_first_row + 31) continue;  // every key of the tile is above this wave's rows
-
-    f32x16 s[2];
-#pragma unroll
-    for (int T2 = 0; T2 < 2; ++T2) s[T2] = f32x16{};
+    const uint16_t* Kb = Ks[buf];
+    const uint16_t* Vb = Vs[buf];
+    f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2)
-        s[T2] = MM<T>::mma(ld16<v8>(Ks + (32 * T2 + l32) * KST + kk * 16 + 8 * hh), qf[kk], s[T2]);
+        s[T2] = MM<T>::mma(rd_rows<v8, D>(Kb, 32 * T2 + l32, kk, hh), qf[kk], s[T2]);
 
+    // Raw scores: keys past the diagonal (and past S) are -inf; max in raw units.
     float mt = -INFINITY;
-    if (k0 + BN - 1 > wave_first_row) {  // tile crosses the diagonal for this wave
+    if (k0 + BN - 1 > wave_first_row) {
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
-          const float x = key > qrow ? -INFINITY : s[T2][r] * scale_log2;
-          s[T2][r] = x;
-          mt = fmaxf(mt, x);
+          if (key > qrow) s[T2][r] = -INFINITY;
+          mt = fmaxf(mt, s[T2][r]);
         }
     } else {
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = s[T2][r] * scale_log2;
-          s[T2][r] = x;
-          mt = fmaxf(mt, x);
-        }
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[T2][r]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
     // Refresh the reference max only when some row's max grew past the
     // threshold (always on the first tile, where m is -inf).
     if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleThreshold) != 0) {
@@ -260,13 +285,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
       for (int t = 0; t < DT; ++t) acc[t] *= alpha;
       m = m_new;
     }
-    const float m_use = m == -INFINITY ? 0.f : m;
+    const float nm = m == -INFINITY ? 0.f : -m;
     float ps = 0.f;
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[T2][r] - m_use);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[T2][r], scale_log2, nm));
         s[T2][r] = p;
         ps += p;
       }
@@ -276,7 +301,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
       const v8 pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
 #pragma unroll
       for (int t = 0; t < DT; ++t)
-        acc[t] = MM<T>::mma(ld16<v8>(Vt + toff(32 * t + l32, VST, ms * 16 + 8 * hh)), pb, acc[t]);
+        acc[t] = MM<T>::mma(rd_tr<v8, D>(Vb, 16 * ms, 32 * t, lane), pb, acc[t]);
     }
   }
 
@@ -285,10 +310,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
     const float inv = 1.0f / ltot;
     uint16_t* op = o + base + (int64_t)qrow * D;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<uint2*>(op + 32 * t + 8 * g + 4 * hh) = pack4<T>(acc[t], 4 * g, inv);
+    for (int t = 0; t < DT; ++t) store_rows<T>(op, acc[t], t, hh, inv);
     if (hh == 0) lse[(int64_t)bh * S + qrow] = (m + log2f(ltot)) * kLn2;
   }
 }
@@ -318,27 +340,23 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const uint16_t* __restr
 }
 
 // ------------------------------------------------------------ dK, dV
-template <typename T, int D>
-__global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
+template <typename T, int D, int NW, int BQ>
+__global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
-    uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int nkb) {
+    uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int BH) {
   using v8 = typename MM<T>::v8;
-  constexpr int BK = 128, BQ = 64;
-  constexpr int KSTEPS = D / 16;
-  constexpr int DT = D / 32;
-  constexpr int RST = D + 8;   // row-major tile stride
-  constexpr int TST = BQ + 8;  // transposed tile stride
-  __shared__ __align__(16) uint16_t Qs[BQ * RST];
-  __shared__ __align__(16) uint16_t Ds[BQ * RST];
-  __shared__ __align__(16) uint16_t Qt[D * TST];
-  __shared__ __align__(16) uint16_t Dt[D * TST];
-  __shared__ __align__(16) float Ls[BQ];
-  __shared__ __align__(16) float Es[BQ];
+  constexpr int BK = 32 * NW;
+  constexpr int KSTEPS = D / 16, DT = D / 32, MT = BQ / 32;
+  __shared__ __align__(16) uint16_t Qs[2][BQ * D];
+  __shared__ __align__(16) uint16_t Ds[2][BQ * D];
+  __shared__ __align__(16) float Ls[2][BQ];
+  __shared__ __align__(16) float Es[2][BQ];
 
-  const int bh = blockIdx.y;
-  const int kb = nkb - 1 - (int)blockIdx.x;
+  int bh, kb;
+  block_coords(BH, bh, kb);  // kb = 0 (the longest walk) first
+  if (bh >= BH) return;
   const int k0 = kb * BK;
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
@@ -351,118 +369,127 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
   v8 kf[KSTEPS], vf[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    const v8 a = ld16<v8>(k + base + (int64_t)krc * D + kk * 16 + 8 * hh);
-    const v8 b = ld16<v8>(v + base + (int64_t)krc * D + kk * 16 + 8 * hh);
-    kf[kk] = key < S ? a : v8{};
-    vf[kk] = key < S ? b : v8{};
+    kf[kk] = *reinterpret_cast<const v8*>(k + base + (int64_t)krc * D + kk * 16 + 8 * hh);
+    vf[kk] = *reinterpret_cast<const v8*>(v + base + (int64_t)krc * D + kk * 16 + 8 * hh);
   }
   f32x16 dka[DT], dva[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) { dka[t] = f32x16{}; dva[t] = f32x16{}; }
 
+  zero_lds<NW * 64>(Qs, sizeof(Qs));
+  zero_lds<NW * 64>(Ds, sizeof(Ds));
   const int i_first = k0 / BQ;
   const int i_end = (S + BQ - 1) / BQ;
   const int wave_first_key = k0 + 32 * w;
-
-  Tile64<D> qt, dt;
-  float lreg = 0.f, ereg = 0.f;
-  auto load_q = [&](int i) {
-    qt.load(q + base, i * BQ, S);
-    dt.load(dout + base, i * BQ, S);
-    const int row = i * BQ + ((int)threadIdx.x & (BQ - 1));
-    const int rc = row < S ? row : S - 1;
-    const float lv = lsep[rc], ev = delp[rc];
-    lreg = row < S ? lv * kLog2e : INFINITY;
-    ereg = row < S ? ev : 0.f;
+  const uint16_t* qp = q + base;
+  const uint16_t* dp_ = dout + base;
+  TileLoader<BQ, D, NW> ld;
+  ld.init();
+  // lse (as log2) and delta of a tile's rows: wave 0 loads them into registers
+  // when the tile is requested and stores them to LDS after its own compute.
+  float lreg = INFINITY, ereg = 0.f;
+  auto load_stats = [&](int i) {
+    if (w == 0 && lane < BQ) {
+      const int row = i * BQ + lane;
+      const int rc = row < S ? row : S - 1;
+      const float lv = lsep[rc], ev = delp[rc];
+      lreg = row < S ? lv * kLog2e : INFINITY;
+      ereg = row < S ? ev : 0.f;
+    }
   };
-  if (i_first < i_end) load_q(i_first);
+  __syncthreads();
+  if (i_first < i_end) {
+    ld.load(qp, i_first * BQ, S, Qs[0]);
+    ld.load(dp_, i_first * BQ, S, Ds[0]);
+    load_stats(i_first);
+    if (w == 0 && lane < BQ) { Ls[0][lane] = lreg; Es[0][lane] = ereg; }
+  }
   for (int i = i_first; i < i_end; ++i) {
+    wait_loads();
     __syncthreads();
-    qt.store_rows(Qs, RST);
-    qt.store_cols(Qt, TST);
-    dt.store_rows(Ds, RST);
-    dt.store_cols(Dt, TST);
-    if (threadIdx.x < BQ) { Ls[threadIdx.x] = lreg; Es[threadIdx.x] = ereg; }
-    __syncthreads();
+    const int buf = (i - i_first) & 1;
+    const bool more = i + 1 < i_end;
+    if (more) {
+      ld.load(qp, (i + 1) * BQ, S, Qs[buf ^ 1]);
+      ld.load(dp_, (i + 1) * BQ, S, Ds[buf ^ 1]);
+      load_stats(i + 1);
+    }
     const int qi0 = i * BQ;
-    if (i + 1 < i_end) load_q(i + 1);
-    if (qi0 + BQ - 1 < wave_first_key) continue;  // all rows above this wave's keys
-
-    f32x16 s[2], dp[2];
+    if (qi0 + BQ - 1 >= wave_first_key) {  // some row of the tile sees some key of this wave
+      const uint16_t* Qb = Qs[buf];
+      const uint16_t* Db = Ds[buf];
+      f32x16 s[MT], dp[MT];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) { s[mt] = f32x16{}; dp[mt] = f32x16{}; }
+      for (int mt = 0; mt < MT; ++mt) { s[mt] = f32x16{}; dp[mt] = f32x16{}; }
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
+      for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        s[mt] = MM<T>::mma(ld16<v8>(Qs + (32 * mt + l32) * RST + kk * 16 + 8 * hh), kf[kk], s[mt]);
-        dp[mt] = MM<T>::mma(ld16<v8>(Ds + (32 * mt + l32) * RST + kk * 16 + 8 * hh), vf[kk], dp[mt]);
-      }
-    const bool diag = qi0 < wave_first_key + 31;
+        for (int mt = 0; mt < MT; ++mt) {
+          s[mt] = MM<T>::mma(rd_rows<v8, D>(Qb, 32 * mt + l32, kk, hh), kf[kk], s[mt]);
+          dp[mt] = MM<T>::mma(rd_rows<v8, D>(Db, 32 * mt + l32, kk, hh), vf[kk], dp[mt]);
+        }
+      // Masking: the diagonal tiles (keys past a row) and a tail tile past S.
+      const bool edge = qi0 < wave_first_key + 31 || qi0 + BQ > S;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int rr = 32 * mt + 8 * g + 4 * hh;  // first row of this 4-row group
-        const float4 l4 = *reinterpret_cast<const float4*>(Ls + rr);
-        const float4 e4 = *reinterpret_cast<const float4*>(Es + rr);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+        for (int g = 0; g < 4; ++g) {
+          const int rr = 32 * mt + 8 * g + 4 * hh;  // first row of this 4-row group
+          const float4 l4 = *reinterpret_cast<const float4*>(&Ls[buf][rr]);
+          const float4 e4 = *reinterpret_cast<const float4*>(&Es[buf][rr]);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+          const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int r = 4 * g + i4;
-          float p = __builtin_amdgcn_exp2f(s[mt][r] * scale_log2 - lv[i4]);
-          if (diag && key > qi0 + rr + i4) p = 0.f;
-          s[mt][r] = p;
-          dp[mt][r] = p * (dp[mt][r] - ev[i4]);
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const int r = 4 * g + i4;
+            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][r], scale_log2, -lv[i4]));
+            if (edge && (key > qi0 + rr + i4 || qi0 + rr + i4 >= S)) p = 0.f;
+            s[mt][r] = p;
+            dp[mt][r] = p * (dp[mt][r] - ev[i4]);
+          }
+        }
+#pragma unroll
+      for (int ms = 0; ms < BQ / 16; ++ms) {
+        const v8 pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
+        const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          dva[t] = MM<T>::mma(rd_tr<v8, D>(Db, 16 * ms, 32 * t, lane), pb, dva[t]);
+          dka[t] = MM<T>::mma(rd_tr<v8, D>(Qb, 16 * ms, 32 * t, lane), sb, dka[t]);
         }
       }
-#pragma unroll
-    for (int ms = 0; ms < BQ / 16; ++ms) {
-      const v8 pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
-      const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const int off = toff(32 * t + l32, TST, ms * 16 + 8 * hh);
-        dva[t] = MM<T>::mma(ld16<v8>(Dt + off), pb, dva[t]);
-        dka[t] = MM<T>::mma(ld16<v8>(Qt + off), sb, dka[t]);
-      }
     }
+    if (more && w == 0 && lane < BQ) { Ls[buf ^ 1][lane] = lreg; Es[buf ^ 1][lane] = ereg; }
   }
 
   if (key < S) {
     uint16_t* dkp = dk + base + (int64_t)key * D;
     uint16_t* dvp = dv + base + (int64_t)key * D;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        *reinterpret_cast<uint2*>(dkp + 32 * t + 8 * g + 4 * hh) = pack4<T>(dka[t], 4 * g, scale);
-        *reinterpret_cast<uint2*>(dvp + 32 * t + 8 * g + 4 * hh) = pack4<T>(dva[t], 4 * g, 1.0f);
-      }
+    for (int t = 0; t < DT; ++t) {
+      store_rows<T>(dkp, dka[t], t, hh, scale);
+      store_rows<T>(dvp, dva[t], t, hh, 1.0f);
+    }
   }
 }
 
 // ------------------------------------------------------------------- dQ
-template <typename T, int D>
-__global__ __launch_bounds__(256, 1) void attn_dq_kernel(
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dq,
-    int S, float scale, float scale_log2, int nqb) {
+    int S, float scale, float scale_log2, int nqb, int BH) {
   using v8 = typename MM<T>::v8;
-  constexpr int BM = 128, BN = 64;
-  constexpr int KSTEPS = D / 16;
-  constexpr int DT = D / 32;
-  constexpr int RST = D + 8;
-  constexpr int TST = BN + 8;
-  __shared__ __align__(16) uint16_t Ks[BN * RST];
-  __shared__ __align__(16) uint16_t Vs[BN * RST];
-  __shared__ __align__(16) uint16_t Kt[D * TST];
+  constexpr int BM = 32 * NW, BN = 64;
+  constexpr int KSTEPS = D / 16, DT = D / 32;
+  __shared__ __align__(16) uint16_t Ks[2][BN * D];
+  __shared__ __align__(16) uint16_t Vs[2][BN * D];
 
-  const int bh = blockIdx.y;
-  const int qb = nqb - 1 - (int)blockIdx.x;
-  const int q0 = qb * BM;
+  int bh, blk;
+  block_coords(BH, bh, blk);
+  if (bh >= BH) return;
+  const int q0 = (nqb - 1 - blk) * BM;
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
@@ -472,10 +499,8 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
   v8 qf[KSTEPS], df[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    const v8 a = ld16<v8>(q + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
-    const v8 b = ld16<v8>(dout + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
-    qf[kk] = qrow < S ? a : v8{};
-    df[kk] = qrow < S ? b : v8{};
+    qf[kk] = *reinterpret_cast<const v8*>(q + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
+    df[kk] = *reinterpret_cast<const v8*>(dout + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
   }
   const float lv = lse[(int64_t)bh * S + qrc], ev = delta[(int64_t)bh * S + qrc];
   const float l2 = qrow < S ? lv * kLog2e : INFINITY;
@@ -484,46 +509,48 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
   f32x16 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
-
   const int kv_end = min(S, q0 + BM);
   const int ntiles = (kv_end + BN - 1) / BN;
   const int wave_first_row = q0 + 32 * w;
+  const uint16_t* kp = k + base;
+  const uint16_t* vp = v + base;
 
-  Tile64<D> kt, vt;
-  kt.load(k + base, 0, S);
-  vt.load(v + base, 0, S);
+  zero_lds<NW * 64>(Ks, sizeof(Ks));
+  zero_lds<NW * 64>(Vs, sizeof(Vs));
+  __syncthreads();
+  TileLoader<BN, D, NW> ld;
+  ld.init();
+  ld.load(kp, 0, S, Ks[0]);
+  ld.load(vp, 0, S, Vs[0]);
   for (int j = 0; j < ntiles; ++j) {
+    wait_loads();
     __syncthreads();
-    kt.store_rows(Ks, RST);
-    kt.store_cols(Kt, TST);
-    vt.store_rows(Vs, RST);
-    __syncthreads();
-    const int k0 = j * BN;
+    const int buf = j & 1;
     if (j + 1 < ntiles) {
-      kt.load(k + base, k0 + BN, S);
-      vt.load(v + base, k0 + BN, S);
+      ld.load(kp, (j + 1) * BN, S, Ks[buf ^ 1]);
+      ld.load(vp, (j + 1) * BN, S, Vs[buf ^ 1]);
     }
+    const int k0 = j * BN;
     if (k0 > wave_first_row + 31) continue;
-
-    f32x16 s[2], dp[2];
-#pragma unroll
-    for (int T2 = 0; T2 < 2; ++T2) { s[T2] = f32x16{}; dp[T2] = f32x16{}; }
+    const uint16_t* Kb = Ks[buf];
+    const uint16_t* Vb = Vs[buf];
+    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2) {
-        s[T2] = MM<T>::mma(ld16<v8>(Ks + (32 * T2 + l32) * RST + kk * 16 + 8 * hh), qf[kk], s[T2]);
-        dp[T2] = MM<T>::mma(ld16<v8>(Vs + (32 * T2 + l32) * RST + kk * 16 + 8 * hh), df[kk], dp[T2]);
+        s[T2] = MM<T>::mma(rd_rows<v8, D>(Kb, 32 * T2 + l32, kk, hh), qf[kk], s[T2]);
+        dp[T2] = MM<T>::mma(rd_rows<v8, D>(Vb, 32 * T2 + l32, kk, hh), df[kk], dp[T2]);
       }
     const bool diag = k0 + BN - 1 > wave_first_row;
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(s[T2][r] * scale_log2 - l2);
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[T2][r], scale_log2, -l2));
         if (diag) {
-          const int key = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
-          if (key > qrow) p = 0.f;
+          const int kkey = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
+          if (kkey > qrow) p = 0.f;
         }
         dp[T2][r] = p * (dp[T2][r] - dl);
       }
@@ -532,36 +559,49 @@ __global__ __launch_bounds__(256, 1) void attn_dq_kernel(
       const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
 #pragma unroll
       for (int t = 0; t < DT; ++t)
-        acc[t] = MM<T>::mma(ld16<v8>(Kt + toff(32 * t + l32, TST, ms * 16 + 8 * hh)), sb, acc[t]);
+        acc[t] = MM<T>::mma(rd_tr<v8, D>(Kb, 16 * ms, 32 * t, lane), sb, acc[t]);
     }
   }
 
   if (qrow < S) {
     uint16_t* op = dq + base + (int64_t)qrow * D;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<uint2*>(op + 32 * t + 8 * g + 4 * hh) = pack4<T>(acc[t], 4 * g, scale);
+    for (int t = 0; t < DT; ++t) store_rows<T>(op, acc[t], t, hh, scale);
   }
 }
 
 // --------------------------------------------------------------- launchers
+constexpr int kFwdWaves = 4;
+constexpr int kDqWaves = 4;
+constexpr int kDkdvRows = 32;
+// dK/dV workgroup width: 8 waves (256 keys) at D = 128, 4 at D = 64 (a 32-row
+// tile of 64 columns is one 16-byte chunk per lane of 4 waves).
+template <int D> constexpr int dkdv_waves() { return D == 128 ? 8 : 4; }
+
 int check_attn(const char* what, int64_t B, int64_t H, int64_t S, int64_t D, int dtype) {
   if (B < 0 || H < 0 || S < 0) { set_error("%s: negative size", what); return 1; }
   if (D != 64 && D != 128) { set_error("%s: head_dim must be 64 or 128, got %lld", what, (long long)D); return 1; }
   if (dtype != EG_BF16 && dtype != EG_F16) { set_error("%s: dtype must be bf16 or fp16", what); return 1; }
-  if (S > (int64_t)1 << 24 || B * H > 65535) { set_error("%s: size out of range", what); return 1; }
+  // One (b, h) slice is addressed with 32-bit buffer offsets: S * D * 2 < 2^31.
+  if (S > ((int64_t)1 << 22) || B * H > ((int64_t)1 << 24)) {
+    set_error("%s: size out of range (seq <= 4194304, batch*heads <= 16777216)", what);
+    return 1;
+  }
   return 0;
+}
+
+inline unsigned grid_for(int64_t BH, int nblocks) {
+  return (unsigned)(((BH + 7) / 8) * 8 * nblocks);
 }
 
 template <typename T, int D>
 int attn_fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
                     int64_t S, float scale, hipStream_t st) {
-  const int nqb = (int)((S + 127) / 128);
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D>), dim3((unsigned)nqb, (unsigned)BH), dim3(256), 0, st,
+  constexpr int NW = kFwdWaves;
+  const int nqb = (int)((S + 32 * NW - 1) / (32 * NW));
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NW>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
-                     (int)S, scale * kLog2e, nqb);
+                     (int)S, scale * kLog2e, nqb, (int)BH);
   return check_launch("eg_attn_fwd");
 }
 
@@ -574,19 +614,42 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
   hipLaunchKernelGGL((attn_delta_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256),
                      0, st, (const uint16_t*)dout, (const uint16_t*)o, delta, nrows);
   if (int rc = check_launch("eg_attn_bwd(delta)")) return rc;
-  const int nkb = (int)((S + 127) / 128);
-  hipLaunchKernelGGL((attn_dkdv_kernel<T, D>), dim3((unsigned)nkb, (unsigned)BH), dim3(256), 0, st,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+  constexpr int NK = dkdv_waves<D>();
+  const int nkb = (int)((S + 32 * NK - 1) / (32 * NK));
+  hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, kDkdvRows>), dim3(grid_for(BH, nkb)), dim3(NK * 64),
+                     0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                      (const uint16_t*)dout, lse, delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale,
-                     scale * kLog2e, nkb);
+                     scale * kLog2e, (int)BH);
   if (int rc = check_launch("eg_attn_bwd(dkdv)")) return rc;
-  const int nqb = (int)((S + 127) / 128);
-  hipLaunchKernelGGL((attn_dq_kernel<T, D>), dim3((unsigned)nqb, (unsigned)BH), dim3(256), 0, st,
+  constexpr int NQ = kDqWaves;
+  const int nqb = (int)((S + 32 * NQ - 1) / (32 * NQ));
+  hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ>), dim3(grid_for(BH, nqb)), dim3(NQ * 64), 0, st,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                      (const uint16_t*)dout, lse, delta, (uint16_t*)dq, (int)S, scale,
-                     scale * kLog2e, nqb);
+                     scale * kLog2e, nqb, (int)BH);
   return check_launch("eg_attn_bwd(dq)");
 }
+
+// Explicit instantiations: hip-clang leaves some implicitly instantiated kernel
+// templates without a host launch stub (undefined symbol at load time); naming
+// every kernel here makes the stubs certain.
+#define EG_ATTN_INSTANTIATE(T, D)                                                            \
+  template __global__ void attn_fwd_kernel<T, D, kFwdWaves>(                                 \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, float, int,   \
+      int);                                                                                  \
+  template __global__ void attn_delta_kernel<T, D>(const uint16_t*, const uint16_t*, float*,   \
+                                                   int64_t);                                 \
+  template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows>(               \
+      const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
+      const float*, uint16_t*, uint16_t*, int, float, float, int);                             \
+  template __global__ void attn_dq_kernel<T, D, kDqWaves>(                                   \
+      const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
+      const float*, uint16_t*, int, float, float, int, int);
+EG_ATTN_INSTANTIATE(bf16_t, 128)
+EG_ATTN_INSTANTIATE(bf16_t, 64)
+EG_ATTN_INSTANTIATE(f16_t, 128)
+EG_ATTN_INSTANTIATE(f16_t, 64)
+#undef EG_ATTN_INSTANTIATE
 
 bool attn_aligned(std::initializer_list<const void*> ptrs) {
   for (const void* p : ptrs)
