@@ -81,6 +81,69 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
     raise KeyError(name)
 
 
+# Kernels each entry point launches, in launch order (index = position).
+KERNELS = {
+    "softmax": {"fwd": ["softmax_fwd"], "bwd": ["softmax_bwd"]},
+    "rmsnorm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_kernel"]},
+    "layernorm": {"fwd": ["norm_fwd_ring"], "bwd": ["norm_bwd_ring", "colsum_kernel"]},
+    "swiglu": {"fwd": ["swiglu_fwd_kernel"], "bwd": ["swiglu_bwd_kernel"]},
+    "rope": {"fwd": ["rope_kernel"], "bwd": ["rope_kernel"]},
+    "causal_attention": {"fwd": ["attn_fwd_kernel"],
+                         "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
+}
+
+# The kernel whose roofline each op reports, with its algorithmic work per launch.
+DOMINANT = {
+    "softmax": ("bwd", 0), "rmsnorm": ("bwd", 0), "layernorm": ("bwd", 0),
+    "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
+}
+
+
+def dominant_work(name: str, w, work: dict) -> float:
+    """Algorithmic bytes (or FLOPs) of one launch of the op's dominant kernel."""
+    d = w.dims
+    es = {"float32": 4, "float16": 2, "bfloat16": 2}[w.dtype]
+    if name == "rmsnorm":  # the column sum writes dweight
+        return work["bwd"] - d["hidden"] * es
+    if name == "layernorm":  # the column sum writes dweight and dbias
+        return work["bwd"] - 2 * d["hidden"] * es
+    if name == "causal_attention":  # dK/dV kernel: S, dP, dV, dK of the five products
+        return work["bwd"] * 4 / 5
+    phase = DOMINANT[name][0]
+    return work[phase]
+
+
+def kernel_times(name: str, fwd, bwd_call, setup_bwd, state, flush, steps: int) -> dict:
+    """Median microseconds of every kernel of the forward and backward entry
+    points, each timed by events the dispatch records (evograd_amd.timing) on a
+    cold cache."""
+    import torch
+
+    from evograd_amd.timing import KernelTimer
+
+    timer = KernelTimer()
+    out = {}
+    try:
+        for phase in ("fwd", "bwd"):
+            for idx, kname in enumerate(KERNELS[name][phase]):
+                samples = []
+                for _ in range(steps):
+                    if phase == "bwd":
+                        setup_bwd()
+                    flush()
+                    timer.arm(idx)
+                    if phase == "fwd":
+                        fwd()
+                    else:
+                        bwd_call(state["saved"])
+                    samples.append(timer.elapsed_ms() * 1e3)
+                out[f"{phase}:{kname}"] = statistics.median(samples)
+        torch.cuda.synchronize()
+    finally:
+        timer.close()
+    return out
+
+
 # ----------------------------------------------------------------- GPU side
 def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     import torch
@@ -144,6 +207,7 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     if autograd_fn is not None:
         ag = summarize(time_regions(autograd_fn, reps=steps, warmup=warmup, flush=flush))
     work = algorithmic_work(name, w, k_heads)
+    kt = kernel_times(name, fwd, bwd_call, setup_bwd, state, flush, steps)
     sf, sb, sfull = summarize(fwd_ms), summarize(bwd_ms), summarize(full_ms)
     out = {
         "config": {"dims": w.dims, "dtype": w.dtype, **({"k_heads": k_heads} if k_heads else {})},
@@ -155,7 +219,20 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
         "autograd_full_us": ag["median_ms"] * 1e3 if ag else None,
         "saved": {k: v for k, v in report.items() if k != "saved_tensors"},
         "saved_tensors": report["saved_tensors"],
+        "kernels_us": kt,
     }
+    phase, idx = DOMINANT[name]
+    kname = KERNELS[name][phase][idx]
+    k_us = kt[f"{phase}:{kname}"]
+    k_work = dominant_work(name, w, work)
+    if work["unit"] == "bytes":
+        k_rate = k_work / (k_us * 1e-6) / 1e9
+        out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "bytes": k_work,
+                                  "achieved_gbs": k_rate, "frac": k_rate / HBM_PEAK_GBS}
+    else:
+        k_rate = k_work / (k_us * 1e-6) / 1e12
+        out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "flops": k_work,
+                                  "achieved_tflops": k_rate, "frac": k_rate / BF16_PEAK_TFLOPS}
     mem_inputs = sum(values[n].numel() * values[n].element_size()
                      for n in op.memory_input_names() if n in values and torch.is_tensor(values[n]))
     out["saved"]["ratio_to_memory_inputs"] = (report["logical_saved_bytes"] / mem_inputs
@@ -381,10 +458,11 @@ def main() -> int:
     head = results[HEADLINE]
     w = head["config"]
     dims = w["dims"]
-    # Dominant kernel of the headline step: the RMSNorm backward launch
-    # (rmsnorm_bwd_kernel + its fixed-order column sum), timed as one region.
-    bwd_bytes = head["algorithmic_bytes"]["bwd"]
-    achieved = bwd_bytes / (head["bwd_us"] * 1e-6) / 1e9
+    # Dominant kernel of the headline step: the RMSNorm backward ring kernel
+    # (norm_bwd_ring: reads dy, x, rstd, weight; writes dx and the partial rows),
+    # its duration from events the dispatch records.
+    dk = head["dominant_kernel"]
+    achieved = dk["achieved_gbs"]
     line = {
         "metric": METRIC,
         "value": round(head["full_us"], 2),
@@ -406,7 +484,9 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "rmsnorm backward (rmsnorm_bwd_kernel + colsum_kernel)",
+            "kernel": dk["name"],
+            "kernel_us": round(dk["us"], 2),
+            "algorithmic_bytes": dk["bytes"],
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -418,7 +498,7 @@ def main() -> int:
         "cpu_model": cpu_model(),
         "ops": results,
     }
-    traffic = load_traffic("rmsnorm_bwd")
+    traffic = load_traffic("norm_bwd_ring")
     if traffic is not None:
         line["roofline"]["traffic"] = traffic.get("hbm_bytes_per_launch")
         line["roofline"]["traffic_source"] = "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"

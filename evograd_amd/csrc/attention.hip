@@ -34,12 +34,13 @@
 //               V tiles; online softmax in the log2 domain, the running max
 //               refreshed only when it grows by more than 2^8 (exact: the
 //               reference point cancels in o = sum / l); S^T = K Q^T, O^T += V^T P^T.
-//   attn_delta: delta = rowsum(do * o).
+//   attn_dq:    (runs first) workgroup = 4 waves x 32 query rows; also computes
+//               delta = rowsum(do * o) for its rows into the workspace;
+//               double-buffered 64-key K, V tiles; S^T = K Q^T, dP^T = V dO^T,
+//               dQ^T += K^T dS^T.
 //   attn_dkdv:  workgroup = NW waves x 32 keys (K, V in registers); double-buffered
 //               32-row Q and dO tiles from the diagonal down; S = Q K^T,
 //               dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
-//   attn_dq:    workgroup = 4 waves x 32 query rows; double-buffered 64-key K, V
-//               tiles; S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
 // The dQ pass recomputes S and dP (7 products executed where the causal
 // FLOP convention counts 5) so that no atomics are needed.
 //
@@ -89,6 +90,24 @@ __device__ __forceinline__ typename MM<T>::v8 pack8(const f32x16& c, int off) {
   typename MM<T>::v8 r;
   __builtin_memcpy(&r, &u, 16);
   return r;
+}
+
+// The two 16-bit values of a packed word, widened to fp32 (element 0 is bits 0..15).
+template <typename T> __device__ __forceinline__ float half_lo(uint32_t u);
+template <typename T> __device__ __forceinline__ float half_hi(uint32_t u);
+template <> __device__ __forceinline__ float half_lo<bf16_t>(uint32_t u) { return __uint_as_float(u << 16); }
+template <> __device__ __forceinline__ float half_hi<bf16_t>(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+template <> __device__ __forceinline__ float half_lo<f16_t>(uint32_t u) {
+  const uint16_t b = (uint16_t)(u & 0xffffu);
+  f16_t h;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+template <> __device__ __forceinline__ float half_hi<f16_t>(uint32_t u) {
+  const uint16_t b = (uint16_t)(u >> 16);
+  f16_t h;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
 }
 
 // Writes the rows of a transposed 32 x 32 result (lane = row of the output, its
@@ -315,30 +334,6 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
   }
 }
 
-// ------------------------------------------------------------ delta = do.o
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_delta_kernel(const uint16_t* __restrict__ dout,
-                                                         const uint16_t* __restrict__ o,
-                                                         float* __restrict__ delta,
-                                                         int64_t nrows) {
-  // D/8 lanes per row, 16-byte loads.
-  constexpr int LPR = D / 8;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gid / LPR;
-  const int sub = (int)(gid % LPR);
-  float s = 0.f;
-  if (row < nrows) {
-    float a[8], b[8];
-    load_f32<T, 8>(reinterpret_cast<const T*>(dout) + row * D + sub * 8, a);
-    load_f32<T, 8>(reinterpret_cast<const T*>(o) + row * D + sub * 8, b);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += a[i] * b[i];
-  }
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (row < nrows && sub == 0) delta[row] = s;
-}
-
 // ------------------------------------------------------------ dK, dV
 template <typename T, int D, int NW, int BQ>
 __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
@@ -478,8 +473,8 @@ template <typename T, int D, int NW>
 __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dq,
-    int S, float scale, float scale_log2, int nqb, int BH) {
+    const uint16_t* __restrict__ o, const float* __restrict__ lse, float* __restrict__ delta,
+    uint16_t* __restrict__ dq, int S, float scale, float scale_log2, int nqb, int BH) {
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
@@ -497,14 +492,30 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
   const int qrow = q0 + 32 * w + l32;
   const int qrc = qrow < S ? qrow : S - 1;
   v8 qf[KSTEPS], df[KSTEPS];
+  // delta = rowsum(do * o) for this row: the lane pair (l, l + 32) holds the
+  // row's D columns between them; summed in a fixed order and written for the
+  // dK/dV kernel, which runs after this one.
+  float dsum = 0.f;
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) {
-    qf[kk] = *reinterpret_cast<const v8*>(q + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
-    df[kk] = *reinterpret_cast<const v8*>(dout + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
+    const int64_t off = base + (int64_t)qrc * D + kk * 16 + 8 * hh;
+    qf[kk] = *reinterpret_cast<const v8*>(q + off);
+    df[kk] = *reinterpret_cast<const v8*>(dout + off);
+    const uint4 ou = *reinterpret_cast<const uint4*>(o + off);
+    uint4 du;
+    __builtin_memcpy(&du, &df[kk], 16);
+    const uint32_t ow[4] = {ou.x, ou.y, ou.z, ou.w}, dw[4] = {du.x, du.y, du.z, du.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dsum += half_lo<T>(dw[e]) * half_lo<T>(ow[e]);
+      dsum += half_hi<T>(dw[e]) * half_hi<T>(ow[e]);
+    }
   }
-  const float lv = lse[(int64_t)bh * S + qrc], ev = delta[(int64_t)bh * S + qrc];
+  dsum += __shfl_xor(dsum, 32, 64);
+  const float lv = lse[(int64_t)bh * S + qrc];
   const float l2 = qrow < S ? lv * kLog2e : INFINITY;
-  const float dl = qrow < S ? ev : 0.f;
+  const float dl = qrow < S ? dsum : 0.f;
+  if (qrow < S && hh == 0) delta[(int64_t)bh * S + qrow] = dsum;
 
   f32x16 acc[DT];
 #pragma unroll
@@ -599,7 +610,7 @@ int attn_fwd_launch(const void* q, const void* k, const void* v, void* o, float*
                     int64_t S, float scale, hipStream_t st) {
   constexpr int NW = kFwdWaves;
   const int nqb = (int)((S + 32 * NW - 1) / (32 * NW));
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NW>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
+  EG_LAUNCH((attn_fwd_kernel<T, D, NW>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
                      (int)S, scale * kLog2e, nqb, (int)BH);
   return check_launch("eg_attn_fwd");
@@ -609,25 +620,21 @@ template <typename T, int D>
 int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* v, const void* o,
                     const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t BH,
                     int64_t S, float scale, hipStream_t st) {
-  const int64_t nrows = BH * S;
-  const int64_t threads = nrows * (D / 8);
-  hipLaunchKernelGGL((attn_delta_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256),
-                     0, st, (const uint16_t*)dout, (const uint16_t*)o, delta, nrows);
-  if (int rc = check_launch("eg_attn_bwd(delta)")) return rc;
-  constexpr int NK = dkdv_waves<D>();
-  const int nkb = (int)((S + 32 * NK - 1) / (32 * NK));
-  hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, kDkdvRows>), dim3(grid_for(BH, nkb)), dim3(NK * 64),
-                     0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                     (const uint16_t*)dout, lse, delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale,
-                     scale * kLog2e, (int)BH);
-  if (int rc = check_launch("eg_attn_bwd(dkdv)")) return rc;
+  // dQ first: it also computes delta = rowsum(do * o) for its rows, which the
+  // dK/dV kernel reads.
   constexpr int NQ = kDqWaves;
   const int nqb = (int)((S + 32 * NQ - 1) / (32 * NQ));
-  hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ>), dim3(grid_for(BH, nqb)), dim3(NQ * 64), 0, st,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                     (const uint16_t*)dout, lse, delta, (uint16_t*)dq, (int)S, scale,
-                     scale * kLog2e, nqb, (int)BH);
-  return check_launch("eg_attn_bwd(dq)");
+  EG_LAUNCH((attn_dq_kernel<T, D, NQ>), dim3(grid_for(BH, nqb)), dim3(NQ * 64), 0, st,
+            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
+            (const uint16_t*)o, lse, delta, (uint16_t*)dq, (int)S, scale, scale * kLog2e, nqb,
+            (int)BH);
+  if (int rc = check_launch("eg_attn_bwd(dq)")) return rc;
+  constexpr int NK = dkdv_waves<D>();
+  const int nkb = (int)((S + 32 * NK - 1) / (32 * NK));
+  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows>), dim3(grid_for(BH, nkb)), dim3(NK * 64), 0, st,
+            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout, lse,
+            delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale, scale * kLog2e, (int)BH);
+  return check_launch("eg_attn_bwd(dkdv)");
 }
 
 // Explicit instantiations: hip-clang leaves some implicitly instantiated kernel
@@ -637,14 +644,12 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
   template __global__ void attn_fwd_kernel<T, D, kFwdWaves>(                                 \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, float, int,   \
       int);                                                                                  \
-  template __global__ void attn_delta_kernel<T, D>(const uint16_t*, const uint16_t*, float*,   \
-                                                   int64_t);                                 \
   template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows>(               \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
       const float*, uint16_t*, uint16_t*, int, float, float, int);                             \
   template __global__ void attn_dq_kernel<T, D, kDqWaves>(                                   \
-      const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
-      const float*, uint16_t*, int, float, float, int, int);
+      const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,     \
+      const float*, float*, uint16_t*, int, float, float, int, int);
 EG_ATTN_INSTANTIATE(bf16_t, 128)
 EG_ATTN_INSTANTIATE(bf16_t, 64)
 EG_ATTN_INSTANTIATE(f16_t, 128)

@@ -7,6 +7,28 @@ namespace eg {
 
 static thread_local char g_error[1024] = "";
 
+// Kernel-timing hook: eg_time_kernel arms the next entry-point call on this
+// thread; that call's `index`-th kernel launch records `start` and `stop`.
+struct TimingArm {
+  hipEvent_t start = nullptr, stop = nullptr;
+  int index = 0;
+  int next = 0;
+  bool pending = false;
+  bool active = false;
+};
+static thread_local TimingArm g_arm;
+
+bool timed_launch(hipEvent_t* start, hipEvent_t* stop) {
+  if (!g_arm.active) return false;
+  const bool hit = g_arm.next == g_arm.index;
+  ++g_arm.next;
+  if (!hit) return false;
+  *start = g_arm.start;
+  *stop = g_arm.stop;
+  g_arm.active = false;
+  return true;
+}
+
 void set_error(const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -14,7 +36,12 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
-void clear_error() { g_error[0] = '\0'; }
+void clear_error() {
+  g_error[0] = '\0';
+  g_arm.active = g_arm.pending;
+  g_arm.pending = false;
+  g_arm.next = 0;
+}
 
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
@@ -36,8 +63,7 @@ int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what) {
   if (!p) { set_error("%s: null pointer", what); return 1; }
   size_t blocks = (bytes + 255) / 256;
   if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(zero_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                     (unsigned char*)p, bytes);
+  EG_LAUNCH(zero_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (unsigned char*)p, bytes);
   return check_launch(what);
 }
 
@@ -60,3 +86,16 @@ int device_cus() {
 extern "C" int eg_abi_version(void) { return 1; }
 
 extern "C" const char* eg_last_error(void) { return eg::g_error; }
+
+extern "C" int eg_time_kernel(void* start_event, void* stop_event, int index) {
+  if (!start_event || !stop_event || index < 0) {
+    eg::set_error("eg_time_kernel: null event or negative index");
+    return 1;
+  }
+  eg::g_arm.start = reinterpret_cast<hipEvent_t>(start_event);
+  eg::g_arm.stop = reinterpret_cast<hipEvent_t>(stop_event);
+  eg::g_arm.index = index;
+  eg::g_arm.pending = true;
+  eg::g_arm.active = false;
+  return 0;
+}

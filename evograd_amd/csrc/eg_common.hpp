@@ -5,6 +5,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdarg.h>
@@ -17,6 +18,8 @@ constexpr int kWave = 64;  // CDNA wavefront width
 
 // ------------------------------------------------------------------ errors
 void set_error(const char* fmt, ...);
+// Called first by every entry point: clears the error slot and starts a new
+// call for the kernel-timing hook (eg_time_kernel).
 void clear_error();
 // Turns a failed launch into an error return; reads (and clears) the HIP
 // runtime's sticky launch error.
@@ -200,6 +203,24 @@ __device__ __forceinline__ void block_reduce2(float& a, float& b, float* lds) {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------ launching
+// True when this launch is the one eg_time_kernel armed for the current call;
+// then *start / *stop are the events to record around it.
+bool timed_launch(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel is launched through EG_LAUNCH: a plain launch, or, for the launch
+// armed by eg_time_kernel, hipExtLaunchKernelGGL with the caller's events, which
+// the dispatch itself records at the kernel's start and end.
+#define EG_LAUNCH(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                              \
+  do {                                                                                \
+    hipEvent_t eg_t0_ = nullptr, eg_t1_ = nullptr;                                    \
+    if (::eg::timed_launch(&eg_t0_, &eg_t1_))                                         \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, eg_t0_, eg_t1_, 0,     \
+                            __VA_ARGS__);                                             \
+    else                                                                              \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);            \
+  } while (0)
 
 // Zeroes `bytes` bytes with a small kernel (no hipMemsetAsync, so the call is
 // safe inside a captured graph). Returns 0 or an error code.

@@ -425,7 +425,7 @@ template <typename T>
 int launch_colsum(const float* p0, const float* p1, T* o0, T* o1, int nparams, int G,
                   int hidden, hipStream_t st, const char* what) {
   const int quads = (hidden + 3) / 4;
-  hipLaunchKernelGGL((colsum_kernel<T>), dim3((unsigned)((quads + 3) / 4), (unsigned)nparams),
+  EG_LAUNCH((colsum_kernel<T>), dim3((unsigned)((quads + 3) / 4), (unsigned)nparams),
                      dim3(256), 0, st, p0, p1, o0, o1, G, hidden);
   return check_launch(what);
 }
@@ -437,7 +437,7 @@ struct FwdRing {
   hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
     const int64_t G = ring_blocks(rows, kFwdBlocks, BLOCK);
-    hipLaunchKernelGGL((norm_fwd_ring<T, VEC, ITEMS, BLOCK, ring_depth<ITEMS>(), LN>),
+    EG_LAUNCH((norm_fwd_ring<T, VEC, ITEMS, BLOCK, ring_depth<ITEMS>(), LN>),
                        dim3((unsigned)G), dim3(BLOCK), 0, st, x, w, b, y, mean, rstd, rows,
                        hidden, eps);
     return true;
@@ -453,7 +453,7 @@ struct BwdRing {
     constexpr int D = LN ? (ring_depth<ITEMS>() > 1 ? ring_depth<ITEMS>() / 2 : 1)
                          : ring_depth<ITEMS>();
     const int64_t G = ring_blocks(rows, LN ? kLnBwdBlocks : kRmsBwdBlocks, BLOCK);
-    hipLaunchKernelGGL((norm_bwd_ring<T, VEC, ITEMS, BLOCK, D, LN>), dim3((unsigned)G),
+    EG_LAUNCH((norm_bwd_ring<T, VEC, ITEMS, BLOCK, D, LN>), dim3((unsigned)G),
                        dim3(BLOCK), 0, st, dy, x, w, mean, rstd, dx, pw, pb, rows, hidden);
     return true;
   }
@@ -535,10 +535,10 @@ extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float*
         (wave_items == 1 || wave_items == 2 || wave_items == 4 || wave_items == 8)) {
       const unsigned grid = (unsigned)((rows + 3) / 4);
       switch (wave_items) {
-        case 1: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
-        case 2: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
-        case 4: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
-        default: hipLaunchKernelGGL((rmsnorm_fwd_wave<T, V, 8>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        case 1: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        case 2: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        case 4: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        default: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 8>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
       }
     } else if (vec_ok<T>(h, {x, weight, y})) {
       FwdRing<T, V, false> f{xp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};

@@ -93,7 +93,7 @@ int launch_rope(const void* q, const void* k, void* qo, void* ko, const void* co
     set_error("eg_rope: grid too large (batch*groups=%lld)", (long long)gy);
     return 1;
   }
-  hipLaunchKernelGGL((rope_kernel<T, TT, VEC, VEC * sizeof(T) == 16>), dim3((unsigned)gx, (unsigned)gy), dim3(kRopeBlock),
+  EG_LAUNCH((rope_kernel<T, TT, VEC, VEC * sizeof(T) == 16>), dim3((unsigned)gx, (unsigned)gy), dim3(kRopeBlock),
                      0, st, (const T*)q, (const T*)k, (T*)qo, (T*)ko, (const TT*)cosv,
                      (const TT*)sinv, (int)hq, (int)hk, (int)tokens, (int)head_dim, hpg, gq, gk,
                      sgn);

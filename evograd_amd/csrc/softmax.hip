@@ -170,7 +170,7 @@ template <typename T, int VEC>
 struct FwdLaunch {
   const T* x; T* y; int64_t rows; int cols; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((softmax_fwd_reg<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+    EG_LAUNCH((softmax_fwd_reg<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
                        dim3(BLOCK), 0, st, x, y, cols);
     return true;
   }
@@ -180,7 +180,7 @@ template <typename T, int VEC>
 struct BwdLaunch {
   const T* y; const T* dy; T* dx; int64_t rows; int cols; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
-    hipLaunchKernelGGL((softmax_bwd_reg<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+    EG_LAUNCH((softmax_bwd_reg<T, VEC, ITEMS, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
                        dim3(BLOCK), 0, st, y, dy, dx, cols);
     return true;
   }
@@ -190,7 +190,7 @@ template <typename T, int VEC>
 void softmax_fwd_vec(const T* x, T* y, int64_t rows, int cols, hipStream_t st) {
   FwdLaunch<T, VEC> l{x, y, rows, cols, st};
   if (!pick_row_config((cols + VEC - 1) / VEC, l))
-    hipLaunchKernelGGL((softmax_fwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
+    EG_LAUNCH((softmax_fwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
                        st, x, y, cols);
 }
 
@@ -198,7 +198,7 @@ template <typename T, int VEC>
 void softmax_bwd_vec(const T* y, const T* dy, T* dx, int64_t rows, int cols, hipStream_t st) {
   BwdLaunch<T, VEC> l{y, dy, dx, rows, cols, st};
   if (!pick_row_config((cols + VEC - 1) / VEC, l))
-    hipLaunchKernelGGL((softmax_bwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
+    EG_LAUNCH((softmax_bwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
                        st, y, dy, dx, cols);
 }
 

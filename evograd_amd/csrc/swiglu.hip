@@ -118,11 +118,11 @@ extern "C" int eg_swiglu_fwd(const void* a, const void* b, void* c, int64_t n, i
     constexpr int V = 16 / sizeof(T);
     if (n % V == 0 && aligned16(a) && aligned16(b) && aligned16(c)) {
       const int64_t np = n / V;
-      hipLaunchKernelGGL((swiglu_fwd_kernel<T, V, kUnrollFwd, true>),
+      EG_LAUNCH((swiglu_fwd_kernel<T, V, kUnrollFwd, true>),
                          dim3((unsigned)grid_for(np, kUnrollFwd)), dim3(kSwigluBlock), 0, st, (const T*)a,
                          (const T*)b, (T*)c, np);
     } else {
-      hipLaunchKernelGGL((swiglu_fwd_kernel<T, 1, kUnrollScalar, false>),
+      EG_LAUNCH((swiglu_fwd_kernel<T, 1, kUnrollScalar, false>),
                          dim3((unsigned)grid_for(n, kUnrollScalar)), dim3(kSwigluBlock), 0, st,
                          (const T*)a, (const T*)b, (T*)c, n);
     }
@@ -145,11 +145,11 @@ extern "C" int eg_swiglu_bwd(const void* dc, const void* a, const void* b, void*
     if (n % V == 0 && aligned16(dc) && aligned16(a) && aligned16(b) && aligned16(da) &&
         aligned16(db)) {
       const int64_t np = n / V;
-      hipLaunchKernelGGL((swiglu_bwd_kernel<T, V, kUnrollBwd, true>),
+      EG_LAUNCH((swiglu_bwd_kernel<T, V, kUnrollBwd, true>),
                          dim3((unsigned)grid_for(np, kUnrollBwd)), dim3(kSwigluBlock), 0, st,
                          (const T*)dc, (const T*)a, (const T*)b, (T*)da, (T*)db, np);
     } else {
-      hipLaunchKernelGGL((swiglu_bwd_kernel<T, 1, kUnrollScalar, false>),
+      EG_LAUNCH((swiglu_bwd_kernel<T, 1, kUnrollScalar, false>),
                          dim3((unsigned)grid_for(n, kUnrollScalar)), dim3(kSwigluBlock), 0, st,
                          (const T*)dc, (const T*)a, (const T*)b, (T*)da, (T*)db, n);
     }

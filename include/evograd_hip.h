@@ -46,6 +46,16 @@ int eg_abi_version(void);
 /* Description of the last failure on the calling thread ("" if none). */
 const char* eg_last_error(void);
 
+/* Measurement hook; no counterpart in the reference (its harness times with
+ * torch.cuda.Event around whole calls, src/evograd/bench/harness.py:173-213).
+ * Arms the next entry-point call on the calling thread: its `index`-th kernel
+ * launch (0-based, in launch order) is made with hipExtLaunchKernelGGL so the
+ * dispatch records `start_event` / `stop_event` (hipEvent_t, created with
+ * timing) at that kernel's start and end. The arm is consumed by that one call
+ * whether or not it reaches the index. For callers that time one kernel of a
+ * multi-kernel entry point (bench.py); results are unchanged. */
+int eg_time_kernel(void* start_event, void* stop_event, int index);
+
 /* ---------------------------------------------------------------- softmax
  * Replaces softmax_forward_ref (src/evograd/ops/level1/softmax/forward_ref.py:6-7):
  *   y = softmax(x.float(), dim=-1).to(x.dtype), x and y [rows, cols].
@@ -139,8 +149,8 @@ int eg_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
                 int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float scale,
                 int dtype, void* stream);
 
-/* Bytes of workspace eg_attn_bwd needs (delta = rowsum(do * o) fp32 and a
- * partial-dq accumulator). */
+/* Bytes of workspace eg_attn_bwd needs: delta = rowsum(do * o), fp32 [batch,
+ * heads, seq]. */
 size_t eg_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t seq,
                                int64_t head_dim);
 
