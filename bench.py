@@ -40,7 +40,8 @@ METRIC = "fwd+bwd step latency (us) + % HBM/MFMA roofline per op; saved bytes vs
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
-ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention")
+ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
+           "fused_add_rms_norm")
 
 
 def log(msg: str) -> None:
@@ -69,6 +70,14 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
     if name == "swiglu":
         n = d["rows"] * d["cols"] * es
         return {"unit": "bytes", "fwd": 3 * n, "bwd": 5 * n}
+    if name == "fused_add_rms_norm":
+        # fwd reads x, r, weight and writes out, rstd; bwd reads dout and the
+        # saved x, r, weight, rstd and writes the one gradient through s (returned
+        # as dx and dr) and dweight.
+        R, C = d["rows"], d["cols"]
+        n = R * C * es
+        return {"unit": "bytes", "fwd": 3 * n + C * es + 4 * R,
+                "bwd": 4 * n + 4 * R + 2 * C * es}
     if name == "rope":
         B, H, T, D = d["B"], d["n_heads"], d["T"], d["head_dim"]
         xb = B * (H + extra_k_heads) * T * D * es
@@ -90,12 +99,14 @@ KERNELS = {
     "rope": {"fwd": ["rope_kernel"], "bwd": ["rope_kernel"]},
     "causal_attention": {"fwd": ["attn_fwd_kernel"],
                          "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
+    "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_kernel"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.
 DOMINANT = {
     "softmax": ("bwd", 0), "rmsnorm": ("bwd", 0), "layernorm": ("bwd", 0),
     "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
+    "fused_add_rms_norm": ("bwd", 0),
 }
 
 
@@ -105,6 +116,8 @@ def dominant_work(name: str, w, work: dict) -> float:
     es = {"float32": 4, "float16": 2, "bfloat16": 2}[w.dtype]
     if name == "rmsnorm":  # the column sum writes dweight
         return work["bwd"] - d["hidden"] * es
+    if name == "fused_add_rms_norm":
+        return work["bwd"] - d["cols"] * es
     if name == "layernorm":  # the column sum writes dweight and dbias
         return work["bwd"] - 2 * d["hidden"] * es
     if name == "causal_attention":  # dK/dV kernel: S, dP, dV, dK of the five products
@@ -269,7 +282,7 @@ def cpu_baseline(name: str) -> dict:
     op = decls.get_op(name)
     w = op.benchmark[0]
     d = dict(w.dims)
-    if name in ("softmax", "rmsnorm", "layernorm", "swiglu"):
+    if name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm"):
         full_rows = d["rows"]
         d["rows"] = max(1, full_rows // 8)
         scale = full_rows / d["rows"]

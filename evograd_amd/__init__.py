@@ -5,7 +5,8 @@ Layout:
 * ``csrc/``     HIP sources of libevograd_hip.so (C ABI in include/evograd_hip.h)
 * ``_lib``      ctypes binding of that library (no CPU fallback)
 * ``opdecl``    the torch-free declaration contract (Active, Inactive, Workload, OpDecl)
-* ``decls``     declarations of softmax, rmsnorm, layernorm, swiglu, rope, causal_attention
+* ``decls``     declarations of softmax, rmsnorm, layernorm, swiglu, rope, causal_attention,
+                fused_add_rms_norm
 * ``pairs``     one module per operator with the reference's
                 ``<op>_forward_with_saved`` / ``<op>_backward_from_saved`` functions
 * ``bind``      ``bind(op, module)`` -> a ``torch.autograd.Function``-backed callable
@@ -21,6 +22,7 @@ PAIR_MODULES = {
     "swiglu": "evograd_amd.pairs.swiglu",
     "rope": "evograd_amd.pairs.rope",
     "causal_attention": "evograd_amd.pairs.attention",
+    "fused_add_rms_norm": "evograd_amd.pairs.fused_add_rms_norm",
 }
 
 

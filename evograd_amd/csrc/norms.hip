@@ -1,4 +1,12 @@
-// RMSNorm and LayerNorm forward/backward for gfx950.
+// RMSNorm, fused residual-add RMSNorm and LayerNorm forward/backward for gfx950.
+//
+// fused_add_rms_norm follows fused_add_rms_norm_forward_ref
+// (src/evograd/ops/level2/fused_add_rms_norm/forward_ref.py:6-16): s = x + r,
+// rstd = rsqrt(mean(s^2) + eps), out = s * rstd * weight; its backward
+// (declared at fused_add_rms_norm/__init__.py:103-106) is RMSNorm's with s in
+// place of x, and dx = dr. Only x, r (the inputs) and rstd are saved: the
+// backward forms s again from x and r, which moves the same number of bytes as
+// reading a saved s while storing no new row-sized tensor.
 //
 // RMSNorm follows rmsnorm_forward_ref (src/evograd/ops/level1/rmsnorm/forward_ref.py:6-21)
 // and the backward rule at src/evograd/ops/level1/rmsnorm/__init__.py:85-86.
@@ -128,14 +136,17 @@ struct SlotSum {
 };
 
 // --------------------------------------------------------------- forward
-template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN>
+// ADD: the normalised row is s = x + r (fused residual add), formed in fp32.
+template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN, bool ADD = false>
 __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
+                                                       const T* __restrict__ r,
                                                        const T* __restrict__ w,
                                                        const T* __restrict__ b,
                                                        T* __restrict__ y,
                                                        float* __restrict__ mean_out,
                                                        float* __restrict__ rstd_out,
                                                        int64_t rows, int hidden, float eps) {
+  static_assert(!(LN && ADD), "the residual add is fused into RMSNorm only");
   __shared__ float slots[2][1][BLOCK / kWave];
   SlotSum<BLOCK, 1> bsum{slots, 0};
   const int64_t G = gridDim.x;
@@ -154,13 +165,16 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
       if (LN) unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(b + col[it]), bv[it]);
     }
   }
-  Pack<T, VEC> xb[DEPTH][ITEMS];
+  Pack<T, VEC> xb[DEPTH][ITEMS], rb[ADD ? DEPTH : 1][ITEMS];
 #pragma unroll
   for (int k = 0; k < DEPTH; ++k) {
     const int64_t row = blockIdx.x + k * G;
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it)
-      if (row < rows && live[it]) xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
+      if (row < rows && live[it]) {
+        xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
+        if (ADD) rb[ADD ? k : 0][it] = ld_raw<T, VEC>(r + row * hidden + col[it]);
+      }
   }
   for (int64_t base = blockIdx.x; base < rows; base += DEPTH * G) {
 #pragma unroll
@@ -172,13 +186,24 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
       for (int it = 0; it < ITEMS; ++it) {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) xv[it][i] = 0.f;
-        if (live[it]) unpack<T, VEC>(xb[k][it], xv[it]);
+        if (live[it]) {
+          unpack<T, VEC>(xb[k][it], xv[it]);
+          if (ADD) {
+            float rv[VEC];
+            unpack<T, VEC>(rb[ADD ? k : 0][it], rv);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) xv[it][i] += rv[i];
+          }
+        }
       }
       const int64_t nrow = row + DEPTH * G;
       if (nrow < rows)
 #pragma unroll
         for (int it = 0; it < ITEMS; ++it)
-          if (live[it]) xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
+          if (live[it]) {
+            xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
+            if (ADD) rb[ADD ? k : 0][it] = ld_raw<T, VEC>(r + nrow * hidden + col[it]);
+          }
       float mean = 0.f;
       if (LN) {
         float s[1] = {0.f};
@@ -220,8 +245,10 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
 }
 
 // RMSNorm forward, one wave per row, for rows of ITEMS x 64 lanes x VEC elements.
-template <typename T, int VEC, int ITEMS>
+// ADD: the normalised row is s = x + r, formed in fp32.
+template <typename T, int VEC, int ITEMS, bool ADD = false>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
+                                                        const T* __restrict__ r,
                                                         const T* __restrict__ w,
                                                         T* __restrict__ y,
                                                         float* __restrict__ rstd_out, int64_t rows,
@@ -231,19 +258,25 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * H;
-  Pack<T, VEC> xp[ITEMS];
+  Pack<T, VEC> xp[ITEMS], rp[ADD ? ITEMS : 1];
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) xp[it] = ld_raw<T, VEC>(xr + (it * kWave + lane) * VEC);
+  for (int it = 0; it < ITEMS; ++it) {
+    xp[it] = ld_raw<T, VEC>(xr + (it * kWave + lane) * VEC);
+    if (ADD) rp[ADD ? it : 0] = ld_raw<T, VEC>(r + row * H + (it * kWave + lane) * VEC);
+  }
+  float sv[ITEMS][VEC];
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      const float v = to_f32(xp[it].v[i]);
+      float v = to_f32(xp[it].v[i]);
+      if (ADD) v += to_f32(rp[ADD ? it : 0].v[i]);
+      sv[it][i] = v;
       ss += v * v;
     }
   ss = wave_reduce(ss, SumOp());
-  const float r = rsqrtf(ss / (float)H + eps);
+  const float rs = rsqrtf(ss / (float)H + eps);
   T* yr = y + row * H;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
@@ -251,21 +284,24 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
     const Pack<T, VEC> wp = *reinterpret_cast<const Pack<T, VEC>*>(w + c);
     float o[VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) o[i] = (to_f32(xp[it].v[i]) * r) * to_f32(wp.v[i]);
+    for (int i = 0; i < VEC; ++i) o[i] = (sv[it][i] * rs) * to_f32(wp.v[i]);
     st_vec<T, VEC>(yr + c, o);
   }
-  if (lane == 0) rstd_out[row] = r;
+  if (lane == 0) rstd_out[row] = rs;
 }
 
 // -------------------------------------------------------------- backward
 // RMSNorm:   xhat = x * rstd, g = dy * w, dx = (g - xhat * mean(g * xhat)) * rstd
 // LayerNorm: xhat = (x - mean) * rstd, dx = rstd * (g - mean(g) - xhat * mean(g * xhat))
 // dweight += dy * xhat, dbias += dy (per thread, per owned column).
-template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN>
+// ADD: the normalised row was s = x + r; it is formed again here from the inputs.
+template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN, bool ADD = false>
 __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
-    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ res,
+    const T* __restrict__ w,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
     float* __restrict__ partial_w, float* __restrict__ partial_b, int64_t rows, int hidden) {
+  static_assert(!(LN && ADD), "the residual add is fused into RMSNorm only");
   constexpr int NS = LN ? 2 : 1;
   __shared__ float slots[2][NS][BLOCK / kWave];
   SlotSum<BLOCK, NS> bsum{slots, 0};
@@ -282,7 +318,7 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
     for (int i = 0; i < VEC; ++i) { wv[it][i] = 0.f; aw[it][i] = 0.f; ab[it][i] = 0.f; }
     if (live[it]) unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(w + col[it]), wv[it]);
   }
-  Pack<T, VEC> xb[DEPTH][ITEMS], gb[DEPTH][ITEMS];
+  Pack<T, VEC> xb[DEPTH][ITEMS], gb[DEPTH][ITEMS], resb[ADD ? DEPTH : 1][ITEMS];
   float rb[DEPTH], mb[DEPTH];
 #pragma unroll
   for (int k = 0; k < DEPTH; ++k) {
@@ -295,6 +331,7 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
         if (live[it]) {
           xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
           gb[k][it] = ld_raw<T, VEC>(dy + row * hidden + col[it]);
+          if (ADD) resb[ADD ? k : 0][it] = ld_raw<T, VEC>(res + row * hidden + col[it]);
         }
       rb[k] = rstd[row];
       if (LN) mb[k] = mean[row];
@@ -315,7 +352,16 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
         float xv[VEC], gv[VEC];
 #pragma unroll
         for (int i = 0; i < VEC; ++i) { xv[i] = 0.f; gv[i] = 0.f; }
-        if (live[it]) { unpack<T, VEC>(xb[k][it], xv); unpack<T, VEC>(gb[k][it], gv); }
+        if (live[it]) {
+          unpack<T, VEC>(xb[k][it], xv);
+          unpack<T, VEC>(gb[k][it], gv);
+          if (ADD) {
+            float av[VEC];
+            unpack<T, VEC>(resb[ADD ? k : 0][it], av);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) xv[i] += av[i];
+          }
+        }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
           // Padding columns (dy = 0 there) must also give xhat = 0 for LayerNorm.
@@ -337,6 +383,7 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
           if (live[it]) {
             xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
             gb[k][it] = ld_raw<T, VEC>(dy + nrow * hidden + col[it]);
+            if (ADD) resb[ADD ? k : 0][it] = ld_raw<T, VEC>(res + nrow * hidden + col[it]);
           }
         rb[k] = rstd[nrow];
         if (LN) mb[k] = mean[nrow];
@@ -431,30 +478,29 @@ int launch_colsum(const float* p0, const float* p1, T* o0, T* o1, int nparams, i
 }
 
 // ------------------------------------------------------------- dispatch
-template <typename T, int VEC, bool LN>
+template <typename T, int VEC, bool LN, bool ADD = false>
 struct FwdRing {
-  const T *x, *w, *b; T* y; float *mean, *rstd; int64_t rows; int hidden; float eps;
+  const T *x, *r, *w, *b; T* y; float *mean, *rstd; int64_t rows; int hidden; float eps;
   hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
     const int64_t G = ring_blocks(rows, kFwdBlocks, BLOCK);
-    EG_LAUNCH((norm_fwd_ring<T, VEC, ITEMS, BLOCK, ring_depth<ITEMS>(), LN>),
-                       dim3((unsigned)G), dim3(BLOCK), 0, st, x, w, b, y, mean, rstd, rows,
-                       hidden, eps);
+    EG_LAUNCH((norm_fwd_ring<T, VEC, ITEMS, BLOCK, ring_depth<ITEMS>(), LN, ADD>),
+              dim3((unsigned)G), dim3(BLOCK), 0, st, x, r, w, b, y, mean, rstd, rows, hidden, eps);
     return true;
   }
 };
 
-template <typename T, int VEC, bool LN>
+template <typename T, int VEC, bool LN, bool ADD = false>
 struct BwdRing {
-  const T *dy, *x, *w; const float *mean, *rstd; T* dx; float *pw, *pb; int64_t rows;
+  const T *dy, *x, *res, *w; const float *mean, *rstd; T* dx; float *pw, *pb; int64_t rows;
   int hidden; hipStream_t st;
   template <int BLOCK, int ITEMS> bool go() {
     // LayerNorm carries two partial sums per column: half the ring depth.
     constexpr int D = LN ? (ring_depth<ITEMS>() > 1 ? ring_depth<ITEMS>() / 2 : 1)
                          : ring_depth<ITEMS>();
     const int64_t G = ring_blocks(rows, LN ? kLnBwdBlocks : kRmsBwdBlocks, BLOCK);
-    EG_LAUNCH((norm_bwd_ring<T, VEC, ITEMS, BLOCK, D, LN>), dim3((unsigned)G),
-                       dim3(BLOCK), 0, st, dy, x, w, mean, rstd, dx, pw, pb, rows, hidden);
+    EG_LAUNCH((norm_bwd_ring<T, VEC, ITEMS, BLOCK, D, LN, ADD>), dim3((unsigned)G), dim3(BLOCK),
+              0, st, dy, x, res, w, mean, rstd, dx, pw, pb, rows, hidden);
     return true;
   }
 };
@@ -514,82 +560,115 @@ extern "C" size_t eg_layernorm_workspace_bytes(int64_t rows, int64_t hidden) {
   return norm_workspace_bytes(rows, hidden, true);
 }
 
-extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd,
-                              int64_t rows, int64_t hidden, float eps, int dtype,
-                              void* stream) {
+// RMSNorm of x (ADD = false) or of x + r (ADD = true); r may be null otherwise.
+template <bool ADD>
+static int rms_fwd_impl(const char* name, const void* x, const void* r, const void* weight,
+                        void* y, float* rstd, int64_t rows, int64_t hidden, float eps, int dtype,
+                        void* stream) {
   clear_error();
-  if (check_norm_dims("eg_rmsnorm_fwd", rows, hidden)) return 1;
+  if (check_norm_dims(name, rows, hidden)) return 1;
   if (rows == 0) return 0;
-  if (!x || !weight || !y || !rstd) { set_error("eg_rmsnorm_fwd: null pointer"); return 1; }
+  if (!x || (ADD && !r) || !weight || !y || !rstd) { set_error("%s: null pointer", name); return 1; }
   hipStream_t st = as_stream(stream);
-  return EG_DISPATCH_FLOAT(dtype, "eg_rmsnorm_fwd", [&] {
+  return EG_DISPATCH_FLOAT(dtype, name, [&] {
     using T = scalar_t;
     constexpr int V = 16 / sizeof(T);
     const int h = (int)hidden;
     const T* xp = (const T*)x;
+    const T* rp = (const T*)r;
     const T* wp = (const T*)weight;
     T* yp = (T*)y;
     bool ok = true;
     const int wave_items = h / (kWave * V);
-    if (vec_ok<T>(h, {x, weight, y}) && h % (kWave * V) == 0 &&
+    const bool vec = vec_ok<T>(h, {x, weight, y}) && (!ADD || aligned16(r));
+    if (vec && h % (kWave * V) == 0 &&
         (wave_items == 1 || wave_items == 2 || wave_items == 4 || wave_items == 8)) {
       const unsigned grid = (unsigned)((rows + 3) / 4);
       switch (wave_items) {
-        case 1: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
-        case 2: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
-        case 4: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
-        default: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 8>), dim3(grid), dim3(256), 0, st, xp, wp, yp, rstd, rows, eps); break;
+        case 1: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 1, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
+        case 2: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 2, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
+        case 4: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 4, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
+        default: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 8, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
       }
-    } else if (vec_ok<T>(h, {x, weight, y})) {
-      FwdRing<T, V, false> f{xp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
+    } else if (vec) {
+      FwdRing<T, V, false, ADD> f{xp, rp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
       ok = pick_ring((h + V - 1) / V, f);
     } else {
-      FwdRing<T, 1, false> f{xp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
+      FwdRing<T, 1, false, ADD> f{xp, rp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
       ok = pick_ring(h, f);
     }
-    if (!ok) { set_error("eg_rmsnorm_fwd: hidden=%d too wide", h); return 1; }
-    return check_launch("eg_rmsnorm_fwd");
+    if (!ok) { set_error("%s: hidden=%d too wide", name, h); return 1; }
+    return check_launch(name);
   });
+}
+
+template <bool ADD>
+static int rms_bwd_impl(const char* name, const void* dy, const void* x, const void* r,
+                        const void* weight, const float* rstd, void* dx, void* dweight,
+                        void* workspace, int64_t rows, int64_t hidden, int dtype, void* stream) {
+  clear_error();
+  if (check_norm_dims(name, rows, hidden)) return 1;
+  if (!dweight) { set_error("%s: null dweight", name); return 1; }
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    // Empty batch: dweight is a sum over no rows.
+    size_t es = dtype == EG_F32 ? 4 : 2;
+    return zero_fill(dweight, (size_t)hidden * es, st, name);
+  }
+  if (!dy || !x || (ADD && !r) || !weight || !rstd || !dx || !workspace) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  return EG_DISPATCH_FLOAT(dtype, name, [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const int h = (int)hidden;
+    float* part = (float*)workspace;
+    const bool vec = vec_ok<T>(h, {dy, x, weight, dx}) && (!ADD || aligned16(r));
+    bool ok;
+    if (vec) {
+      BwdRing<T, V, false, ADD> f{(const T*)dy, (const T*)x, (const T*)r, (const T*)weight, nullptr,
+                                  rstd, (T*)dx, part, nullptr, rows, h, st};
+      ok = pick_ring((h + V - 1) / V, f);
+    } else {
+      BwdRing<T, 1, false, ADD> f{(const T*)dy, (const T*)x, (const T*)r, (const T*)weight, nullptr,
+                                  rstd, (T*)dx, part, nullptr, rows, h, st};
+      ok = pick_ring(h, f);
+    }
+    if (!ok) { set_error("%s: hidden=%d too wide", name, h); return 1; }
+    if (int rc = check_launch(name)) return rc;
+    const int G = (int)bwd_blocks(rows, h, false, vec, (int)sizeof(T));
+    return launch_colsum<T>(part, part, (T*)dweight, (T*)dweight, 1, G, h, st, name);
+  });
+}
+
+extern "C" int eg_rmsnorm_fwd(const void* x, const void* weight, void* y, float* rstd,
+                              int64_t rows, int64_t hidden, float eps, int dtype,
+                              void* stream) {
+  return rms_fwd_impl<false>("eg_rmsnorm_fwd", x, nullptr, weight, y, rstd, rows, hidden, eps,
+                             dtype, stream);
 }
 
 extern "C" int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight,
                               const float* rstd, void* dx, void* dweight, void* workspace,
                               int64_t rows, int64_t hidden, int dtype, void* stream) {
-  clear_error();
-  if (check_norm_dims("eg_rmsnorm_bwd", rows, hidden)) return 1;
-  if (!dweight) { set_error("eg_rmsnorm_bwd: null dweight"); return 1; }
-  hipStream_t st = as_stream(stream);
-  if (rows == 0) {
-    // Empty batch: dweight is a sum over no rows.
-    size_t es = dtype == EG_F32 ? 4 : 2;
-    return zero_fill(dweight, (size_t)hidden * es, st, "eg_rmsnorm_bwd");
-  }
-  if (!dy || !x || !weight || !rstd || !dx || !workspace) {
-    set_error("eg_rmsnorm_bwd: null pointer");
-    return 1;
-  }
-  return EG_DISPATCH_FLOAT(dtype, "eg_rmsnorm_bwd", [&] {
-    using T = scalar_t;
-    constexpr int V = 16 / sizeof(T);
-    const int h = (int)hidden;
-    float* part = (float*)workspace;
-    const bool vec = vec_ok<T>(h, {dy, x, weight, dx});
-    bool ok;
-    if (vec) {
-      BwdRing<T, V, false> f{(const T*)dy, (const T*)x, (const T*)weight, nullptr, rstd, (T*)dx,
-                             part, nullptr, rows, h, st};
-      ok = pick_ring((h + V - 1) / V, f);
-    } else {
-      BwdRing<T, 1, false> f{(const T*)dy, (const T*)x, (const T*)weight, nullptr, rstd, (T*)dx,
-                             part, nullptr, rows, h, st};
-      ok = pick_ring(h, f);
-    }
-    if (!ok) { set_error("eg_rmsnorm_bwd: hidden=%d too wide", h); return 1; }
-    if (int rc = check_launch("eg_rmsnorm_bwd")) return rc;
-    const int G = (int)bwd_blocks(rows, h, false, vec, (int)sizeof(T));
-    return launch_colsum<T>(part, part, (T*)dweight, (T*)dweight, 1, G, h, st,
-                            "eg_rmsnorm_bwd(colsum)");
-  });
+  return rms_bwd_impl<false>("eg_rmsnorm_bwd", dy, x, nullptr, weight, rstd, dx, dweight,
+                             workspace, rows, hidden, dtype, stream);
+}
+
+extern "C" int eg_fused_add_rmsnorm_fwd(const void* x, const void* r, const void* weight,
+                                        void* y, float* rstd, int64_t rows, int64_t hidden,
+                                        float eps, int dtype, void* stream) {
+  return rms_fwd_impl<true>("eg_fused_add_rmsnorm_fwd", x, r, weight, y, rstd, rows, hidden, eps,
+                            dtype, stream);
+}
+
+extern "C" int eg_fused_add_rmsnorm_bwd(const void* dout, const void* x, const void* r,
+                                        const void* weight, const float* rstd, void* ds,
+                                        void* dweight, void* workspace, int64_t rows,
+                                        int64_t hidden, int dtype, void* stream) {
+  return rms_bwd_impl<true>("eg_fused_add_rmsnorm_bwd", dout, x, r, weight, rstd, ds, dweight,
+                            workspace, rows, hidden, dtype, stream);
 }
 
 extern "C" int eg_layernorm_fwd(const void* x, const void* weight, const void* bias, void* y,
@@ -609,10 +688,10 @@ extern "C" int eg_layernorm_fwd(const void* x, const void* weight, const void* b
     const int h = (int)hidden;
     bool ok;
     if (vec_ok<T>(h, {x, weight, bias, y})) {
-      FwdRing<T, V, true> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
+      FwdRing<T, V, true> f{(const T*)x, nullptr, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
       ok = pick_ring((h + V - 1) / V, f);
     } else {
-      FwdRing<T, 1, true> f{(const T*)x, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
+      FwdRing<T, 1, true> f{(const T*)x, nullptr, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
       ok = pick_ring(h, f);
     }
     if (!ok) { set_error("eg_layernorm_fwd: hidden=%d too wide", h); return 1; }
@@ -647,10 +726,10 @@ extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weigh
     float* pb = pw + (int64_t)G * h;
     bool ok;
     if (vec) {
-      BwdRing<T, V, true> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
+      BwdRing<T, V, true> f{(const T*)dy, (const T*)x, nullptr, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
       ok = pick_ring((h + V - 1) / V, f);
     } else {
-      BwdRing<T, 1, true> f{(const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
+      BwdRing<T, 1, true> f{(const T*)dy, (const T*)x, nullptr, (const T*)weight, mean, rstd, (T*)dx, pw, pb, rows, h, st};
       ok = pick_ring(h, f);
     }
     if (!ok) { set_error("eg_layernorm_bwd: hidden=%d too wide", h); return 1; }

@@ -9,6 +9,7 @@ drop-in the reference's harness looks up:
 * layernorm  src/evograd/ops/level1/layernorm/__init__.py:124-171
 * swiglu     src/evograd/ops/level1/swiglu/__init__.py:61-97
 * rope       src/evograd/ops/level1/rope/__init__.py:98-162
+* fused_add_rms_norm  src/evograd/ops/level2/fused_add_rms_norm/__init__.py:76-122
 * causal_attention: the reference has no standalone declaration; its semantics
   are F.scaled_dot_product_attention(q, k, v, is_causal=True) inside
   src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-108. It is
@@ -118,6 +119,49 @@ RMSNORM = declare_op(
     ),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_rmsnorm_inputs",
+)
+
+# ------------------------------------------------------- fused_add_rms_norm
+# Correctness: the reference's standard 2-D shapes (src/evograd/ops/_common.py:18-22)
+# plus ragged/wide rows; benchmark: its Llama-3-8B residual-stream workload at the
+# largest token count of the sweep (rows = 16384 tokens, cols = hidden 4096).
+FUSED_ADD_RMS_NORM = declare_op(
+    name="fused_add_rms_norm",
+    forward="oracle.forward_refs:fused_add_rms_norm_forward_ref",
+    runtime_forward="oracle.forward_refs:fused_add_rms_norm_runtime_ref",
+    dims=("rows", "cols"),
+    args=(
+        Active("x", "[rows, cols]"),
+        Active("r", "[rows, cols]"),
+        Active("weight", "[cols]"),
+        Inactive("eps", default=1e-6),
+    ),
+    output=Active("out", "[rows, cols]"),
+    forward_semantics=(
+        "Set s=x+r, compute rstd=rsqrt(mean(s**2,lastdim)+eps) in fp32, "
+        "and return s*rstd*weight."
+    ),
+    backward_semantics=(
+        "Return dx, dr, dweight. dx and dr are the same gradient through s; "
+        "dweight reduces dout*s*rstd across rows."
+    ),
+    reference_dtype="float32",
+    correctness=(
+        _w2(((8, 64), (17, 128)), ("float32",))
+        + _w2(((32, 256), (64, 512)), ("float16", "bfloat16"))
+        + (
+            Workload(dims=dict(rows=1, cols=4096), dtype="bfloat16"),
+            Workload(dims=dict(rows=17, cols=1000), dtype="bfloat16"),
+            Workload(dims=dict(rows=17, cols=127), dtype="float32"),
+            Workload(dims=dict(rows=1500, cols=1024), dtype="bfloat16"),
+            Workload(dims=dict(rows=300, cols=4096), dtype="bfloat16"),
+        )
+    ),
+    benchmark=(
+        Workload(dims=dict(rows=16384, cols=4096), dtype="bfloat16", label="llama3_8b"),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_fused_add_rms_norm_inputs",
 )
 
 # ---------------------------------------------------------------- layernorm
@@ -253,7 +297,8 @@ CAUSAL_ATTENTION = declare_op(
 )
 
 OPS: dict[str, OpDecl] = {
-    op.name: op for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION)
+    op.name: op
+    for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM)
 }
 
 

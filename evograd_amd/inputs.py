@@ -56,6 +56,20 @@ def make_rmsnorm_inputs(op, workload, device="cuda"):
     return {"x": x, "weight": weight, "eps": float(workload.extra.get("eps", 1e-5)), "dy": dy}
 
 
+def make_fused_add_rms_norm_inputs(op, workload, device="cuda"):
+    """fused_add_rms_norm/__init__.py:55-64: seed rows*100003+cols; x, r, weight, dout
+    ~ N(0,1) in that order; eps 1e-6."""
+    rows, cols = workload.dims["rows"], workload.dims["cols"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100003 + cols)
+    x = torch.randn((rows, cols), device=device, dtype=dt)
+    r = torch.randn((rows, cols), device=device, dtype=dt)
+    weight = torch.randn((cols,), device=device, dtype=dt)
+    dout = torch.randn((rows, cols), device=device, dtype=dt)
+    return {"x": x, "r": r, "weight": weight, "eps": float(workload.extra.get("eps", 1e-6)),
+            "dout": dout}
+
+
 def make_layernorm_inputs(op, workload, device="cuda"):
     """layernorm/__init__.py:16-24: seed rows*100000+hidden; x, weight, bias, dy ~ N(0,1)."""
     rows, hidden = workload.dims["rows"], workload.dims["hidden"]
@@ -130,6 +144,7 @@ RECIPES = {
     "make_softmax_inputs": make_softmax_inputs,
     "make_rmsnorm_inputs": make_rmsnorm_inputs,
     "make_layernorm_inputs": make_layernorm_inputs,
+    "make_fused_add_rms_norm_inputs": make_fused_add_rms_norm_inputs,
     "make_swiglu_inputs": make_swiglu_inputs,
     "make_rope_inputs": make_rope_inputs,
     "make_attention_inputs": make_attention_inputs,

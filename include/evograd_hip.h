@@ -88,6 +88,27 @@ int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const floa
                    void* dx, void* dweight, void* workspace, int64_t rows, int64_t hidden,
                    int dtype, void* stream);
 
+/* ----------------------------------------------------- fused_add_rms_norm
+ * Replaces fused_add_rms_norm_forward_ref
+ * (src/evograd/ops/level2/fused_add_rms_norm/forward_ref.py:6-16):
+ *   s = x + r; rstd = rsqrt(mean(s^2, -1) + eps); out = (s * rstd) * weight
+ * s is formed in fp32 and never stored; x, r, out [rows, hidden] (dtype), weight
+ * [hidden], rstd [rows] fp32 (saved with x and r). */
+int eg_fused_add_rmsnorm_fwd(const void* x, const void* r, const void* weight, void* out,
+                             float* rstd, int64_t rows, int64_t hidden, float eps, int dtype,
+                             void* stream);
+
+/* Replaces the autograd backward declared at
+ * src/evograd/ops/level2/fused_add_rms_norm/__init__.py:103-106: with s = x + r
+ * formed again from the inputs, shat = s * rstd, g = dout * weight,
+ *   ds = (g - shat * mean(g * shat, -1)) * rstd   (= dx = dr, written once to ds)
+ *   dweight = sum_rows(dout * shat)               (two stages, fixed order)
+ * Workspace: eg_rmsnorm_workspace_bytes(rows, hidden). */
+int eg_fused_add_rmsnorm_bwd(const void* dout, const void* x, const void* r,
+                             const void* weight, const float* rstd, void* ds, void* dweight,
+                             void* workspace, int64_t rows, int64_t hidden, int dtype,
+                             void* stream);
+
 /* -------------------------------------------------------------- layernorm
  * Replaces layernorm_forward_ref (src/evograd/ops/level1/layernorm/forward_ref.py:6-23):
  *   mean = mean(x, -1); var = mean((x - mean)^2, -1); rstd = rsqrt(var + eps)

@@ -33,6 +33,25 @@ def rmsnorm_runtime_ref(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5
     return F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
 
 
+def fused_add_rms_norm_forward_ref(x: torch.Tensor, residual: torch.Tensor,
+                                   weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """src/evograd/ops/level2/fused_add_rms_norm/forward_ref.py:6-16: the sum in the
+    input dtype, its mean square in fp32, then (s * rstd) * weight with rstd cast
+    to the sum's dtype."""
+    if x.shape != residual.shape or x.ndim != 2:
+        raise ValueError("x and residual must be equal 2D tensors")
+    summed = x + residual
+    rstd = torch.rsqrt(summed.float().pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (summed * rstd.to(summed.dtype)) * weight
+
+
+def fused_add_rms_norm_runtime_ref(x: torch.Tensor, residual: torch.Tensor,
+                                   weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """src/evograd/ops/level2/fused_add_rms_norm/forward_ref.py:19-34: the add, then
+    the fused F.rms_norm (the eager baseline's spelling)."""
+    return F.rms_norm(x + residual, (x.shape[-1],), weight=weight, eps=eps)
+
+
 def layernorm_forward_ref(x, weight, bias, eps: float = 1e-5):
     """src/evograd/ops/level1/layernorm/forward_ref.py:6-23."""
     if x.ndim != 2:
@@ -105,6 +124,8 @@ FORWARDS = {
     "softmax_forward_ref": softmax_forward_ref,
     "rmsnorm_forward_ref": rmsnorm_forward_ref,
     "rmsnorm_runtime_ref": rmsnorm_runtime_ref,
+    "fused_add_rms_norm_forward_ref": fused_add_rms_norm_forward_ref,
+    "fused_add_rms_norm_runtime_ref": fused_add_rms_norm_runtime_ref,
     "layernorm_forward_ref": layernorm_forward_ref,
     "layernorm_runtime_ref": layernorm_runtime_ref,
     "swiglu_forward_ref": swiglu_forward_ref,

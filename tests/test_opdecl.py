@@ -77,10 +77,16 @@ def test_validation_rejects_bad_declarations():
                    correctness=(Workload(dims={"n": 4}, dtype="float16"),), **base)
 
 
+BASELINE_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention")
+
+
 def test_baseline_workloads_present():
-    labels = {name: [w for w in op.benchmark if w.label == "baseline"]
-              for name, op in decls.OPS.items()}
+    labels = {name: [w for w in decls.get_op(name).benchmark if w.label == "baseline"]
+              for name in BASELINE_OPS}
     assert all(labels.values()), labels
+    # the operators beyond BASELINE.json carry the reference's own timed workload
+    farn = decls.FUSED_ADD_RMS_NORM.benchmark[0]
+    assert farn.dims == {"rows": 16384, "cols": 4096} and farn.dtype == "bfloat16"
     assert decls.RMSNORM.benchmark[0].dims == {"rows": 16384, "hidden": 4096}
     assert decls.RMSNORM.benchmark[0].extra["eps"] == 1e-6
     assert decls.SWIGLU.benchmark[0].dims == {"rows": 16384, "cols": 14336}

@@ -110,6 +110,53 @@ def test_rmsnorm_gradient_fd_and_brute_force_dweight():
     assert torch.allclose(g["dweight"], dw)
 
 
+# ------------------------------------------------------- fused_add_rms_norm
+def test_fused_add_rms_norm_forward_closed_forms():
+    w = torch.tensor([1.0, 2.0, -0.5, 3.0], dtype=torch.float64)
+    x = torch.randn(3, 4, dtype=torch.float64)
+    # r = 0 is RMSNorm of x (pinned above); the sum is symmetric in x and r
+    assert torch.allclose(fr.fused_add_rms_norm_forward_ref(x, torch.zeros_like(x), w, 1e-6),
+                          fr.rmsnorm_forward_ref(x, w, 1e-6))
+    r = torch.randn(3, 4, dtype=torch.float64)
+    assert torch.allclose(fr.fused_add_rms_norm_forward_ref(x, r, w, 1e-6),
+                          fr.fused_add_rms_norm_forward_ref(r, x, w, 1e-6))
+    # s = x + r = 3 everywhere: mean(s^2) = 9, out = 3 w / sqrt(9 + eps)
+    xc = torch.full((2, 4), 1.0, dtype=torch.float64)
+    out = fr.fused_add_rms_norm_forward_ref(xc, 2 * xc, w, eps=7.0)
+    assert torch.allclose(out, (3.0 * w / 4.0).expand(2, 4))
+    # x = -r: s = 0 gives 0 (rstd = 1/sqrt(eps), finite)
+    assert torch.all(fr.fused_add_rms_norm_forward_ref(x, -x, w, 1e-6) == 0)
+
+
+def test_fused_add_rms_norm_rounds_like_the_reference_in_bf16():
+    """In bf16 the reference rounds the sum, then s * bf16(rstd), then * weight."""
+    g = torch.Generator().manual_seed(3)
+    x, r = (torch.randn(4, 64, generator=g).bfloat16() for _ in range(2))
+    w = torch.randn(64, generator=g).bfloat16()
+    s = (x.float() + r.float()).bfloat16()
+    rstd = torch.rsqrt(s.float().pow(2).mean(-1, keepdim=True) + 1e-6).bfloat16()
+    expect = ((s.float() * rstd.float()).bfloat16().float() * w.float()).bfloat16()
+    assert torch.equal(fr.fused_add_rms_norm_forward_ref(x, r, w, 1e-6), expect)
+
+
+def test_fused_add_rms_norm_gradient_fd_dx_equals_dr_and_dweight():
+    op = decls.FUSED_ADD_RMS_NORM
+    inputs = _f64(make_case_inputs(op, Workload(dims=dict(rows=5, cols=24), dtype="float32"),
+                                   "cpu"))
+    _fd_check(op, inputs)
+    _, g = oracle(op, inputs, use_reference_dtype=False)
+    assert torch.equal(g["dx"], g["dr"])
+    s = inputs["x"] + inputs["r"]
+    dw = torch.zeros(24, dtype=torch.float64)
+    for row in range(5):
+        dw += inputs["dout"][row] * s[row] / math.sqrt(float((s[row] ** 2).mean()) + inputs["eps"])
+    assert torch.allclose(g["dweight"], dw)
+    # the gradient through s equals RMSNorm's gradient at x = s
+    rms_in = {"x": s, "weight": inputs["weight"], "eps": inputs["eps"], "dy": inputs["dout"]}
+    _, gr = oracle(decls.RMSNORM, rms_in, use_reference_dtype=False)
+    assert torch.allclose(g["dx"], gr["dx"]) and torch.allclose(g["dweight"], gr["dweight"])
+
+
 # ---------------------------------------------------------------- layernorm
 def test_layernorm_forward_closed_forms():
     x = torch.randn(4, 50, dtype=torch.float64) * 3 + 2
