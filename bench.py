@@ -41,7 +41,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
 ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
-           "fused_add_rms_norm")
+           "fused_add_rms_norm", "causal_attention_gqa")
 
 
 def log(msg: str) -> None:
@@ -83,8 +83,8 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
         xb = B * (H + extra_k_heads) * T * D * es
         tables = 2 * T * D * 4
         return {"unit": "bytes", "fwd": 2 * xb + tables, "bwd": 2 * xb + tables}
-    if name == "causal_attention":
-        B, H, S, D = d["B"], d["H"], d["S"], d["D"]
+    if name in ("causal_attention", "causal_attention_gqa"):
+        B, H, S, D = d["B"], d["H"], d["S"], d["D"]  # FLOPs count query heads
         dense = 2.0 * S * S * D * B * H  # one S x S x D product
         return {"unit": "flops", "fwd": 2 * dense / 2, "bwd": 5 * dense / 2}
     raise KeyError(name)
@@ -100,13 +100,15 @@ KERNELS = {
     "causal_attention": {"fwd": ["attn_fwd_kernel"],
                          "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
     "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_kernel"]},
+    "causal_attention_gqa": {"fwd": ["attn_fwd_kernel"],
+                             "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.
 DOMINANT = {
     "softmax": ("bwd", 0), "rmsnorm": ("bwd", 0), "layernorm": ("bwd", 0),
     "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
-    "fused_add_rms_norm": ("bwd", 0),
+    "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
 }
 
 
@@ -120,7 +122,8 @@ def dominant_work(name: str, w, work: dict) -> float:
         return work["bwd"] - d["cols"] * es
     if name == "layernorm":  # the column sum writes dweight and dbias
         return work["bwd"] - 2 * d["hidden"] * es
-    if name == "causal_attention":  # dK/dV kernel: S, dP, dV, dK of the five products
+    if name in ("causal_attention", "causal_attention_gqa"):
+        # dK/dV kernel: S, dP, dV, dK of the five products
         return work["bwd"] * 4 / 5
     phase = DOMINANT[name][0]
     return work[phase]
@@ -292,6 +295,13 @@ def cpu_baseline(name: str) -> dict:
         d["B"], d["n_heads"] = 1, 8
         scale = full / 8
         sample = f"8 of {full} (batch, head) rows of q and k"
+    elif name == "causal_attention_gqa":
+        # one kv head and its group of query heads
+        full = d["B"] * d["KVH"]
+        d["H"] //= d["KVH"]
+        d["B"], d["KVH"] = 1, 1
+        scale = float(full)
+        sample = f"1 of {full} (batch, kv head) groups of {d['H']} query heads"
     else:
         full = d["B"] * d["H"]
         d["B"], d["H"] = 1, 1

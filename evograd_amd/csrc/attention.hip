@@ -8,8 +8,11 @@
 //   dv = P^T do,  dS = P * (dP - delta) with dP = do v^T,  dq = scale * dS k,
 //   dk = scale * dS^T q.
 //
-// Layout: q, k, v, o, do, dq, dk, dv are [B, H, S, D] row-major (D contiguous);
-// lse and delta are fp32 [B, H, S].
+// Layout: q, o, do, dq are [B, H, S, D] row-major (D contiguous); k, v, dk, dv
+// are [B, Hkv, S, D] with H a multiple of Hkv (grouped-query attention: query
+// head h reads kv head h / (H / Hkv), the repeat_interleave of
+// src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-105 without the
+// copy; Hkv = H is ordinary multi-head attention); lse and delta are fp32 [B, H, S].
 //
 // MFMA: v_mfma_f32_32x32x16_{bf16,f16}. Lane l of a wave holds, for an M x K
 // operand A, row l%32 and k = 8*(l/32) .. +7; for B (K x N), column l%32 and the
@@ -213,27 +216,38 @@ __device__ __forceinline__ void block_coords(int BH, int& bh, int& blk) {
   blk = rest / groups;
 }
 
+// Grouped-query attention: query head `bh_q` (flat over batch x heads) reads key/
+// value head bh_q / group. A virtual head index v (the one block_coords spreads
+// over the XCDs) maps to bh_q = (v % BHkv) * group + v / BHkv, so the `group`
+// query heads that share a kv head have the same v % 8, i.e. the same XCD and L2,
+// whenever BHkv is a multiple of 8. With group = 1 this is the identity.
+__device__ __forceinline__ int query_head(int v, int BHkv, int group) {
+  return (v % BHkv) * group + v / BHkv;
+}
+
 // ------------------------------------------------------------------ forward
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int S,
-    float scale_log2, int nqb, int BH) {
+    float scale_log2, int nqb, int BH, int group) {
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
   __shared__ __align__(16) uint16_t Ks[2][BN * D];
   __shared__ __align__(16) uint16_t Vs[2][BN * D];
 
-  int bh, blk;
-  block_coords(BH, bh, blk);
-  if (bh >= BH) return;
+  int vh, blk;
+  block_coords(BH, vh, blk);
+  if (vh >= BH) return;
+  const int bh = query_head(vh, BH / group, group);
   const int q0 = (nqb - 1 - blk) * BM;  // longest rows first
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
-  const uint16_t* kp = k + base;
-  const uint16_t* vp = v + base;
+  const int64_t kvbase = (int64_t)(bh / group) * S * D;
+  const uint16_t* kp = k + kvbase;
+  const uint16_t* vp = v + kvbase;
 
   const int qrow = q0 + 32 * w + l32;
   const int qrc = qrow < S ? qrow : S - 1;
@@ -340,7 +354,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
-    uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int BH) {
+    uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int BHkv, int group) {
   using v8 = typename MM<T>::v8;
   constexpr int BK = 32 * NW;
   constexpr int KSTEPS = D / 16, DT = D / 32, MT = BQ / 32;
@@ -349,15 +363,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   __shared__ __align__(16) float Ls[2][BQ];
   __shared__ __align__(16) float Es[2][BQ];
 
-  int bh, kb;
-  block_coords(BH, bh, kb);  // kb = 0 (the longest walk) first
-  if (bh >= BH) return;
+  int kvh, kb;
+  block_coords(BHkv, kvh, kb);  // kb = 0 (the longest walk) first
+  if (kvh >= BHkv) return;
   const int k0 = kb * BK;
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
-  const int64_t base = (int64_t)bh * S * D;
-  const float* lsep = lse + (int64_t)bh * S;
-  const float* delp = delta + (int64_t)bh * S;
+  const int64_t base = (int64_t)kvh * S * D;  // k, v, dk, dv
 
   const int key = k0 + 32 * w + l32;
   const int krc = key < S ? key : S - 1;
@@ -373,43 +385,51 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
 
   zero_lds<NW * 64>(Qs, sizeof(Qs));
   zero_lds<NW * 64>(Ds, sizeof(Ds));
+  // The walk: for each query head of the group (in order), the q tiles from the
+  // diagonal block to S. dK and dV accumulate over all of them in registers, so
+  // the kv-head gradient is the group sum without atomics or a second pass.
   const int i_first = k0 / BQ;
-  const int i_end = (S + BQ - 1) / BQ;
+  const int ntq = (S + BQ - 1) / BQ - i_first;
+  const int nsteps = group * ntq;
   const int wave_first_key = k0 + 32 * w;
-  const uint16_t* qp = q + base;
-  const uint16_t* dp_ = dout + base;
   TileLoader<BQ, D, NW> ld;
   ld.init();
+  auto qhead = [&](int step) { return kvh * group + step / ntq; };
+  auto qtile = [&](int step) { return i_first + step % ntq; };
   // lse (as log2) and delta of a tile's rows: wave 0 loads them into registers
   // when the tile is requested and stores them to LDS after its own compute.
   float lreg = INFINITY, ereg = 0.f;
-  auto load_stats = [&](int i) {
+  auto load_stats = [&](int step) {
     if (w == 0 && lane < BQ) {
-      const int row = i * BQ + lane;
+      const int64_t hb = (int64_t)qhead(step) * S;
+      const int row = qtile(step) * BQ + lane;
       const int rc = row < S ? row : S - 1;
-      const float lv = lsep[rc], ev = delp[rc];
+      const float lv = lse[hb + rc], ev = delta[hb + rc];
       lreg = row < S ? lv * kLog2e : INFINITY;
       ereg = row < S ? ev : 0.f;
     }
   };
+  auto load_tiles = [&](int step, int buf) {
+    const int64_t hb = (int64_t)qhead(step) * S * D;
+    ld.load(q + hb, qtile(step) * BQ, S, Qs[buf]);
+    ld.load(dout + hb, qtile(step) * BQ, S, Ds[buf]);
+  };
   __syncthreads();
-  if (i_first < i_end) {
-    ld.load(qp, i_first * BQ, S, Qs[0]);
-    ld.load(dp_, i_first * BQ, S, Ds[0]);
-    load_stats(i_first);
+  if (nsteps > 0) {
+    load_tiles(0, 0);
+    load_stats(0);
     if (w == 0 && lane < BQ) { Ls[0][lane] = lreg; Es[0][lane] = ereg; }
   }
-  for (int i = i_first; i < i_end; ++i) {
+  for (int step = 0; step < nsteps; ++step) {
     wait_loads();
     __syncthreads();
-    const int buf = (i - i_first) & 1;
-    const bool more = i + 1 < i_end;
+    const int buf = step & 1;
+    const bool more = step + 1 < nsteps;
     if (more) {
-      ld.load(qp, (i + 1) * BQ, S, Qs[buf ^ 1]);
-      ld.load(dp_, (i + 1) * BQ, S, Ds[buf ^ 1]);
-      load_stats(i + 1);
+      load_tiles(step + 1, buf ^ 1);
+      load_stats(step + 1);
     }
-    const int qi0 = i * BQ;
+    const int qi0 = qtile(step) * BQ;
     if (qi0 + BQ - 1 >= wave_first_key) {  // some row of the tile sees some key of this wave
       const uint16_t* Qb = Qs[buf];
       const uint16_t* Db = Ds[buf];
@@ -474,20 +494,23 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const uint16_t* __restrict__ o, const float* __restrict__ lse, float* __restrict__ delta,
-    uint16_t* __restrict__ dq, int S, float scale, float scale_log2, int nqb, int BH) {
+    uint16_t* __restrict__ dq, int S, float scale, float scale_log2, int nqb, int BH,
+    int group) {
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
   __shared__ __align__(16) uint16_t Ks[2][BN * D];
   __shared__ __align__(16) uint16_t Vs[2][BN * D];
 
-  int bh, blk;
-  block_coords(BH, bh, blk);
-  if (bh >= BH) return;
+  int vh, blk;
+  block_coords(BH, vh, blk);
+  if (vh >= BH) return;
+  const int bh = query_head(vh, BH / group, group);
   const int q0 = (nqb - 1 - blk) * BM;
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t base = (int64_t)bh * S * D;
+  const int64_t kvbase = (int64_t)(bh / group) * S * D;
 
   const int qrow = q0 + 32 * w + l32;
   const int qrc = qrow < S ? qrow : S - 1;
@@ -523,8 +546,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
   const int kv_end = min(S, q0 + BM);
   const int ntiles = (kv_end + BN - 1) / BN;
   const int wave_first_row = q0 + 32 * w;
-  const uint16_t* kp = k + base;
-  const uint16_t* vp = v + base;
+  const uint16_t* kp = k + kvbase;
+  const uint16_t* vp = v + kvbase;
 
   zero_lds<NW * 64>(Ks, sizeof(Ks));
   zero_lds<NW * 64>(Vs, sizeof(Vs));
@@ -589,8 +612,14 @@ constexpr int kDkdvRows = 32;
 // tile of 64 columns is one 16-byte chunk per lane of 4 waves).
 template <int D> constexpr int dkdv_waves() { return D == 128 ? 8 : 4; }
 
-int check_attn(const char* what, int64_t B, int64_t H, int64_t S, int64_t D, int dtype) {
+int check_attn(const char* what, int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D,
+               int dtype) {
   if (B < 0 || H < 0 || S < 0) { set_error("%s: negative size", what); return 1; }
+  if (H > 0 && (Hkv <= 0 || H % Hkv != 0)) {
+    set_error("%s: heads (%lld) must be a positive multiple of kv_heads (%lld)", what,
+              (long long)H, (long long)Hkv);
+    return 1;
+  }
   if (D != 64 && D != 128) { set_error("%s: head_dim must be 64 or 128, got %lld", what, (long long)D); return 1; }
   if (dtype != EG_BF16 && dtype != EG_F16) { set_error("%s: dtype must be bf16 or fp16", what); return 1; }
   // One (b, h) slice is addressed with 32-bit buffer offsets: S * D * 2 < 2^31.
@@ -607,19 +636,20 @@ inline unsigned grid_for(int64_t BH, int nblocks) {
 
 template <typename T, int D>
 int attn_fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
-                    int64_t S, float scale, hipStream_t st) {
+                    int64_t S, int group, float scale, hipStream_t st) {
   constexpr int NW = kFwdWaves;
   const int nqb = (int)((S + 32 * NW - 1) / (32 * NW));
   EG_LAUNCH((attn_fwd_kernel<T, D, NW>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
-                     (int)S, scale * kLog2e, nqb, (int)BH);
+            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, (int)S,
+            scale * kLog2e, nqb, (int)BH, group);
   return check_launch("eg_attn_fwd");
 }
 
+// BH counts query heads (x batch); the key/value tensors hold BH / group heads.
 template <typename T, int D>
 int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* v, const void* o,
                     const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t BH,
-                    int64_t S, float scale, hipStream_t st) {
+                    int64_t S, int group, float scale, hipStream_t st) {
   // dQ first: it also computes delta = rowsum(do * o) for its rows, which the
   // dK/dV kernel reads.
   constexpr int NQ = kDqWaves;
@@ -627,13 +657,15 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
   EG_LAUNCH((attn_dq_kernel<T, D, NQ>), dim3(grid_for(BH, nqb)), dim3(NQ * 64), 0, st,
             (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
             (const uint16_t*)o, lse, delta, (uint16_t*)dq, (int)S, scale, scale * kLog2e, nqb,
-            (int)BH);
+            (int)BH, group);
   if (int rc = check_launch("eg_attn_bwd(dq)")) return rc;
   constexpr int NK = dkdv_waves<D>();
   const int nkb = (int)((S + 32 * NK - 1) / (32 * NK));
-  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows>), dim3(grid_for(BH, nkb)), dim3(NK * 64), 0, st,
-            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout, lse,
-            delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale, scale * kLog2e, (int)BH);
+  const int64_t BHkv = BH / group;
+  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows>), dim3(grid_for(BHkv, nkb)), dim3(NK * 64), 0,
+            st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
+            lse, delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale, scale * kLog2e, (int)BHkv,
+            group);
   return check_launch("eg_attn_bwd(dkdv)");
 }
 
@@ -643,13 +675,13 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
 #define EG_ATTN_INSTANTIATE(T, D)                                                            \
   template __global__ void attn_fwd_kernel<T, D, kFwdWaves>(                                 \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, float, int,   \
-      int);                                                                                  \
+      int, int);                                                                             \
   template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows>(               \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
-      const float*, uint16_t*, uint16_t*, int, float, float, int);                             \
+      const float*, uint16_t*, uint16_t*, int, float, float, int, int);                        \
   template __global__ void attn_dq_kernel<T, D, kDqWaves>(                                   \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,     \
-      const float*, float*, uint16_t*, int, float, float, int, int);
+      const float*, float*, uint16_t*, int, float, float, int, int, int);
 EG_ATTN_INSTANTIATE(bf16_t, 128)
 EG_ATTN_INSTANTIATE(bf16_t, 64)
 EG_ATTN_INSTANTIATE(f16_t, 128)
@@ -674,29 +706,31 @@ extern "C" size_t eg_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t 
   return (size_t)(batch * heads * seq) * sizeof(float);
 }
 
-extern "C" int eg_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
-                           int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                           float scale, int dtype, void* stream) {
+extern "C" int eg_attn_gqa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                               int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                               int64_t head_dim, float scale, int dtype, void* stream) {
   clear_error();
-  if (check_attn("eg_attn_fwd", batch, heads, seq, head_dim, dtype)) return 1;
+  if (check_attn("eg_attn_fwd", batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
   if (batch == 0 || heads == 0 || seq == 0) return 0;
   if (!q || !k || !v || !o || !lse) { set_error("eg_attn_fwd: null pointer"); return 1; }
   if (!attn_aligned({q, k, v, o})) { set_error("eg_attn_fwd: tensors must be 16-byte aligned"); return 1; }
   hipStream_t st = as_stream(stream);
   const int64_t BH = batch * heads;
+  const int group = (int)(heads / kv_heads);
   if (dtype == EG_BF16)
-    return head_dim == 128 ? attn_fwd_launch<bf16_t, 128>(q, k, v, o, lse, BH, seq, scale, st)
-                           : attn_fwd_launch<bf16_t, 64>(q, k, v, o, lse, BH, seq, scale, st);
-  return head_dim == 128 ? attn_fwd_launch<f16_t, 128>(q, k, v, o, lse, BH, seq, scale, st)
-                         : attn_fwd_launch<f16_t, 64>(q, k, v, o, lse, BH, seq, scale, st);
+    return head_dim == 128 ? attn_fwd_launch<bf16_t, 128>(q, k, v, o, lse, BH, seq, group, scale, st)
+                           : attn_fwd_launch<bf16_t, 64>(q, k, v, o, lse, BH, seq, group, scale, st);
+  return head_dim == 128 ? attn_fwd_launch<f16_t, 128>(q, k, v, o, lse, BH, seq, group, scale, st)
+                         : attn_fwd_launch<f16_t, 64>(q, k, v, o, lse, BH, seq, group, scale, st);
 }
 
-extern "C" int eg_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
-                           const void* o, const float* lse, void* dq, void* dk, void* dv,
-                           void* workspace, int64_t batch, int64_t heads, int64_t seq,
-                           int64_t head_dim, float scale, int dtype, void* stream) {
+extern "C" int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* v,
+                               const void* o, const float* lse, void* dq, void* dk, void* dv,
+                               void* workspace, int64_t batch, int64_t heads, int64_t kv_heads,
+                               int64_t seq, int64_t head_dim, float scale, int dtype,
+                               void* stream) {
   clear_error();
-  if (check_attn("eg_attn_bwd", batch, heads, seq, head_dim, dtype)) return 1;
+  if (check_attn("eg_attn_bwd", batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
   if (batch == 0 || heads == 0 || seq == 0) return 0;
   if (!dout || !q || !k || !v || !o || !lse || !dq || !dk || !dv || !workspace) {
     set_error("eg_attn_bwd: null pointer");
@@ -708,12 +742,27 @@ extern "C" int eg_attn_bwd(const void* dout, const void* q, const void* k, const
   }
   hipStream_t st = as_stream(stream);
   const int64_t BH = batch * heads;
+  const int group = (int)(heads / kv_heads);
   float* delta = (float*)workspace;
   if (dtype == EG_BF16)
     return head_dim == 128
-               ? attn_bwd_launch<bf16_t, 128>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, scale, st)
-               : attn_bwd_launch<bf16_t, 64>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, scale, st);
+               ? attn_bwd_launch<bf16_t, 128>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, group, scale, st)
+               : attn_bwd_launch<bf16_t, 64>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, group, scale, st);
   return head_dim == 128
-             ? attn_bwd_launch<f16_t, 128>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, scale, st)
-             : attn_bwd_launch<f16_t, 64>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, scale, st);
+             ? attn_bwd_launch<f16_t, 128>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, group, scale, st)
+             : attn_bwd_launch<f16_t, 64>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, group, scale, st);
+}
+
+extern "C" int eg_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                           int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                           float scale, int dtype, void* stream) {
+  return eg_attn_gqa_fwd(q, k, v, o, lse, batch, heads, heads, seq, head_dim, scale, dtype, stream);
+}
+
+extern "C" int eg_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                           const void* o, const float* lse, void* dq, void* dk, void* dv,
+                           void* workspace, int64_t batch, int64_t heads, int64_t seq,
+                           int64_t head_dim, float scale, int dtype, void* stream) {
+  return eg_attn_gqa_bwd(dout, q, k, v, o, lse, dq, dk, dv, workspace, batch, heads, heads, seq,
+                         head_dim, scale, dtype, stream);
 }

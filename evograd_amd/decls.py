@@ -296,9 +296,54 @@ CAUSAL_ATTENTION = declare_op(
     make_inputs="evograd_amd.inputs:make_attention_inputs",
 )
 
+# ----------------------------------------------- grouped-query causal attention
+# The attention of src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:
+# 101-107 as the layer runs it: n_kv_heads < n_heads, k and v repeated over each
+# query group. Benchmark: the BASELINE attention batch and sequence with
+# Llama-3-8B's 32 query and 8 kv heads (src/evograd/opdecl/models.py:250-262).
+CAUSAL_ATTENTION_GQA = declare_op(
+    name="causal_attention_gqa",
+    forward="oracle.forward_refs:causal_attention_gqa_forward_ref",
+    runtime_forward="oracle.forward_refs:causal_attention_gqa_runtime_ref",
+    dims=("B", "H", "KVH", "S", "D"),
+    args=(
+        Active("q", "[B, H, S, D]"),
+        Active("k", "[B, KVH, S, D]"),
+        Active("v", "[B, KVH, S, D]"),
+    ),
+    output=Active("o", "[B, H, S, D]"),
+    forward_semantics=(
+        "k and v repeated over each group of H/KVH query heads (repeat_interleave on "
+        "the head axis), then o = softmax(q @ k^T / sqrt(D) + causal mask) @ v."
+    ),
+    backward_semantics=(
+        "Return dq, dk, dv; dk and dv are summed over the query heads sharing each kv "
+        "head; P is recomputed from the saved logsumexp."
+    ),
+    reference_dtype="float32",
+    correctness=tuple(
+        Workload(dims=dict(B=b, H=h, KVH=kv, S=s, D=d), dtype=dt)
+        for b, h, kv, s, d in (
+            (1, 4, 1, 64, 128),
+            (2, 8, 2, 129, 128),
+            (1, 4, 2, 200, 64),
+            (1, 2, 2, 100, 128),
+            (1, 32, 8, 512, 128),
+        )
+        for dt in ("bfloat16", "float16")
+    ),
+    benchmark=(
+        Workload(dims=dict(B=4, H=32, KVH=8, S=4096, D=128), dtype="bfloat16",
+                 label="llama3_8b"),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_attention_gqa_inputs",
+)
+
 OPS: dict[str, OpDecl] = {
     op.name: op
-    for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM)
+    for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM,
+               CAUSAL_ATTENTION_GQA)
 }
 
 

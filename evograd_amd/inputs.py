@@ -140,6 +140,21 @@ def make_attention_inputs(op, workload, device="cuda"):
     return {"q": q, "k": k, "v": v, "do": do}
 
 
+def make_attention_gqa_inputs(op, workload, device="cuda"):
+    """Generic seed (inputs.py:40-49); q, do [B, H, S, D] and k, v [B, KVH, S, D]
+    ~ N(0,1), drawn in the order q, k, v, do."""
+    d = workload.dims
+    qs = (d["B"], d["H"], d["S"], d["D"])
+    ks = (d["B"], d["KVH"], d["S"], d["D"])
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(case_seed(workload))
+    q = torch.randn(qs, device=device, dtype=dt)
+    k = torch.randn(ks, device=device, dtype=dt)
+    v = torch.randn(ks, device=device, dtype=dt)
+    do = torch.randn(qs, device=device, dtype=dt)
+    return {"q": q, "k": k, "v": v, "do": do}
+
+
 RECIPES = {
     "make_softmax_inputs": make_softmax_inputs,
     "make_rmsnorm_inputs": make_rmsnorm_inputs,
@@ -148,6 +163,7 @@ RECIPES = {
     "make_swiglu_inputs": make_swiglu_inputs,
     "make_rope_inputs": make_rope_inputs,
     "make_attention_inputs": make_attention_inputs,
+    "make_attention_gqa_inputs": make_attention_gqa_inputs,
 }
 
 

@@ -170,8 +170,18 @@ int eg_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
                 int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float scale,
                 int dtype, void* stream);
 
-/* Bytes of workspace eg_attn_bwd needs: delta = rowsum(do * o), fp32 [batch,
- * heads, seq]. */
+/* Grouped-query attention: q, o [batch, heads, seq, head_dim]; k, v [batch,
+ * kv_heads, seq, head_dim] with heads a multiple of kv_heads. Query head h attends
+ * with kv head h / (heads / kv_heads): the repeat_interleave of k and v at
+ * src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-105 followed by
+ * the SDPA call at :107, without materialising the repeated tensors.
+ * eg_attn_fwd is this with kv_heads = heads. */
+int eg_attn_gqa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                    int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                    int64_t head_dim, float scale, int dtype, void* stream);
+
+/* Bytes of workspace eg_attn_bwd / eg_attn_gqa_bwd need: delta = rowsum(do * o),
+ * fp32 [batch, heads, seq] (heads = query heads). */
 size_t eg_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t seq,
                                int64_t head_dim);
 
@@ -181,6 +191,15 @@ int eg_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
                 const void* o, const float* lse, void* dq, void* dk, void* dv,
                 void* workspace, int64_t batch, int64_t heads, int64_t seq,
                 int64_t head_dim, float scale, int dtype, void* stream);
+
+/* Backward of eg_attn_gqa_fwd: dq [batch, heads, seq, head_dim]; dk, dv [batch,
+ * kv_heads, seq, head_dim], each the sum over the heads/kv_heads query heads that
+ * share the kv head (the gradient of the repeat_interleave), accumulated in fp32
+ * in a fixed order. */
+int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* v,
+                    const void* o, const float* lse, void* dq, void* dk, void* dv,
+                    void* workspace, int64_t batch, int64_t heads, int64_t kv_heads,
+                    int64_t seq, int64_t head_dim, float scale, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

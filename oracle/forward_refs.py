@@ -111,6 +111,28 @@ def causal_attention_runtime_ref(q, k, v):
     return F.scaled_dot_product_attention(q, k, v, is_causal=True)
 
 
+def causal_attention_gqa_forward_ref(q, k, v):
+    """src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-107: each kv
+    head repeated over its group of query heads (repeat_interleave on the head
+    axis), then causal attention."""
+    repeat = q.shape[1] // k.shape[1]
+    if repeat * k.shape[1] != q.shape[1]:
+        raise ValueError("query heads must be a multiple of kv heads")
+    if repeat > 1:
+        k = k.repeat_interleave(repeat, dim=1)
+        v = v.repeat_interleave(repeat, dim=1)
+    return causal_attention_forward_ref(q, k, v)
+
+
+def causal_attention_gqa_runtime_ref(q, k, v):
+    """The reference's eager spelling: repeat_interleave, then F.sdpa (:101-107)."""
+    repeat = q.shape[1] // k.shape[1]
+    if repeat > 1:
+        k = k.repeat_interleave(repeat, dim=1)
+        v = v.repeat_interleave(repeat, dim=1)
+    return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+
+
 def causal_attention_lse_ref(q, k):
     """logsumexp over keys of the scaled, causally masked scores, fp32 [B, H, S]:
     the statistic the attention forward saves."""
@@ -132,4 +154,6 @@ FORWARDS = {
     "rope_forward_ref": rope_forward_ref,
     "causal_attention_forward_ref": causal_attention_forward_ref,
     "causal_attention_runtime_ref": causal_attention_runtime_ref,
+    "causal_attention_gqa_forward_ref": causal_attention_gqa_forward_ref,
+    "causal_attention_gqa_runtime_ref": causal_attention_gqa_runtime_ref,
 }

@@ -68,3 +68,53 @@ def test_attention_baseline_config():
     rep = verify(OP, pair_module("causal_attention"), device="cuda", workloads=(w,))
     torch.cuda.empty_cache()
     assert rep.ok, "\n".join(rep.failures())
+
+
+GQA = decls.CAUSAL_ATTENTION_GQA
+
+
+@pytest.mark.parametrize("w", GQA.correctness, ids=lambda w: w.key())
+def test_attention_gqa_correctness_workloads(w):
+    _note("gqa", w.dims, w.dtype)
+    rep = verify(GQA, pair_module("causal_attention_gqa"), device="cuda", workloads=(w,))
+    assert rep.ok, "\n".join(rep.failures())
+
+
+def test_attention_gqa_matches_mha_on_repeated_kv():
+    """The GQA kernels read each kv head in place of a repeated copy: o, lse and dq
+    are bitwise those of the MHA kernels on repeat_interleave'd k, v; dk, dv are the
+    group sums of the MHA gradients (one rounding instead of one per head)."""
+    w = Workload(dims=dict(B=2, H=8, KVH=2, S=300, D=128), dtype="bfloat16")
+    _note("gqa vs mha", w.dims)
+    inp = make_case_inputs(GQA, w, "cuda")
+    mod = pair_module("causal_attention")
+    kr, vr = (inp[n].repeat_interleave(4, dim=1).contiguous() for n in ("k", "v"))
+    og, sg = mod.causal_attention_forward_with_saved(inp["q"], inp["k"], inp["v"])
+    om, sm = mod.causal_attention_forward_with_saved(inp["q"], kr, vr)
+    assert torch.equal(og, om) and torch.equal(sg[-1], sm[-1])
+    dqg, dkg, dvg = mod.causal_attention_backward_from_saved(inp["do"], sg)
+    dqm, dkm, dvm = mod.causal_attention_backward_from_saved(inp["do"], sm)
+    assert torch.equal(dqg, dqm)
+    for a, b in ((dkg, dkm), (dvg, dvm)):
+        ref = b.float().view(2, 2, 4, 300, 128).sum(2)
+        assert a.shape == (2, 2, 300, 128)
+        assert torch.allclose(a.float(), ref, atol=3e-2, rtol=2e-2), (a.float() - ref).abs().max()
+
+
+def test_attention_gqa_backward_is_bitwise_deterministic():
+    w = Workload(dims=dict(B=1, H=32, KVH=8, S=1024, D=128), dtype="bfloat16")
+    _note("gqa determinism", w.dims)
+    inp = make_case_inputs(GQA, w, "cuda")
+    mod = pair_module("causal_attention_gqa")
+    _, saved = mod.causal_attention_gqa_forward_with_saved(inp["q"], inp["k"], inp["v"])
+    a = mod.causal_attention_gqa_backward_from_saved(inp["do"], saved)
+    b = mod.causal_attention_gqa_backward_from_saved(inp["do"], saved)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+
+def test_attention_gqa_llama3_8b_config():
+    w = GQA.benchmark[0]
+    _note("gqa llama3_8b", w.dims)
+    rep = verify(GQA, pair_module("causal_attention_gqa"), device="cuda", workloads=(w,))
+    torch.cuda.empty_cache()
+    assert rep.ok, "\n".join(rep.failures())

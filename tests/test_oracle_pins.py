@@ -313,6 +313,38 @@ def test_attention_gradient_fd():
 
 
 # ------------------------------------------------------- oracle machinery
+def test_attention_gqa_reduces_to_mha_and_loops_over_groups():
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(2, 6, 9, 8, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(2, 2, 9, 8, generator=g, dtype=torch.float64) for _ in range(2))
+    # KVH == H is ordinary attention
+    kk, vv = (torch.randn(2, 6, 9, 8, generator=g, dtype=torch.float64) for _ in range(2))
+    assert torch.allclose(fr.causal_attention_gqa_forward_ref(q, kk, vv),
+                          fr.causal_attention_forward_ref(q, kk, vv))
+    # query head h attends with kv head h // 3 (interleaved repeat, not tiled)
+    out = fr.causal_attention_gqa_forward_ref(q, k, v)
+    for h in range(6):
+        ref = _attn_brute(q[:, h:h + 1], k[:, h // 3:h // 3 + 1], v[:, h // 3:h // 3 + 1])[0]
+        assert torch.allclose(out[:, h:h + 1], ref)
+    with pytest.raises(ValueError):
+        fr.causal_attention_gqa_forward_ref(q, k[:, :1].expand(2, 4, 9, 8).contiguous()[:, :4], v)
+
+
+def test_attention_gqa_gradient_fd_and_group_sums():
+    op = decls.CAUSAL_ATTENTION_GQA
+    w = Workload(dims=dict(B=1, H=4, KVH=2, S=6, D=8), dtype="float32")
+    inputs = _f64(make_case_inputs(op, w, "cpu"))
+    _fd_check(op, inputs)
+    _, g = oracle(op, inputs, use_reference_dtype=False)
+    # dk, dv are the MHA gradients of the repeated k, v summed over each group
+    rep = {"q": inputs["q"], "k": inputs["k"].repeat_interleave(2, 1),
+           "v": inputs["v"].repeat_interleave(2, 1), "do": inputs["do"]}
+    _, gm = oracle(decls.CAUSAL_ATTENTION, rep, use_reference_dtype=False)
+    assert torch.allclose(g["dq"], gm["dq"])
+    for name in ("dk", "dv"):
+        assert torch.allclose(g[name], gm[name].view(1, 2, 2, 6, 8).sum(2))
+
+
 def test_oracle_promotes_and_casts_back():
     w = Workload(dims=dict(rows=4, hidden=32), dtype="bfloat16")
     inputs = make_case_inputs(decls.RMSNORM, w, "cpu")
