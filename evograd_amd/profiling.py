@@ -3,6 +3,7 @@
     python -m evograd_amd.profiling stats    <prefix>_kernel_stats.csv [FILTER]
     python -m evograd_amd.profiling counters <prefix>_counter_collection.csv [FILTER]
     python -m evograd_amd.profiling traffic  FETCH.csv WRITE.csv KERNEL_SUBSTRING [KEY]
+    python -m evograd_amd.profiling mfma     COUNTERS.csv KERNEL_STATS.csv [FILTER] [GHZ]
 
 ``traffic`` turns the FETCH_SIZE and WRITE_SIZE readings (KiB per dispatch,
 summed over the L2 channels) of one kernel into HBM bytes per launch, scaled by
@@ -78,6 +79,33 @@ def counters(path: str, filt: str = "") -> str:
     return "\n".join(lines)
 
 
+def mfma(counter_csv: str, stats_csv: str, filt: str = "", ghz: float = 2.4) -> str:
+    """MFMA utilisation per kernel: SQ_VALU_MFMA_BUSY_CYCLES (summed over all
+    SIMDs; a 32x32x16 bf16 MFMA keeps its SIMD busy 32 cycles) divided by the
+    kernel's mean duration (kernel trace) x clock x 1024 SIMDs (256 CUs x 4), and
+    the executed MFMA FLOPs (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512)."""
+    table = _counter_table(counter_csv)
+    dur = {}
+    for r in csv.DictReader(open(stats_csv)):
+        dur[short_name(r["Name"])] = float(r["AverageNs"]) * 1e-9
+    lines = ["| kernel | mean us (trace) | MFMA busy % | executed MFMA TFLOP | executed TFLOP/s |",
+             "|---|---:|---:|---:|---:|"]
+    for k, cs in table.items():
+        if filt and filt not in k:
+            continue
+        name = short_name(k)
+        t = dur.get(name)
+        busy = cs.get("SQ_VALU_MFMA_BUSY_CYCLES")
+        mops = cs.get("SQ_INSTS_VALU_MFMA_MOPS_BF16")
+        if t is None or not busy:
+            continue
+        util = statistics.mean(busy) / (t * ghz * 1e9 * 1024)
+        flops = statistics.mean(mops) * 512 if mops else float("nan")
+        lines.append(f"| `{name}` | {t * 1e6:.1f} | {100 * util:.1f} | {flops / 1e12:.3f} | "
+                     f"{flops / t / 1e12:.1f} |")
+    return "\n".join(lines)
+
+
 def traffic(fetch_csv: str, write_csv: str, kernel: str, key: str = "") -> dict:
     f, w = _counter_table(fetch_csv), _counter_table(write_csv)
 
@@ -118,6 +146,9 @@ def main(argv: list) -> int:
         print(stats(argv[1], argv[2] if len(argv) > 2 else ""))
     elif cmd == "counters":
         print(counters(argv[1], argv[2] if len(argv) > 2 else ""))
+    elif cmd == "mfma":
+        print(mfma(argv[1], argv[2], argv[3] if len(argv) > 3 else "",
+                   float(argv[4]) if len(argv) > 4 else 2.4))
     elif cmd == "traffic":
         print(json.dumps(traffic(argv[1], argv[2], argv[3], argv[4] if len(argv) > 4 else ""), indent=1))
     else:
