@@ -45,6 +45,25 @@ TOLERANCES = {
 }
 
 
+# Shape regimes of the reference declarations: the row (token) count splits small
+# from large shapes at Llama-3's 4096 tokens (2048 for vocabulary-wide rows),
+# src/evograd/opdecl/models.py:306-307.
+LLAMA_REGIME_SPLIT = 4096.0
+LLAMA_VOCAB_REGIME_SPLIT = 2048.0
+
+
+def _rows_feature(workload) -> float:
+    return float(workload.dims["rows"])
+
+
+def _tokens_feature(workload) -> float:
+    return float(workload.dims["T"])
+
+
+def _seq_feature(workload) -> float:
+    return float(workload.dims["S"])
+
+
 def _w2(shapes, dtypes, row="rows", col="cols", label=""):
     return tuple(
         Workload(dims={row: r, col: c}, dtype=dt, label=label)
@@ -73,6 +92,8 @@ SOFTMAX = declare_op(
     benchmark=_w2(((4096, 4096),), ("float32",), label="baseline"),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_softmax_inputs",
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_VOCAB_REGIME_SPLIT,
 )
 
 # ------------------------------------------------------------------ rmsnorm
@@ -119,6 +140,8 @@ RMSNORM = declare_op(
     ),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_rmsnorm_inputs",
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 # ------------------------------------------------------- fused_add_rms_norm
@@ -162,6 +185,8 @@ FUSED_ADD_RMS_NORM = declare_op(
     ),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_fused_add_rms_norm_inputs",
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 # ---------------------------------------------------------------- layernorm
@@ -201,6 +226,8 @@ LAYERNORM = declare_op(
     ),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_layernorm_inputs",
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 # ------------------------------------------------------------------- swiglu
@@ -224,6 +251,8 @@ SWIGLU = declare_op(
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_swiglu_inputs",
     backward_may_overwrite=("a", "b"),
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 # --------------------------------------------------------------------- rope
@@ -257,6 +286,8 @@ ROPE = declare_op(
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_rope_inputs",
     memory_inputs=("x",),
+    regime_feature=_tokens_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 # --------------------------------------------------------- causal attention
@@ -294,6 +325,8 @@ CAUSAL_ATTENTION = declare_op(
     ),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_attention_inputs",
+    regime_feature=_seq_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 # ----------------------------------------------- grouped-query causal attention
@@ -338,6 +371,8 @@ CAUSAL_ATTENTION_GQA = declare_op(
     ),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_attention_gqa_inputs",
+    regime_feature=_seq_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
 )
 
 OPS: dict[str, OpDecl] = {

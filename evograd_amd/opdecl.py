@@ -110,6 +110,11 @@ class OpDecl:
     make_inputs: str | None = None
     memory_inputs: tuple | None = None
     backward_may_overwrite: tuple = ()
+    # Shape regimes (activity.py:258-262): regime_feature maps an object with a
+    # ``dims`` mapping to a float; a shape dispatcher routes below regime_split to
+    # its small-shape program.
+    regime_feature: Callable | None = None
+    regime_split: float | None = None
 
     # ---- derived views (activity.py:289-337)
     def active_args(self) -> tuple:
@@ -181,6 +186,13 @@ class OpDecl:
         for name in self.backward_may_overwrite:
             if name not in [a.name for a in self.active_args()]:
                 raise ValueError(f"{self.name}: backward_may_overwrite names non-Active {name!r}")
+        if self.regime_feature is not None or self.regime_split is not None:
+            # activity.py:463-471
+            if not callable(self.regime_feature) or self.regime_split is None:
+                raise ValueError(f"{self.name}: shape regimes require callable regime_feature "
+                                 "and numeric regime_split")
+            if self.regime_split <= 0:
+                raise ValueError(f"{self.name}: regime_split must be positive")
 
     def _validate_shape(self, arg_name: str, shape: str) -> None:
         text = shape.strip()

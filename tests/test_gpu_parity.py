@@ -136,3 +136,24 @@ def test_fused_add_rms_norm_backward_deterministic_and_grads_not_aliased():
     gx, gr = leaves[0].grad, leaves[1].grad
     assert torch.equal(gx, gr)
     assert gx.untyped_storage().data_ptr() != gr.untyped_storage().data_ptr()
+
+
+def test_shape_dispatch_routes_hip_programs():
+    """The wire format with HIP programs on both routes: the dispatched pair passes
+    the gate below and above the declaration's 4096-row split, and the saved state
+    carries the route tag."""
+    from evograd_amd.dispatch import ShapeDispatch
+    from evograd_amd.opdecl import Workload
+
+    op = decls.RMSNORM
+    hip = pair_module("rmsnorm")
+    pair = ShapeDispatch(op, hip, hip)
+    small = Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16")
+    large = Workload(dims=dict(rows=4096, hidden=4096), dtype="bfloat16")
+    print("\n[gpu-parity] dispatch rmsnorm", small.dims, large.dims, flush=True)
+    for w, route in ((small, 0), (large, 1)):
+        rep = verify(op, pair, device="cuda", workloads=(w,))
+        assert rep.ok, "\n".join(rep.failures())
+        inp = make_case_inputs(op, w, "cuda")
+        _, saved = pair.rmsnorm_forward_with_saved(inp["x"], inp["weight"], inp["eps"])
+        assert saved[0] == route
