@@ -41,7 +41,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
 ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
-           "fused_add_rms_norm", "causal_attention_gqa")
+           "fused_add_rms_norm", "causal_attention_gqa", "cross_entropy")
 
 
 def log(msg: str) -> None:
@@ -78,6 +78,12 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
         n = R * C * es
         return {"unit": "bytes", "fwd": 3 * n + C * es + 4 * R,
                 "bwd": 4 * n + 4 * R + 2 * C * es}
+    if name == "cross_entropy":
+        # fwd reads logits and target once and writes lse and the loss; bwd reads
+        # logits, target and lse and writes dlogits.
+        R, C = d["rows"], d["cols"]
+        n = R * C * es
+        return {"unit": "bytes", "fwd": n + 8 * R + 4 * R + es, "bwd": 2 * n + 8 * R + 4 * R}
     if name == "rope":
         B, H, T, D = d["B"], d["n_heads"], d["T"], d["head_dim"]
         xb = B * (H + extra_k_heads) * T * D * es
@@ -102,6 +108,7 @@ KERNELS = {
     "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_kernel"]},
     "causal_attention_gqa": {"fwd": ["attn_fwd_kernel"],
                              "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
+    "cross_entropy": {"fwd": ["xent_lse_kernel", "xent_mean_kernel"], "bwd": ["xent_bwd_kernel"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.
@@ -109,6 +116,7 @@ DOMINANT = {
     "softmax": ("bwd", 0), "rmsnorm": ("bwd", 0), "layernorm": ("bwd", 0),
     "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
     "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
+    "cross_entropy": ("bwd", 0),
 }
 
 
@@ -285,7 +293,8 @@ def cpu_baseline(name: str) -> dict:
     op = decls.get_op(name)
     w = op.benchmark[0]
     d = dict(w.dims)
-    if name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm"):
+    if name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm",
+                "cross_entropy"):
         full_rows = d["rows"]
         d["rows"] = max(1, full_rows // 8)
         scale = full_rows / d["rows"]

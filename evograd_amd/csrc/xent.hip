@@ -1,0 +1,267 @@
+// Hard-label mean cross entropy over vocabulary-wide rows, for gfx950.
+//
+// Forward restates cross_entropy_forward_ref
+// (src/evograd/ops/level1/cross_entropy/forward_ref.py:6-12): per row
+// lse = logsumexp(logits[r]) in fp32, the row loss lse - logits[r, target[r]],
+// the mean over rows whose target is not ignore_index (-100 in the reference),
+// cast to the logits dtype. Backward is the rule of
+// src/evograd/ops/level1/cross_entropy/__init__.py:91-94:
+// dlogits = dloss * (softmax(logits) - onehot(target)) / n_valid, zero on ignored
+// rows.
+//
+// Saved state is lse [rows] fp32 and n_valid (one fp32 count) beside the inputs.
+// Kernels:
+//   xent_lse_kernel   one workgroup per row, one HBM read of the row: 16-byte
+//                     non-temporal loads, UNROLL packs in flight per thread, an
+//                     online (max, sum of exp2) per thread, one max and one sum
+//                     over the workgroup; writes lse[row].
+//   xent_mean_kernel  one workgroup: the row losses (lse - the target logit,
+//                     one gathered element per row) summed in a fixed order, and
+//                     the count of non-ignored rows; writes the loss and n_valid.
+//   xent_bwd_kernel   (row, column chunk) grid; one read of the row chunk and one
+//                     write of dlogits, with dloss read from device memory.
+// No atomics: every sum has a fixed order, so results are bitwise repeatable.
+//
+// A target outside [0, cols) that is not ignore_index makes that row's loss and
+// gradient NaN (torch raises there); it is never used as an index.
+#include "eg_common.hpp"
+
+namespace eg {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kUnroll = 4;        // packs in flight per thread
+constexpr int kBwdBlock = 256;
+constexpr int kMeanBlock = 1024;
+
+// Reference point of a running max, as torch's logsumexp takes it: an infinite
+// max is replaced by 0 so that exp(x - ref) stays defined.
+__device__ __forceinline__ float lse_ref(float m) { return __builtin_isinf(m) ? 0.f : m; }
+
+template <typename T, int VEC, int BLOCK, bool NT>
+__global__ __launch_bounds__(BLOCK) void xent_lse_kernel(const T* __restrict__ x,
+                                                         float* __restrict__ lse, int cols) {
+  __shared__ float red[BLOCK / kWave];
+  constexpr int STEP = BLOCK * VEC;
+  const T* __restrict__ xr = x + (int64_t)blockIdx.x * cols;
+  float m = -INFINITY;  // running max of this thread's elements
+  float s = 0.f;        // sum of exp(v - lse_ref(m)) over them
+  for (int base = (int)threadIdx.x * VEC; base < cols; base += STEP * kUnroll) {
+    float v[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = base + u * STEP;
+      if (c < cols) {
+        load_vec<T, VEC, NT>(xr + c, v[u]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[u][i] = -INFINITY;
+      }
+    }
+    float bm = m;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) bm = fmaxf(bm, v[u][i]);
+    const float r_new = lse_ref(bm);
+    const float rl = r_new * kLog2e;
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        acc += __builtin_amdgcn_exp2f(__builtin_fmaf(v[u][i], kLog2e, -rl));
+    // s == 0 also covers the first batch (m = -inf), where the rescale factor
+    // could overflow.
+    s = (s == 0.f) ? acc
+                   : __builtin_fmaf(s, __builtin_amdgcn_exp2f((lse_ref(m) - r_new) * kLog2e),
+                                    acc);
+    m = bm;
+  }
+  const float gm = block_reduce<BLOCK>(m, MaxOp(), red);
+  const float gref = lse_ref(gm);
+  const float part =
+      (s == 0.f) ? 0.f : s * __builtin_amdgcn_exp2f((lse_ref(m) - gref) * kLog2e);
+  const float total = block_reduce<BLOCK>(part, SumOp(), red);
+  if (threadIdx.x == 0) lse[blockIdx.x] = gref + log2f(total) * kLn2;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kMeanBlock) void xent_mean_kernel(
+    const T* __restrict__ x, const int64_t* __restrict__ target, const float* __restrict__ lse,
+    T* __restrict__ loss, float* __restrict__ n_valid, int64_t rows, int cols,
+    int64_t ignore_index) {
+  __shared__ float red[kMeanBlock / kWave];
+  float sum = 0.f, count = 0.f;
+  for (int64_t r = threadIdx.x; r < rows; r += kMeanBlock) {
+    const int64_t t = target[r];
+    if (t == ignore_index) continue;
+    const float picked = (t >= 0 && t < cols) ? to_f32(x[r * cols + t]) : NAN;
+    sum += lse[r] - picked;
+    count += 1.f;
+  }
+  sum = block_reduce<kMeanBlock>(sum, SumOp(), red);
+  count = block_reduce<kMeanBlock>(count, SumOp(), red);
+  if (threadIdx.x == 0) {
+    loss[0] = from_f32<T>(sum / count);
+    n_valid[0] = count;
+  }
+}
+
+template <typename T, int VEC, bool NT>
+__global__ __launch_bounds__(kBwdBlock) void xent_bwd_kernel(
+    const T* __restrict__ dloss, const T* __restrict__ x, const int64_t* __restrict__ target,
+    const float* __restrict__ lse, const float* __restrict__ n_valid, T* __restrict__ dx,
+    int cols, int64_t ignore_index) {
+  constexpr int STEP = kBwdBlock * VEC;
+  const int64_t row = blockIdx.x;
+  const int64_t t = target[row];
+  const int c0 = (int)blockIdx.y * (STEP * kUnroll) + (int)threadIdx.x * VEC;
+  T* __restrict__ dr = dx + row * cols;
+  if (t == ignore_index) {
+    float z[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) z[i] = 0.f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = c0 + u * STEP;
+      if (c < cols) store_vec<T, VEC, NT>(dr + c, z);
+    }
+    return;
+  }
+  // The reference's mean divides by the non-ignored count: g = dloss / n.
+  const float g = (t >= 0 && t < cols) ? to_f32(dloss[0]) / n_valid[0] : NAN;
+  const float ll = lse[row] * kLog2e;
+  const int tc = (int)t;
+  const T* __restrict__ xr = x + row * cols;
+  float v[kUnroll][VEC];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int c = c0 + u * STEP;
+    if (c < cols) load_vec<T, VEC, NT>(xr + c, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int c = c0 + u * STEP;
+    if (c < cols) {
+      float o[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(v[u][i], kLog2e, -ll));
+        o[i] = g * (c + i == tc ? p - 1.f : p);
+      }
+      store_vec<T, VEC, NT>(dr + c, o);
+    }
+  }
+}
+
+// Smallest power-of-two workgroup (64..1024 threads) whose threads cover a row
+// of `npack` packs in one pass of kUnroll packs each.
+template <typename Launch>
+void pick_lse_block(int64_t npack, Launch&& launch) {
+  const int64_t per = (npack + kUnroll - 1) / kUnroll;
+  if (per <= 64) launch.template go<64>();
+  else if (per <= 128) launch.template go<128>();
+  else if (per <= 256) launch.template go<256>();
+  else if (per <= 512) launch.template go<512>();
+  else launch.template go<1024>();
+}
+
+template <typename T, int VEC>
+struct LseLaunch {
+  const T* x; float* lse; int64_t rows; int cols; hipStream_t st;
+  template <int BLOCK> void go() {
+    EG_LAUNCH((xent_lse_kernel<T, VEC, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+              dim3(BLOCK), 0, st, x, lse, cols);
+  }
+};
+
+int check_xent(const char* what, int64_t rows, int64_t cols) {
+  if (rows < 0 || cols < 0) {
+    set_error("%s: negative size rows=%lld cols=%lld", what, (long long)rows, (long long)cols);
+    return 1;
+  }
+  if (rows > 0 && cols == 0) {
+    set_error("%s: cross entropy over zero classes", what);
+    return 1;
+  }
+  // rows: the grid's x extent and an exactly representable fp32 count; cols: int.
+  if (rows > ((int64_t)1 << 24) || cols > ((int64_t)1 << 30)) {
+    set_error("%s: size out of range rows=%lld cols=%lld", what, (long long)rows,
+              (long long)cols);
+    return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" int eg_cross_entropy_fwd(const void* logits, const int64_t* target, void* loss,
+                                    float* lse, float* n_valid, int64_t rows, int64_t cols,
+                                    int64_t ignore_index, int dtype, void* stream) {
+  clear_error();
+  if (check_xent("eg_cross_entropy_fwd", rows, cols)) return 1;
+  if (!loss || !n_valid || (rows > 0 && (!logits || !target || !lse))) {
+    set_error("eg_cross_entropy_fwd: null pointer");
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_cross_entropy_fwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const T* xp = static_cast<const T*>(logits);
+    if (rows > 0) {
+      if (cols % V == 0 && aligned16(logits)) {
+        pick_lse_block(cols / V, LseLaunch<T, V>{xp, lse, rows, (int)cols, st});
+      } else {
+        pick_lse_block(cols, LseLaunch<T, 1>{xp, lse, rows, (int)cols, st});
+      }
+    }
+    // Also for rows == 0: the mean of no rows is 0/0 (NaN), as in torch.
+    EG_LAUNCH((xent_mean_kernel<T>), dim3(1), dim3(kMeanBlock), 0, st, xp, target, lse,
+              static_cast<T*>(loss), n_valid, rows, (int)cols, ignore_index);
+    return check_launch("eg_cross_entropy_fwd");
+  });
+}
+
+extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
+                                    const int64_t* target, const float* lse,
+                                    const float* n_valid, void* dlogits, int64_t rows,
+                                    int64_t cols, int64_t ignore_index, int dtype,
+                                    void* stream) {
+  clear_error();
+  if (check_xent("eg_cross_entropy_bwd", rows, cols)) return 1;
+  if (rows == 0) return 0;
+  if (!dloss || !logits || !target || !lse || !n_valid || !dlogits) {
+    set_error("eg_cross_entropy_bwd: null pointer");
+    return 1;
+  }
+  if ((cols + kBwdBlock * kUnroll - 1) / (kBwdBlock * kUnroll) > 65535) {
+    set_error("eg_cross_entropy_bwd: cols=%lld exceeds the column-chunk grid", (long long)cols);
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  return EG_DISPATCH_FLOAT(dtype, "eg_cross_entropy_bwd", [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const T* gp = static_cast<const T*>(dloss);
+    const T* xp = static_cast<const T*>(logits);
+    T* dp = static_cast<T*>(dlogits);
+    if (cols % V == 0 && aligned16(logits) && aligned16(dlogits)) {
+      const int64_t chunks = (cols + kBwdBlock * V * kUnroll - 1) / (kBwdBlock * V * kUnroll);
+      EG_LAUNCH((xent_bwd_kernel<T, V, V * sizeof(T) == 16>),
+                dim3((unsigned)rows, (unsigned)chunks), dim3(kBwdBlock), 0, st, gp, xp, target,
+                lse, n_valid, dp, (int)cols, ignore_index);
+    } else {
+      const int64_t chunks = (cols + kBwdBlock * kUnroll - 1) / (kBwdBlock * kUnroll);
+      EG_LAUNCH((xent_bwd_kernel<T, 1, false>), dim3((unsigned)rows, (unsigned)chunks),
+                dim3(kBwdBlock), 0, st, gp, xp, target, lse, n_valid, dp, (int)cols,
+                ignore_index);
+    }
+    return check_launch("eg_cross_entropy_bwd");
+  });
+}

@@ -1,4 +1,4 @@
-"""Declarations of the six autograd-pair operators this library implements.
+"""Declarations of the autograd-pair operators this library implements.
 
 Argument names, activity, output and gradient names follow the reference's
 declarations exactly, so a candidate module written against them is the same
@@ -10,6 +10,7 @@ drop-in the reference's harness looks up:
 * swiglu     src/evograd/ops/level1/swiglu/__init__.py:61-97
 * rope       src/evograd/ops/level1/rope/__init__.py:98-162
 * fused_add_rms_norm  src/evograd/ops/level2/fused_add_rms_norm/__init__.py:76-122
+* cross_entropy  src/evograd/ops/level1/cross_entropy/__init__.py:76-111
 * causal_attention: the reference has no standalone declaration; its semantics
   are F.scaled_dot_product_attention(q, k, v, is_causal=True) inside
   src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-108. It is
@@ -375,10 +376,65 @@ CAUSAL_ATTENTION_GQA = declare_op(
     regime_split=LLAMA_REGIME_SPLIT,
 )
 
+# ------------------------------------------------------------ cross_entropy
+# src/evograd/ops/level1/cross_entropy/__init__.py:76-111. The gradient's entries
+# have magnitude about dloss / (rows * cols), so a flat atol would pass anything:
+# the atol of dlogits is scaled by 1 / (rows * cols) and the comparison rests on
+# the relative term.
+def _xent_tolerance(workload, result_name, atol, rtol):
+    if result_name == "dlogits":
+        atol = atol / (workload.dims["rows"] * workload.dims["cols"])
+    return atol, rtol
+
+
+CROSS_ENTROPY = declare_op(
+    name="cross_entropy",
+    forward="oracle.forward_refs:cross_entropy_forward_ref",
+    dims=("rows", "cols"),
+    args=(
+        Active("logits", "[rows, cols]"),
+        Inactive("target", "[rows]", dtype="int64"),
+    ),
+    output=Active("loss", "[]"),
+    forward_semantics=(
+        "Mean-reduced hard-label cross entropy with ignore_index=-100, no label "
+        "smoothing, z-loss, or class weights; logsumexp in fp32."
+    ),
+    backward_semantics=(
+        "dlogits = dloss * (softmax(logits) - onehot(target)) / n_valid, zero on ignored "
+        "rows; target receives no gradient."
+    ),
+    reference_dtype="float32",
+    correctness=(
+        _w2(((8, 512), (16, 1024)), ("float32",))
+        + _w2(((32, 4096), (64, 2048)), ("float16", "bfloat16"))
+        # ragged widths (the scalar path, GPT-2's odd vocabulary), a single row, a
+        # Llama-3 vocabulary row, and every third row ignored
+        + _w2(((5, 127), (1, 4096), (4, 128256)), ("float32", "bfloat16"))
+        + _w2(((3, 50257),), ("bfloat16",))
+        + tuple(
+            Workload(dims=dict(rows=r, cols=c), dtype=dt, label="ignore3",
+                     extra={"ignore_every": 3})
+            for r, c, dt in ((16, 1024, "float32"), (64, 2048, "bfloat16"))
+        )
+    ),
+    # Llama-3-8B logits at the sweep's largest token count
+    # (src/evograd/opdecl/models.py:84-86, :293).
+    benchmark=(
+        Workload(dims=dict(rows=8192, cols=128256), dtype="bfloat16", label="llama3_8b"),
+    ),
+    tolerances=TOLERANCES,
+    tolerance_hook=_xent_tolerance,
+    make_inputs="evograd_amd.inputs:make_cross_entropy_inputs",
+    memory_inputs=("logits",),
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_VOCAB_REGIME_SPLIT,
+)
+
 OPS: dict[str, OpDecl] = {
     op.name: op
     for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM,
-               CAUSAL_ATTENTION_GQA)
+               CAUSAL_ATTENTION_GQA, CROSS_ENTROPY)
 }
 
 

@@ -155,6 +155,23 @@ def make_attention_gqa_inputs(op, workload, device="cuda"):
     return {"q": q, "k": k, "v": v, "do": do}
 
 
+def make_cross_entropy_inputs(op, workload, device="cuda"):
+    """cross_entropy/__init__.py:48-56: seed rows*100003+cols; logits ~ N(0,1), target
+    uniform in [0, cols) (int64), dloss = U[0,1) + 0.5 (0-dim, logits dtype), drawn in
+    that order. ``extra["ignore_every"] = k`` then sets every k-th target (rows 0, k,
+    2k, ...) to the ignore index -100."""
+    rows, cols = workload.dims["rows"], workload.dims["cols"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100003 + cols)
+    logits = torch.randn((rows, cols), device=device, dtype=dt)
+    target = torch.randint(0, cols, (rows,), device=device, dtype=torch.int64)
+    dloss = torch.rand((), device=device, dtype=dt) + 0.5
+    every = int(workload.extra.get("ignore_every", 0))
+    if every:
+        target[::every] = -100
+    return {"logits": logits, "target": target, "dloss": dloss}
+
+
 RECIPES = {
     "make_softmax_inputs": make_softmax_inputs,
     "make_rmsnorm_inputs": make_rmsnorm_inputs,
@@ -164,6 +181,7 @@ RECIPES = {
     "make_rope_inputs": make_rope_inputs,
     "make_attention_inputs": make_attention_inputs,
     "make_attention_gqa_inputs": make_attention_gqa_inputs,
+    "make_cross_entropy_inputs": make_cross_entropy_inputs,
 }
 
 

@@ -201,6 +201,28 @@ int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* 
                     void* workspace, int64_t batch, int64_t heads, int64_t kv_heads,
                     int64_t seq, int64_t head_dim, float scale, int dtype, void* stream);
 
+/* ---------------------------------------------------------- cross entropy
+ * Replaces cross_entropy_forward_ref
+ * (src/evograd/ops/level1/cross_entropy/forward_ref.py:6-12):
+ *   loss = F.cross_entropy(logits.float(), target, reduction="mean",
+ *                          ignore_index=ignore_index).to(logits.dtype)
+ * logits [rows, cols] (dtype); target [rows] int64; loss one element (dtype).
+ * Saved: lse [rows] fp32 (logsumexp of each row) and n_valid, one fp32 (the
+ * number of rows whose target != ignore_index). A target outside [0, cols) that
+ * is not ignore_index makes the loss NaN. rows == 0 gives NaN (0/0), as torch. */
+int eg_cross_entropy_fwd(const void* logits, const int64_t* target, void* loss, float* lse,
+                         float* n_valid, int64_t rows, int64_t cols, int64_t ignore_index,
+                         int dtype, void* stream);
+
+/* Backward of eg_cross_entropy_fwd, the rule declared at
+ * src/evograd/ops/level1/cross_entropy/__init__.py:91-94:
+ *   dlogits = dloss * (softmax(logits) - onehot(target)) / n_valid,
+ * zero on rows whose target is ignore_index. dloss is one element (dtype) in
+ * device memory; dlogits [rows, cols] (dtype). */
+int eg_cross_entropy_bwd(const void* dloss, const void* logits, const int64_t* target,
+                         const float* lse, const float* n_valid, void* dlogits, int64_t rows,
+                         int64_t cols, int64_t ignore_index, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -142,6 +142,13 @@ def causal_attention_lse_ref(q, k):
     return torch.logsumexp(s.masked_fill(mask, float("-inf")), dim=-1)
 
 
+def cross_entropy_forward_ref(logits: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """src/evograd/ops/level1/cross_entropy/forward_ref.py:6-12: mean hard-label cross
+    entropy of the fp32-widened logits, ignore_index -100, cast to the logits dtype."""
+    loss = F.cross_entropy(logits.float(), target, reduction="mean", ignore_index=-100)
+    return loss.to(logits.dtype)
+
+
 FORWARDS = {
     "softmax_forward_ref": softmax_forward_ref,
     "rmsnorm_forward_ref": rmsnorm_forward_ref,
@@ -156,4 +163,5 @@ FORWARDS = {
     "causal_attention_runtime_ref": causal_attention_runtime_ref,
     "causal_attention_gqa_forward_ref": causal_attention_gqa_forward_ref,
     "causal_attention_gqa_runtime_ref": causal_attention_gqa_runtime_ref,
+    "cross_entropy_forward_ref": cross_entropy_forward_ref,
 }

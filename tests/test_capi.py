@@ -58,8 +58,18 @@ def test_host_side_validation_errors_without_gpu():
         _lib.call("eg_rope", None, None, None, None, None, None, 1, 1, 0, 4, 5, 0, 0, 0, None)
     with pytest.raises(RuntimeError, match="dtype"):
         _lib.call("eg_swiglu_fwd", 16, 16, 16, 8, 7, None)
+    with pytest.raises(RuntimeError, match="zero classes"):
+        _lib.call("eg_cross_entropy_fwd", 16, 16, 16, 16, 16, 4, 0, -100, _lib.EG_F32, None)
+    with pytest.raises(RuntimeError, match="null"):
+        _lib.call("eg_cross_entropy_bwd", None, 16, 16, 16, 16, 16, 4, 8, -100, _lib.EG_F32,
+                  None)
+    with pytest.raises(RuntimeError, match="out of range"):
+        _lib.call("eg_cross_entropy_bwd", 16, 16, 16, 16, 16, 16, (1 << 24) + 1, 8, -100,
+                  _lib.EG_BF16, None)
     # empty inputs are a no-op, not an error
     _lib.call("eg_softmax_fwd", None, None, 0, 0, _lib.EG_F32, None)
+    _lib.call("eg_cross_entropy_bwd", None, None, None, None, None, None, 0, 8, -100,
+              _lib.EG_F32, None)
 
 
 def test_pairs_refuse_cpu_tensors():

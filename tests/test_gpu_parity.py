@@ -21,7 +21,8 @@ from oracle.verify import verify
 
 pytestmark = pytest.mark.gpu
 
-MEMORY_BOUND = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "fused_add_rms_norm")
+MEMORY_BOUND = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "fused_add_rms_norm",
+                "cross_entropy")
 
 
 def _cases(names):

@@ -39,7 +39,10 @@ def test_tolerances_match_the_gate():
     for op in decls.OPS.values():
         for name in (op.output.name, *op.grad_names()):
             if "bfloat16" in op.tolerances:
-                assert op.tolerance_for(w, name) == (2e-2, 2e-2)
+                expect = (2e-2, 2e-2)
+                if op.name == "cross_entropy" and name == "dlogits":
+                    expect = (2e-2 / (4 * 8), 2e-2)  # atol scaled to the entry size
+                assert op.tolerance_for(w, name) == pytest.approx(expect)
     w32 = Workload(dims=dict(rows=4, cols=8), dtype="float32")
     assert decls.SOFTMAX.tolerance_for(w32, "dx") == (1e-5, 1e-5)
     override = Workload(dims=dict(rows=4, cols=8), dtype="float32", atol=1.0, rtol=2.0)

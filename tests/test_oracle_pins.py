@@ -388,3 +388,97 @@ def test_inputs_are_deterministic_and_follow_recipes():
     assert rr["cos"].dtype == torch.float32 and rr["x"].dtype == torch.bfloat16
     assert case_seed(Workload(dims=dict(B=1, H=1, S=1, D=1), dtype="x")) == (
         ((((1 * 131 + 1) * 131 + 1) * 131 + 1) * 131) + ord("x"))
+
+
+# ------------------------------------------------------------- cross entropy
+def _xent_brute(logits, target, ignore=-100):
+    """Pure-Python fp64 mean cross entropy over non-ignored rows."""
+    total, n = 0.0, 0
+    for row, t in zip(logits.tolist(), target.tolist()):
+        if t == ignore:
+            continue
+        top = max(row)
+        lse = top + math.log(sum(math.exp(v - top) for v in row))
+        total += lse - row[t]
+        n += 1
+    return total / n if n else float("nan")
+
+
+def test_cross_entropy_forward_closed_forms_and_brute_force():
+    # two classes, logits (0, ln 2): p = (1/3, 2/3)
+    x = torch.tensor([[0.0, math.log(2.0)]] * 2, dtype=torch.float64)
+    assert math.isclose(float(fr.cross_entropy_forward_ref(x, torch.tensor([1, 1]))),
+                        math.log(1.5), rel_tol=1e-6)
+    assert math.isclose(float(fr.cross_entropy_forward_ref(x, torch.tensor([0, 0]))),
+                        math.log(3.0), rel_tol=1e-6)
+    # equal logits: log(cols), whatever the constant and the targets
+    flat = torch.full((3, 1000), 7.25)
+    assert math.isclose(float(fr.cross_entropy_forward_ref(flat, torch.tensor([0, 500, 999]))),
+                        math.log(1000.0), rel_tol=1e-6)
+    # a dominant target logit costs ~0; a dominant other logit costs its margin
+    hot = torch.zeros(1, 9)
+    hot[0, 4] = 60.0
+    assert float(fr.cross_entropy_forward_ref(hot, torch.tensor([4]))) < 1e-6
+    assert math.isclose(float(fr.cross_entropy_forward_ref(hot, torch.tensor([2]))), 60.0,
+                        rel_tol=1e-6)
+    # brute force with ignored rows; shift invariance per row
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(7, 13, generator=g, dtype=torch.float64) * 3
+    target = torch.randint(0, 13, (7,), generator=g)
+    target[[1, 4]] = -100
+    ref = _xent_brute(logits, target)
+    assert math.isclose(float(fr.cross_entropy_forward_ref(logits, target)), ref, rel_tol=1e-6)
+    shifted = logits + torch.arange(7, dtype=torch.float64)[:, None] * 10
+    assert math.isclose(float(fr.cross_entropy_forward_ref(shifted, target)), ref, rel_tol=1e-5)
+    # every row ignored: 0/0
+    assert math.isnan(float(fr.cross_entropy_forward_ref(logits, torch.full((7,), -100))))
+    # output dtype follows the logits
+    assert fr.cross_entropy_forward_ref(logits.bfloat16(), target).dtype == torch.bfloat16
+
+
+def test_cross_entropy_gradient_fd_and_structure():
+    w = Workload(dims=dict(rows=6, cols=19), dtype="float32", extra={"ignore_every": 4})
+    inputs = _f64(make_case_inputs(decls.CROSS_ENTROPY, w, "cpu"))
+    assert inputs["target"].tolist()[0] == -100 and inputs["target"].tolist()[4] == -100
+    _fd_check(decls.CROSS_ENTROPY, inputs)
+    _, g = oracle(decls.CROSS_ENTROPY, inputs, use_reference_dtype=False)
+    d = g["dlogits"]
+    valid = inputs["target"] != -100
+    # ignored rows get nothing; valid rows sum to zero (shift invariance)
+    assert torch.count_nonzero(d[~valid]) == 0
+    assert torch.allclose(d[valid].sum(-1), torch.zeros(int(valid.sum()), dtype=d.dtype),
+                          atol=1e-7)
+    # only the target entry of a valid row is negative, and it is -(dloss/n)(1 - p_t)
+    neg = d < 0
+    assert torch.equal(neg.nonzero()[:, 1], inputs["target"][valid])
+    # dlogits / (dloss / n) + onehot is the (separately pinned) softmax of the row
+    scale = float(inputs["dloss"]) / int(valid.sum())
+    onehot = torch.nn.functional.one_hot(inputs["target"][valid], 19).to(d.dtype)
+    assert torch.allclose(d[valid] / scale + onehot,
+                          fr.softmax_forward_ref(inputs["logits"][valid]).to(d.dtype), atol=1e-6)
+    # all rows ignored: zero gradient (the NaN mean never reaches it)
+    inputs["target"] = torch.full((6,), -100)
+    _, g0 = oracle(decls.CROSS_ENTROPY, inputs, use_reference_dtype=False)
+    assert torch.count_nonzero(g0["dlogits"]) == 0
+
+
+def test_cross_entropy_inputs_and_declaration():
+    op = decls.CROSS_ENTROPY
+    w = Workload(dims=dict(rows=8, cols=512), dtype="float32")
+    a = make_case_inputs(op, w, "cpu")
+    torch.manual_seed(8 * 100003 + 512)
+    assert torch.equal(a["logits"], torch.randn(8, 512))
+    assert torch.equal(a["target"], torch.randint(0, 512, (8,), dtype=torch.int64))
+    assert torch.equal(a["dloss"], torch.rand(()) + 0.5)
+    assert op.memory_input_names() == ("logits",)
+    assert op.grad_names() == ("dlogits",) and op.upstream_grad_name == "dloss"
+    # the reference's six correctness cases are all present
+    keys = {(tuple(w.dims.values()), w.dtype) for w in op.correctness}
+    for dims, dt in (((8, 512), "float32"), ((16, 1024), "float32"),
+                     ((32, 4096), "float16"), ((64, 2048), "float16"),
+                     ((32, 4096), "bfloat16"), ((64, 2048), "bfloat16")):
+        assert (dims, dt) in keys
+    # dlogits' atol is scaled to the gradient's per-entry size
+    atol, rtol = op.tolerance_for(w, "dlogits")
+    assert atol == pytest.approx(1e-5 / (8 * 512)) and rtol == 1e-5
+    assert op.tolerance_for(w, "loss") == (1e-5, 1e-5)
