@@ -108,7 +108,8 @@ KERNELS = {
     "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_kernel"]},
     "causal_attention_gqa": {"fwd": ["attn_fwd_kernel"],
                              "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
-    "cross_entropy": {"fwd": ["xent_lse_kernel", "xent_mean_kernel"], "bwd": ["xent_bwd_kernel"]},
+    "cross_entropy": {"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
+                      "bwd": ["xent_bwd_flat_kernel"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.

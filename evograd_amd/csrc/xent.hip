@@ -12,14 +12,17 @@
 // Saved state is lse [rows] fp32 and n_valid (one fp32 count) beside the inputs.
 // Kernels:
 //   xent_lse_kernel   one workgroup per row, one HBM read of the row: 16-byte
-//                     non-temporal loads, UNROLL packs in flight per thread, an
+//                     non-temporal loads, kUnroll packs in flight per thread, an
 //                     online (max, sum of exp2) per thread, one max and one sum
-//                     over the workgroup; writes lse[row].
-//   xent_mean_kernel  one workgroup: the row losses (lse - the target logit,
-//                     one gathered element per row) summed in a fixed order, and
-//                     the count of non-ignored rows; writes the loss and n_valid.
-//   xent_bwd_kernel   (row, column chunk) grid; one read of the row chunk and one
-//                     write of dlogits, with dloss read from device memory.
+//                     over the workgroup; writes lse[row] and the row loss
+//                     lse - logits[row, target] (the target logit gathered by
+//                     thread 0) into the workspace.
+//   xent_mean_kernel  one workgroup: the row losses summed in a fixed order and
+//                     the non-ignored rows counted; writes the loss and n_valid.
+//   xent_bwd_flat_kernel  wide rows: one read of the logits and one write of
+//                     dlogits, workgroups in address order over the flattened
+//                     matrix; dloss read from device memory.
+//   xent_bwd_rows_kernel  narrow rows: one workgroup per row.
 // No atomics: every sum has a fixed order, so results are bitwise repeatable.
 //
 // A target outside [0, cols) that is not ignore_index makes that row's loss and
@@ -41,10 +44,22 @@ __device__ __forceinline__ float lse_ref(float m) { return __builtin_isinf(m) ? 
 
 template <typename T, int VEC, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void xent_lse_kernel(const T* __restrict__ x,
-                                                         float* __restrict__ lse, int cols) {
+                                                         const int64_t* __restrict__ target,
+                                                         float* __restrict__ lse,
+                                                         float* __restrict__ rowloss, int cols,
+                                                         int64_t ignore_index) {
   __shared__ float red[BLOCK / kWave];
   constexpr int STEP = BLOCK * VEC;
-  const T* __restrict__ xr = x + (int64_t)blockIdx.x * cols;
+  const int64_t row = blockIdx.x;
+  const T* __restrict__ xr = x + row * cols;
+  // The target logit is gathered before the row stream starts, so its latency
+  // overlaps the first batch of loads.
+  int64_t t = 0;
+  float picked = 0.f;
+  if (threadIdx.x == 0) {
+    t = target[row];
+    if (t != ignore_index) picked = (t >= 0 && t < cols) ? to_f32(xr[t]) : NAN;
+  }
   float m = -INFINITY;  // running max of this thread's elements
   float s = 0.f;        // sum of exp(v - lse_ref(m)) over them
   for (int base = (int)threadIdx.x * VEC; base < cols; base += STEP * kUnroll) {
@@ -84,22 +99,37 @@ __global__ __launch_bounds__(BLOCK) void xent_lse_kernel(const T* __restrict__ x
   const float part =
       (s == 0.f) ? 0.f : s * __builtin_amdgcn_exp2f((lse_ref(m) - gref) * kLog2e);
   const float total = block_reduce<BLOCK>(part, SumOp(), red);
-  if (threadIdx.x == 0) lse[blockIdx.x] = gref + log2f(total) * kLn2;
+  if (threadIdx.x == 0) {
+    const float l = gref + log2f(total) * kLn2;
+    lse[row] = l;
+    rowloss[row] = (t == ignore_index) ? 0.f : l - picked;
+  }
 }
+
+// One workgroup; each thread takes kMeanRows rows per pass with all their loads
+// issued before any is used, then a fixed-order workgroup sum.
+constexpr int kMeanRows = 8;
 
 template <typename T>
 __global__ __launch_bounds__(kMeanBlock) void xent_mean_kernel(
-    const T* __restrict__ x, const int64_t* __restrict__ target, const float* __restrict__ lse,
-    T* __restrict__ loss, float* __restrict__ n_valid, int64_t rows, int cols,
-    int64_t ignore_index) {
+    const int64_t* __restrict__ target, const float* __restrict__ rowloss, T* __restrict__ loss,
+    float* __restrict__ n_valid, int64_t rows, int64_t ignore_index) {
   __shared__ float red[kMeanBlock / kWave];
   float sum = 0.f, count = 0.f;
-  for (int64_t r = threadIdx.x; r < rows; r += kMeanBlock) {
-    const int64_t t = target[r];
-    if (t == ignore_index) continue;
-    const float picked = (t >= 0 && t < cols) ? to_f32(x[r * cols + t]) : NAN;
-    sum += lse[r] - picked;
-    count += 1.f;
+  for (int64_t r0 = threadIdx.x; r0 < rows; r0 += (int64_t)kMeanBlock * kMeanRows) {
+    float l[kMeanRows], ok[kMeanRows];
+#pragma unroll
+    for (int j = 0; j < kMeanRows; ++j) {
+      const int64_t r = r0 + (int64_t)j * kMeanBlock;
+      const bool in = r < rows;
+      ok[j] = (in && target[r] != ignore_index) ? 1.f : 0.f;
+      l[j] = in ? rowloss[r] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kMeanRows; ++j) {
+      sum += l[j];
+      count += ok[j];
+    }
   }
   sum = block_reduce<kMeanBlock>(sum, SumOp(), red);
   count = block_reduce<kMeanBlock>(count, SumOp(), red);
@@ -109,48 +139,115 @@ __global__ __launch_bounds__(kMeanBlock) void xent_mean_kernel(
   }
 }
 
+// Per-row factors of the backward: g = dloss / n_valid (NaN for an out-of-range
+// target), lse in log2 units, the target column, and whether the row is ignored.
+struct RowGrad {
+  float g, ll;
+  int tc;
+  bool ignored;
+};
+
+template <typename T>
+__device__ __forceinline__ RowGrad row_grad(const T* __restrict__ dloss,
+                                            const int64_t* __restrict__ target,
+                                            const float* __restrict__ lse,
+                                            const float* __restrict__ n_valid, int64_t row,
+                                            int cols, int64_t ignore_index) {
+  const int64_t t = target[row];
+  RowGrad r;
+  r.ignored = t == ignore_index;
+  r.g = (t >= 0 && t < cols) ? to_f32(dloss[0]) / n_valid[0] : NAN;
+  r.ll = lse[row] * kLog2e;
+  r.tc = (int)t;
+  return r;
+}
+
+// dlogits of one pack of VEC columns starting at column c of a row.
+template <int VEC>
+__device__ __forceinline__ void grad_pack(const RowGrad& rg, int c, const float (&v)[VEC],
+                                          float (&o)[VEC]) {
+  if (rg.ignored) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) o[i] = 0.f;
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+    o[i] = rg.g * __builtin_amdgcn_exp2f(__builtin_fmaf(v[i], kLog2e, -rg.ll));
+  const unsigned k = (unsigned)(rg.tc - c);
+  if (k < (unsigned)VEC) {
+    // the target column: g * (p - 1)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i)
+      if (i == (int)k) o[i] -= rg.g;
+  }
+}
+
+// Wide rows: the matrix as one flat sequence of packs, workgroup b covering
+// packs [b * PER, (b + 1) * PER) in address order, so the workgroups in flight
+// stream through contiguous memory. A workgroup spans at most two rows
+// (packs per row >= PER, checked by the host).
+constexpr int kFlatBlock = 512;
+constexpr int kFlatUnroll = 2;
+constexpr int kFlatPer = kFlatBlock * kFlatUnroll;
+
 template <typename T, int VEC, bool NT>
-__global__ __launch_bounds__(kBwdBlock) void xent_bwd_kernel(
+__global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
+    const T* __restrict__ dloss, const T* __restrict__ x, const int64_t* __restrict__ target,
+    const float* __restrict__ lse, const float* __restrict__ n_valid, T* __restrict__ dx,
+    int64_t rows, int cols, int64_t ignore_index) {
+  const int64_t ppr = cols / VEC;  // packs per row
+  const int64_t npack = rows * ppr;
+  const int64_t first = (int64_t)blockIdx.x * kFlatPer;
+  const int64_t row0 = first / ppr;
+  const int64_t bound = (row0 + 1) * ppr;  // first pack of the next row
+  const RowGrad r0 = row_grad(dloss, target, lse, n_valid, row0, cols, ignore_index);
+  const bool two = first + kFlatPer > bound && row0 + 1 < rows;
+  const RowGrad r1 = two ? row_grad(dloss, target, lse, n_valid, row0 + 1, cols, ignore_index)
+                         : r0;
+  float v[kFlatUnroll][VEC];
+#pragma unroll
+  for (int u = 0; u < kFlatUnroll; ++u) {
+    const int64_t p = first + u * kFlatBlock + threadIdx.x;
+    if (p < npack) load_vec<T, VEC, NT>(x + p * VEC, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kFlatUnroll; ++u) {
+    const int64_t p = first + u * kFlatBlock + threadIdx.x;
+    if (p < npack) {
+      const bool hi = p >= bound;
+      const int c = (int)((hi ? p - bound : p - row0 * ppr) * VEC);
+      float o[VEC];
+      grad_pack<VEC>(hi ? r1 : r0, c, v[u], o);
+      store_vec<T, VEC, NT>(dx + p * VEC, o);
+    }
+  }
+}
+
+// Narrow rows (fewer packs than one flat workgroup covers): a (row, chunk) grid.
+template <typename T, int VEC, bool NT>
+__global__ __launch_bounds__(kBwdBlock) void xent_bwd_rows_kernel(
     const T* __restrict__ dloss, const T* __restrict__ x, const int64_t* __restrict__ target,
     const float* __restrict__ lse, const float* __restrict__ n_valid, T* __restrict__ dx,
     int cols, int64_t ignore_index) {
   constexpr int STEP = kBwdBlock * VEC;
   const int64_t row = blockIdx.x;
-  const int64_t t = target[row];
+  const RowGrad rg = row_grad(dloss, target, lse, n_valid, row, cols, ignore_index);
   const int c0 = (int)blockIdx.y * (STEP * kUnroll) + (int)threadIdx.x * VEC;
-  T* __restrict__ dr = dx + row * cols;
-  if (t == ignore_index) {
-    float z[VEC];
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) z[i] = 0.f;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int c = c0 + u * STEP;
-      if (c < cols) store_vec<T, VEC, NT>(dr + c, z);
-    }
-    return;
-  }
-  // The reference's mean divides by the non-ignored count: g = dloss / n.
-  const float g = (t >= 0 && t < cols) ? to_f32(dloss[0]) / n_valid[0] : NAN;
-  const float ll = lse[row] * kLog2e;
-  const int tc = (int)t;
   const T* __restrict__ xr = x + row * cols;
+  T* __restrict__ dr = dx + row * cols;
   float v[kUnroll][VEC];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int c = c0 + u * STEP;
-    if (c < cols) load_vec<T, VEC, NT>(xr + c, v[u]);
+    if (c < cols && !rg.ignored) load_vec<T, VEC, NT>(xr + c, v[u]);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int c = c0 + u * STEP;
     if (c < cols) {
       float o[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(v[u][i], kLog2e, -ll));
-        o[i] = g * (c + i == tc ? p - 1.f : p);
-      }
+      grad_pack<VEC>(rg, c, v[u], o);
       store_vec<T, VEC, NT>(dr + c, o);
     }
   }
@@ -170,12 +267,30 @@ void pick_lse_block(int64_t npack, Launch&& launch) {
 
 template <typename T, int VEC>
 struct LseLaunch {
-  const T* x; float* lse; int64_t rows; int cols; hipStream_t st;
+  const T* x; const int64_t* target; float* lse; float* rowloss; int64_t rows; int cols;
+  int64_t ignore_index; hipStream_t st;
   template <int BLOCK> void go() {
     EG_LAUNCH((xent_lse_kernel<T, VEC, BLOCK, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
-              dim3(BLOCK), 0, st, x, lse, cols);
+              dim3(BLOCK), 0, st, x, target, lse, rowloss, cols, ignore_index);
   }
 };
+
+template <typename T, int VEC>
+void launch_bwd(const T* gp, const T* xp, const int64_t* target, const float* lse,
+                const float* n_valid, T* dp, int64_t rows, int cols, int64_t ignore_index,
+                hipStream_t st) {
+  constexpr bool NT = VEC * sizeof(T) == 16;
+  const int64_t ppr = cols / VEC;
+  if (ppr >= kFlatPer) {
+    const int64_t blocks = (rows * ppr + kFlatPer - 1) / kFlatPer;
+    EG_LAUNCH((xent_bwd_flat_kernel<T, VEC, NT>), dim3((unsigned)blocks), dim3(kFlatBlock), 0,
+              st, gp, xp, target, lse, n_valid, dp, rows, cols, ignore_index);
+  } else {
+    const int64_t chunks = (ppr + kBwdBlock * kUnroll - 1) / (kBwdBlock * kUnroll);
+    EG_LAUNCH((xent_bwd_rows_kernel<T, VEC, NT>), dim3((unsigned)rows, (unsigned)chunks),
+              dim3(kBwdBlock), 0, st, gp, xp, target, lse, n_valid, dp, cols, ignore_index);
+  }
+}
 
 int check_xent(const char* what, int64_t rows, int64_t cols) {
   if (rows < 0 || cols < 0) {
@@ -200,30 +315,38 @@ int check_xent(const char* what, int64_t rows, int64_t cols) {
 
 using namespace eg;
 
+extern "C" size_t eg_cross_entropy_workspace_bytes(int64_t rows) {
+  return rows > 0 ? (size_t)rows * sizeof(float) : 0;
+}
+
 extern "C" int eg_cross_entropy_fwd(const void* logits, const int64_t* target, void* loss,
-                                    float* lse, float* n_valid, int64_t rows, int64_t cols,
-                                    int64_t ignore_index, int dtype, void* stream) {
+                                    float* lse, float* n_valid, void* workspace, int64_t rows,
+                                    int64_t cols, int64_t ignore_index, int dtype,
+                                    void* stream) {
   clear_error();
   if (check_xent("eg_cross_entropy_fwd", rows, cols)) return 1;
-  if (!loss || !n_valid || (rows > 0 && (!logits || !target || !lse))) {
+  if (!loss || !n_valid || (rows > 0 && (!logits || !target || !lse || !workspace))) {
     set_error("eg_cross_entropy_fwd: null pointer");
     return 1;
   }
   hipStream_t st = as_stream(stream);
+  float* rowloss = static_cast<float*>(workspace);
   return EG_DISPATCH_FLOAT(dtype, "eg_cross_entropy_fwd", [&] {
     using T = scalar_t;
     constexpr int V = 16 / sizeof(T);
     const T* xp = static_cast<const T*>(logits);
     if (rows > 0) {
       if (cols % V == 0 && aligned16(logits)) {
-        pick_lse_block(cols / V, LseLaunch<T, V>{xp, lse, rows, (int)cols, st});
+        pick_lse_block(cols / V, LseLaunch<T, V>{xp, target, lse, rowloss, rows, (int)cols,
+                                                 ignore_index, st});
       } else {
-        pick_lse_block(cols, LseLaunch<T, 1>{xp, lse, rows, (int)cols, st});
+        pick_lse_block(cols, LseLaunch<T, 1>{xp, target, lse, rowloss, rows, (int)cols,
+                                             ignore_index, st});
       }
     }
     // Also for rows == 0: the mean of no rows is 0/0 (NaN), as in torch.
-    EG_LAUNCH((xent_mean_kernel<T>), dim3(1), dim3(kMeanBlock), 0, st, xp, target, lse,
-              static_cast<T*>(loss), n_valid, rows, (int)cols, ignore_index);
+    EG_LAUNCH((xent_mean_kernel<T>), dim3(1), dim3(kMeanBlock), 0, st, target, rowloss,
+              static_cast<T*>(loss), n_valid, rows, ignore_index);
     return check_launch("eg_cross_entropy_fwd");
   });
 }
@@ -240,8 +363,10 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
     set_error("eg_cross_entropy_bwd: null pointer");
     return 1;
   }
-  if ((cols + kBwdBlock * kUnroll - 1) / (kBwdBlock * kUnroll) > 65535) {
-    set_error("eg_cross_entropy_bwd: cols=%lld exceeds the column-chunk grid", (long long)cols);
+  // flat grid: at most 2^32 threads in x
+  if (rows * cols / kFlatPer >= ((int64_t)1 << 32) / kFlatBlock) {
+    set_error("eg_cross_entropy_bwd: rows*cols=%lld exceeds the launch grid",
+              (long long)(rows * cols));
     return 1;
   }
   hipStream_t st = as_stream(stream);
@@ -251,17 +376,10 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
     const T* gp = static_cast<const T*>(dloss);
     const T* xp = static_cast<const T*>(logits);
     T* dp = static_cast<T*>(dlogits);
-    if (cols % V == 0 && aligned16(logits) && aligned16(dlogits)) {
-      const int64_t chunks = (cols + kBwdBlock * V * kUnroll - 1) / (kBwdBlock * V * kUnroll);
-      EG_LAUNCH((xent_bwd_kernel<T, V, V * sizeof(T) == 16>),
-                dim3((unsigned)rows, (unsigned)chunks), dim3(kBwdBlock), 0, st, gp, xp, target,
-                lse, n_valid, dp, (int)cols, ignore_index);
-    } else {
-      const int64_t chunks = (cols + kBwdBlock * kUnroll - 1) / (kBwdBlock * kUnroll);
-      EG_LAUNCH((xent_bwd_kernel<T, 1, false>), dim3((unsigned)rows, (unsigned)chunks),
-                dim3(kBwdBlock), 0, st, gp, xp, target, lse, n_valid, dp, (int)cols,
-                ignore_index);
-    }
+    if (cols % V == 0 && aligned16(logits) && aligned16(dlogits))
+      launch_bwd<T, V>(gp, xp, target, lse, n_valid, dp, rows, (int)cols, ignore_index, st);
+    else
+      launch_bwd<T, 1>(gp, xp, target, lse, n_valid, dp, rows, (int)cols, ignore_index, st);
     return check_launch("eg_cross_entropy_bwd");
   });
 }

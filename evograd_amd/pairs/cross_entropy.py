@@ -17,7 +17,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._util import as_contiguous, tag
+from ._util import as_contiguous, tag, workspace
 
 IGNORE_INDEX = -100
 
@@ -41,9 +41,10 @@ def cross_entropy_forward_with_saved(logits: torch.Tensor, target: torch.Tensor)
     rows, cols = logits.shape
     loss = torch.empty((), dtype=logits.dtype, device=logits.device)
     stats = torch.empty(rows + 1, dtype=torch.float32, device=logits.device)
+    ws = workspace(_lib.query("eg_cross_entropy_workspace_bytes", rows), logits.device)
     base = stats.data_ptr()
     _lib.call("eg_cross_entropy_fwd", _lib.ptr(logits), _lib.ptr(target), _lib.ptr(loss), base,
-              base + 4 * rows, rows, cols, IGNORE_INDEX, tag(logits.dtype),
+              base + 4 * rows, _lib.ptr(ws), rows, cols, IGNORE_INDEX, tag(logits.dtype),
               _lib.stream_of(logits))
     return loss, (logits, target, stats)
 

@@ -209,10 +209,14 @@ int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* 
  * logits [rows, cols] (dtype); target [rows] int64; loss one element (dtype).
  * Saved: lse [rows] fp32 (logsumexp of each row) and n_valid, one fp32 (the
  * number of rows whose target != ignore_index). A target outside [0, cols) that
- * is not ignore_index makes the loss NaN. rows == 0 gives NaN (0/0), as torch. */
+ * is not ignore_index makes the loss NaN. rows == 0 gives NaN (0/0), as torch.
+ * Workspace: eg_cross_entropy_workspace_bytes(rows). */
 int eg_cross_entropy_fwd(const void* logits, const int64_t* target, void* loss, float* lse,
-                         float* n_valid, int64_t rows, int64_t cols, int64_t ignore_index,
-                         int dtype, void* stream);
+                         float* n_valid, void* workspace, int64_t rows, int64_t cols,
+                         int64_t ignore_index, int dtype, void* stream);
+
+/* Bytes of workspace eg_cross_entropy_fwd needs: one fp32 row loss per row. */
+size_t eg_cross_entropy_workspace_bytes(int64_t rows);
 
 /* Backward of eg_cross_entropy_fwd, the rule declared at
  * src/evograd/ops/level1/cross_entropy/__init__.py:91-94:

@@ -47,6 +47,7 @@ def test_library_loads_and_exports_every_symbol():
     assert lib.eg_rmsnorm_workspace_bytes(16384, 64) == 2048 * 64 * 4
     assert lib.eg_layernorm_workspace_bytes(3, 64) == 2 * 3 * 64 * 4
     assert lib.eg_rmsnorm_workspace_bytes(0, 64) == 0
+    assert lib.eg_cross_entropy_workspace_bytes(8192) == 8192 * 4
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
@@ -59,7 +60,7 @@ def test_host_side_validation_errors_without_gpu():
     with pytest.raises(RuntimeError, match="dtype"):
         _lib.call("eg_swiglu_fwd", 16, 16, 16, 8, 7, None)
     with pytest.raises(RuntimeError, match="zero classes"):
-        _lib.call("eg_cross_entropy_fwd", 16, 16, 16, 16, 16, 4, 0, -100, _lib.EG_F32, None)
+        _lib.call("eg_cross_entropy_fwd", 16, 16, 16, 16, 16, 16, 4, 0, -100, _lib.EG_F32, None)
     with pytest.raises(RuntimeError, match="null"):
         _lib.call("eg_cross_entropy_bwd", None, 16, 16, 16, 16, 16, 4, 8, -100, _lib.EG_F32,
                   None)
