@@ -41,7 +41,8 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
 ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
-           "fused_add_rms_norm", "causal_attention_gqa", "cross_entropy")
+           "fused_add_rms_norm", "causal_attention_gqa", "cross_entropy",
+           "fused_linear_cross_entropy")
 
 
 def log(msg: str) -> None:
@@ -84,6 +85,11 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
         R, C = d["rows"], d["cols"]
         n = R * C * es
         return {"unit": "bytes", "fwd": n + 8 * R + 4 * R + es, "bwd": 2 * n + 8 * R + 4 * R}
+    if name == "fused_linear_cross_entropy":
+        # three rows x hidden x vocab products, all in the forward (the backward
+        # only scales the saved gradients)
+        R, Hd, V = d["rows"], d["hidden"], d["vocab"]
+        return {"unit": "flops", "fwd": 3 * 2.0 * R * Hd * V, "bwd": 0.0}
     if name == "rope":
         B, H, T, D = d["B"], d["n_heads"], d["T"], d["head_dim"]
         xb = B * (H + extra_k_heads) * T * D * es
@@ -110,6 +116,9 @@ KERNELS = {
                              "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
     "cross_entropy": {"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
                       "bwd": ["xent_bwd_flat_kernel"]},
+    # first chunk's launches of the forward; the backward's dx scaling
+    "fused_linear_cross_entropy": {"fwd": ["xent_lse_kernel", "xent_bwd_flat_kernel"],
+                                   "bwd": ["scale_copy_kernel"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.
@@ -118,6 +127,7 @@ DOMINANT = {
     "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
     "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
     "cross_entropy": ("bwd", 0),
+    "fused_linear_cross_entropy": ("fwd", 1),
 }
 
 
@@ -125,6 +135,13 @@ def dominant_work(name: str, w, work: dict) -> float:
     """Algorithmic bytes (or FLOPs) of one launch of the op's dominant kernel."""
     d = w.dims
     es = {"float32": 4, "float16": 2, "bfloat16": 2}[w.dtype]
+    if name == "fused_linear_cross_entropy":
+        # the unit-gradient kernel of one chunk: reads the chunk's fp32 logits,
+        # writes dlogits in the input dtype (the GEMMs are the library's)
+        from evograd_amd.pairs.fused_linear_cross_entropy import chunk_rows
+
+        rc = chunk_rows(d["rows"], d["vocab"])
+        return rc * d["vocab"] * (4 + es) + rc * 12
     if name == "rmsnorm":  # the column sum writes dweight
         return work["bwd"] - d["hidden"] * es
     if name == "fused_add_rms_norm":
@@ -250,7 +267,8 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     kname = KERNELS[name][phase][idx]
     k_us = kt[f"{phase}:{kname}"]
     k_work = dominant_work(name, w, work)
-    if work["unit"] == "bytes":
+    k_unit = "bytes" if name == "fused_linear_cross_entropy" else work["unit"]
+    if k_unit == "bytes":
         k_rate = k_work / (k_us * 1e-6) / 1e9
         out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "bytes": k_work,
                                   "achieved_gbs": k_rate, "frac": k_rate / HBM_PEAK_GBS}
@@ -294,8 +312,13 @@ def cpu_baseline(name: str) -> dict:
     op = decls.get_op(name)
     w = op.benchmark[0]
     d = dict(w.dims)
-    if name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm",
-                "cross_entropy"):
+    if name == "fused_linear_cross_entropy":
+        full_rows = d["rows"]
+        d["rows"] = 64
+        scale = full_rows / d["rows"]
+        sample = f"{d['rows']} of {full_rows} rows"
+    elif name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm",
+                  "cross_entropy"):
         full_rows = d["rows"]
         d["rows"] = max(1, full_rows // 8)
         scale = full_rows / d["rows"]

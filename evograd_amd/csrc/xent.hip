@@ -29,6 +29,8 @@
 // gradient NaN (torch raises there); it is never used as an index.
 #include "eg_common.hpp"
 
+#include <algorithm>
+
 namespace eg {
 namespace {
 
@@ -139,16 +141,18 @@ __global__ __launch_bounds__(kMeanBlock) void xent_mean_kernel(
   }
 }
 
-// Per-row factors of the backward: g = dloss / n_valid (NaN for an out-of-range
-// target), lse in log2 units, the target column, and whether the row is ignored.
+// Per-row factors of the backward: g = dloss / n_valid, or 1 when dloss is null
+// (the unit gradient softmax - onehot of the fused linear cross entropy); NaN
+// for an out-of-range target. Also lse in log2 units, the target column, and
+// whether the row is ignored.
 struct RowGrad {
   float g, ll;
   int tc;
   bool ignored;
 };
 
-template <typename T>
-__device__ __forceinline__ RowGrad row_grad(const T* __restrict__ dloss,
+template <typename TD>
+__device__ __forceinline__ RowGrad row_grad(const TD* __restrict__ dloss,
                                             const int64_t* __restrict__ target,
                                             const float* __restrict__ lse,
                                             const float* __restrict__ n_valid, int64_t row,
@@ -156,7 +160,8 @@ __device__ __forceinline__ RowGrad row_grad(const T* __restrict__ dloss,
   const int64_t t = target[row];
   RowGrad r;
   r.ignored = t == ignore_index;
-  r.g = (t >= 0 && t < cols) ? to_f32(dloss[0]) / n_valid[0] : NAN;
+  const float g = dloss ? to_f32(dloss[0]) / n_valid[0] : 1.f;
+  r.g = (t >= 0 && t < cols) ? g : NAN;
   r.ll = lse[row] * kLog2e;
   r.tc = (int)t;
   return r;
@@ -186,15 +191,16 @@ __device__ __forceinline__ void grad_pack(const RowGrad& rg, int c, const float 
 // Wide rows: the matrix as one flat sequence of packs, workgroup b covering
 // packs [b * PER, (b + 1) * PER) in address order, so the workgroups in flight
 // stream through contiguous memory. A workgroup spans at most two rows
-// (packs per row >= PER, checked by the host).
+// (packs per row >= PER, checked by the host). TI is the logits type, TO the
+// gradient's, TD the type of dloss.
 constexpr int kFlatBlock = 512;
 constexpr int kFlatUnroll = 2;
 constexpr int kFlatPer = kFlatBlock * kFlatUnroll;
 
-template <typename T, int VEC, bool NT>
+template <typename TI, typename TO, typename TD, int VEC, bool NT>
 __global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
-    const T* __restrict__ dloss, const T* __restrict__ x, const int64_t* __restrict__ target,
-    const float* __restrict__ lse, const float* __restrict__ n_valid, T* __restrict__ dx,
+    const TD* __restrict__ dloss, const TI* __restrict__ x, const int64_t* __restrict__ target,
+    const float* __restrict__ lse, const float* __restrict__ n_valid, TO* __restrict__ dx,
     int64_t rows, int cols, int64_t ignore_index) {
   const int64_t ppr = cols / VEC;  // packs per row
   const int64_t npack = rows * ppr;
@@ -209,7 +215,7 @@ __global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
 #pragma unroll
   for (int u = 0; u < kFlatUnroll; ++u) {
     const int64_t p = first + u * kFlatBlock + threadIdx.x;
-    if (p < npack) load_vec<T, VEC, NT>(x + p * VEC, v[u]);
+    if (p < npack) load_vec<TI, VEC, NT>(x + p * VEC, v[u]);
   }
 #pragma unroll
   for (int u = 0; u < kFlatUnroll; ++u) {
@@ -219,28 +225,28 @@ __global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
       const int c = (int)((hi ? p - bound : p - row0 * ppr) * VEC);
       float o[VEC];
       grad_pack<VEC>(hi ? r1 : r0, c, v[u], o);
-      store_vec<T, VEC, NT>(dx + p * VEC, o);
+      store_vec<TO, VEC, NT>(dx + p * VEC, o);
     }
   }
 }
 
-// Narrow rows (fewer packs than one flat workgroup covers): a (row, chunk) grid.
-template <typename T, int VEC, bool NT>
+// Narrow rows (fewer packs than one flat workgroup covers): one workgroup per row.
+template <typename TI, typename TO, typename TD, int VEC, bool NT>
 __global__ __launch_bounds__(kBwdBlock) void xent_bwd_rows_kernel(
-    const T* __restrict__ dloss, const T* __restrict__ x, const int64_t* __restrict__ target,
-    const float* __restrict__ lse, const float* __restrict__ n_valid, T* __restrict__ dx,
+    const TD* __restrict__ dloss, const TI* __restrict__ x, const int64_t* __restrict__ target,
+    const float* __restrict__ lse, const float* __restrict__ n_valid, TO* __restrict__ dx,
     int cols, int64_t ignore_index) {
   constexpr int STEP = kBwdBlock * VEC;
   const int64_t row = blockIdx.x;
   const RowGrad rg = row_grad(dloss, target, lse, n_valid, row, cols, ignore_index);
   const int c0 = (int)blockIdx.y * (STEP * kUnroll) + (int)threadIdx.x * VEC;
-  const T* __restrict__ xr = x + row * cols;
-  T* __restrict__ dr = dx + row * cols;
+  const TI* __restrict__ xr = x + row * cols;
+  TO* __restrict__ dr = dx + row * cols;
   float v[kUnroll][VEC];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int c = c0 + u * STEP;
-    if (c < cols && !rg.ignored) load_vec<T, VEC, NT>(xr + c, v[u]);
+    if (c < cols && !rg.ignored) load_vec<TI, VEC, NT>(xr + c, v[u]);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -248,8 +254,26 @@ __global__ __launch_bounds__(kBwdBlock) void xent_bwd_rows_kernel(
     if (c < cols) {
       float o[VEC];
       grad_pack<VEC>(rg, c, v[u], o);
-      store_vec<T, VEC, NT>(dr + c, o);
+      store_vec<TO, VEC, NT>(dr + c, o);
     }
+  }
+}
+
+// dst[i] = src[i] * mul[0] / div[0] (either factor optional), 16-byte loads when
+// the source allows them.
+template <typename TS, typename TO, typename TM, int VEC>
+__global__ __launch_bounds__(256) void scale_copy_kernel(const TS* __restrict__ src,
+                                                         TO* __restrict__ dst, int64_t npack,
+                                                         const TM* __restrict__ mul,
+                                                         const float* __restrict__ div) {
+  const float f = (mul ? to_f32(mul[0]) : 1.f) / (div ? div[0] : 1.f);
+  for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < npack;
+       p += (int64_t)gridDim.x * 256) {
+    float v[VEC];
+    load_vec<TS, VEC, VEC * sizeof(TS) == 16>(src + p * VEC, v);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[i] *= f;
+    store_vec<TO, VEC, VEC * sizeof(TO) == 16>(dst + p * VEC, v);
   }
 }
 
@@ -275,19 +299,19 @@ struct LseLaunch {
   }
 };
 
-template <typename T, int VEC>
-void launch_bwd(const T* gp, const T* xp, const int64_t* target, const float* lse,
-                const float* n_valid, T* dp, int64_t rows, int cols, int64_t ignore_index,
+template <typename TI, typename TO, typename TD, int VEC>
+void launch_bwd(const TD* gp, const TI* xp, const int64_t* target, const float* lse,
+                const float* n_valid, TO* dp, int64_t rows, int cols, int64_t ignore_index,
                 hipStream_t st) {
-  constexpr bool NT = VEC * sizeof(T) == 16;
+  constexpr bool NT = VEC * sizeof(TI) == 16;
   const int64_t ppr = cols / VEC;
   if (ppr >= kFlatPer) {
     const int64_t blocks = (rows * ppr + kFlatPer - 1) / kFlatPer;
-    EG_LAUNCH((xent_bwd_flat_kernel<T, VEC, NT>), dim3((unsigned)blocks), dim3(kFlatBlock), 0,
-              st, gp, xp, target, lse, n_valid, dp, rows, cols, ignore_index);
+    EG_LAUNCH((xent_bwd_flat_kernel<TI, TO, TD, VEC, NT>), dim3((unsigned)blocks),
+              dim3(kFlatBlock), 0, st, gp, xp, target, lse, n_valid, dp, rows, cols,
+              ignore_index);
   } else {
-    const int64_t chunks = (ppr + kBwdBlock * kUnroll - 1) / (kBwdBlock * kUnroll);
-    EG_LAUNCH((xent_bwd_rows_kernel<T, VEC, NT>), dim3((unsigned)rows, (unsigned)chunks),
+    EG_LAUNCH((xent_bwd_rows_kernel<TI, TO, TD, VEC, NT>), dim3((unsigned)rows, 1u),
               dim3(kBwdBlock), 0, st, gp, xp, target, lse, n_valid, dp, cols, ignore_index);
   }
 }
@@ -377,9 +401,129 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
     const T* xp = static_cast<const T*>(logits);
     T* dp = static_cast<T*>(dlogits);
     if (cols % V == 0 && aligned16(logits) && aligned16(dlogits))
-      launch_bwd<T, V>(gp, xp, target, lse, n_valid, dp, rows, (int)cols, ignore_index, st);
+      launch_bwd<T, T, T, V>(gp, xp, target, lse, n_valid, dp, rows, (int)cols, ignore_index,
+                             st);
     else
-      launch_bwd<T, 1>(gp, xp, target, lse, n_valid, dp, rows, (int)cols, ignore_index, st);
+      launch_bwd<T, T, T, 1>(gp, xp, target, lse, n_valid, dp, rows, (int)cols, ignore_index,
+                             st);
     return check_launch("eg_cross_entropy_bwd");
+  });
+}
+
+// ------------------------------------------------ fused linear cross entropy
+// The chunked fused linear cross entropy of
+// src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152 runs, per row
+// chunk, the projection on the library GEMM and these two steps on the chunk's
+// fp32 logits; the mean and the final scaling use the entries below.
+
+namespace eg {
+namespace {
+
+template <typename F>
+int dispatch_type(int dtype, const char* what, F&& f) {
+  switch (dtype) {
+    case EG_F32: return f(float{});
+    case EG_F16: return f(f16_t{});
+    case EG_BF16: return f(bf16_t{});
+    default: set_error("%s: unsupported dtype %d", what, dtype); return 1;
+  }
+}
+
+}  // namespace
+}  // namespace eg
+
+extern "C" int eg_flce_chunk(const float* logits, const int64_t* target, float* lse,
+                             float* rowloss, void* dlogits, int64_t rows, int64_t cols,
+                             int64_t ignore_index, int grad_dtype, void* stream) {
+  clear_error();
+  if (check_xent("eg_flce_chunk", rows, cols)) return 1;
+  if (rows == 0) return 0;
+  if (!logits || !target || !lse || !rowloss || !dlogits) {
+    set_error("eg_flce_chunk: null pointer");
+    return 1;
+  }
+  if (rows * cols / kFlatPer >= ((int64_t)1 << 32) / kFlatBlock) {
+    set_error("eg_flce_chunk: rows*cols=%lld exceeds the launch grid", (long long)(rows * cols));
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  return dispatch_type(grad_dtype, "eg_flce_chunk", [&](auto tag) {
+    using TO = decltype(tag);
+    TO* dp = static_cast<TO*>(dlogits);
+    const float* none = nullptr;
+    if (cols % 4 == 0 && aligned16(logits)) {
+      pick_lse_block(cols / 4, LseLaunch<float, 4>{logits, target, lse, rowloss, rows, (int)cols,
+                                                   ignore_index, st});
+      launch_bwd<float, TO, float, 4>(none, logits, target, lse, nullptr, dp, rows, (int)cols,
+                                      ignore_index, st);
+    } else {
+      pick_lse_block(cols, LseLaunch<float, 1>{logits, target, lse, rowloss, rows, (int)cols,
+                                               ignore_index, st});
+      launch_bwd<float, TO, float, 1>(none, logits, target, lse, nullptr, dp, rows, (int)cols,
+                                      ignore_index, st);
+    }
+    return check_launch("eg_flce_chunk");
+  });
+}
+
+extern "C" int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* loss,
+                                     float* n_valid, int64_t rows, int64_t ignore_index,
+                                     int loss_dtype, void* stream) {
+  clear_error();
+  if (rows < 0 || rows > ((int64_t)1 << 24)) {
+    set_error("eg_cross_entropy_mean: rows=%lld out of range", (long long)rows);
+    return 1;
+  }
+  if (!loss || !n_valid || (rows > 0 && (!target || !rowloss))) {
+    set_error("eg_cross_entropy_mean: null pointer");
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  return dispatch_type(loss_dtype, "eg_cross_entropy_mean", [&](auto tag) {
+    using T = decltype(tag);
+    EG_LAUNCH((xent_mean_kernel<T>), dim3(1), dim3(kMeanBlock), 0, st, target, rowloss,
+              static_cast<T*>(loss), n_valid, rows, ignore_index);
+    return check_launch("eg_cross_entropy_mean");
+  });
+}
+
+extern "C" int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype,
+                             int64_t n, const void* mul, int mul_dtype, const float* div,
+                             void* stream) {
+  clear_error();
+  if (n < 0) {
+    set_error("eg_scale_copy: negative size %lld", (long long)n);
+    return 1;
+  }
+  if (n == 0) return 0;
+  if (!src || !dst) {
+    set_error("eg_scale_copy: null pointer");
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  const int blocks = device_cus() * 8;
+  return dispatch_type(src_dtype, "eg_scale_copy", [&](auto stag) {
+    using TS = decltype(stag);
+    return dispatch_type(dst_dtype, "eg_scale_copy", [&](auto dtag) {
+      using TO = decltype(dtag);
+      return dispatch_type(mul_dtype, "eg_scale_copy", [&](auto mtag) {
+        using TM = decltype(mtag);
+        constexpr int V = 16 / sizeof(TS);
+        const TS* sp = static_cast<const TS*>(src);
+        TO* dp = static_cast<TO*>(dst);
+        const TM* mp = static_cast<const TM*>(mul);
+        if (n % V == 0 && aligned16(src) && ((uintptr_t)dst % (V * sizeof(TO))) == 0) {
+          const int64_t np = n / V;
+          const unsigned g = (unsigned)std::min<int64_t>(blocks, (np + 255) / 256);
+          EG_LAUNCH((scale_copy_kernel<TS, TO, TM, V>), dim3(g), dim3(256), 0, st, sp, dp, np, mp,
+                    div);
+        } else {
+          const unsigned g = (unsigned)std::min<int64_t>(blocks, (n + 255) / 256);
+          EG_LAUNCH((scale_copy_kernel<TS, TO, TM, 1>), dim3(g), dim3(256), 0, st, sp, dp, n, mp,
+                    div);
+        }
+        return check_launch("eg_scale_copy");
+      });
+    });
   });
 }

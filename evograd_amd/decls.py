@@ -11,6 +11,7 @@ drop-in the reference's harness looks up:
 * rope       src/evograd/ops/level1/rope/__init__.py:98-162
 * fused_add_rms_norm  src/evograd/ops/level2/fused_add_rms_norm/__init__.py:76-122
 * cross_entropy  src/evograd/ops/level1/cross_entropy/__init__.py:76-111
+* fused_linear_cross_entropy  src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152
 * causal_attention: the reference has no standalone declaration; its semantics
   are F.scaled_dot_product_attention(q, k, v, is_causal=True) inside
   src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-108. It is
@@ -431,10 +432,70 @@ CROSS_ENTROPY = declare_op(
     regime_split=LLAMA_VOCAB_REGIME_SPLIT,
 )
 
+# ------------------------------------------------ fused_linear_cross_entropy
+# src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152. Like the
+# reference declaration there is no reference_dtype: the forward widens x and
+# weight itself and returns an fp32 loss, and the gradients come back in the
+# inputs' dtypes. dx entries scale as 1/rows and dweight entries as 1/vocab
+# (a softmax probability times an x entry), so their atols are scaled by those.
+def _flce_tolerance(workload, result_name, atol, rtol):
+    if result_name == "dx":
+        atol = atol / workload.dims["rows"]
+    elif result_name == "dweight":
+        atol = atol / workload.dims["vocab"]
+    return atol, rtol
+
+
+FUSED_LINEAR_CROSS_ENTROPY = declare_op(
+    name="fused_linear_cross_entropy",
+    forward="oracle.forward_refs:fused_linear_cross_entropy_forward_ref",
+    dims=("rows", "hidden", "vocab"),
+    args=(
+        Active("x", "[rows, hidden]"),
+        Active("weight", "[vocab, hidden]"),
+        Inactive("target", "[rows]", dtype="int64"),
+    ),
+    output=Active("loss", "[]"),
+    forward_semantics=(
+        "logits = x @ weight.T, mean hard-label cross entropy against target with "
+        "ignore_index=-100; projection and logsumexp accumulated in fp32; the "
+        "[rows, vocab] logits are never materialised in full."
+    ),
+    backward_semantics=(
+        "dlogits = dloss * (softmax(logits) - onehot(target)) / n_valid; dx = dlogits @ "
+        "weight, dweight = dlogits.T @ x, in the inputs' dtypes, fp32 accumulation."
+    ),
+    correctness=tuple(
+        Workload(dims=dict(rows=r, hidden=h, vocab=v), dtype=dt)
+        for r, h, v in ((8, 64, 512), (17, 128, 1000))
+        for dt in ("float32", "float16", "bfloat16")
+    ) + (
+        # a vocabulary that is not a multiple of 4 (scalar chunk kernels) and
+        # every third row ignored
+        Workload(dims=dict(rows=33, hidden=64, vocab=1001), dtype="bfloat16"),
+        Workload(dims=dict(rows=48, hidden=128, vocab=2048), dtype="bfloat16", label="ignore3",
+                 extra={"ignore_every": 3}),
+        Workload(dims=dict(rows=48, hidden=128, vocab=2048), dtype="float32", label="ignore3",
+                 extra={"ignore_every": 3}),
+    ),
+    # Llama-3-8B lm_head at the sweep's largest token count
+    # (src/evograd/opdecl/models.py:84-86, :293).
+    benchmark=(
+        Workload(dims=dict(rows=8192, hidden=4096, vocab=128256), dtype="bfloat16",
+                 label="llama3_8b"),
+    ),
+    tolerances=TOLERANCES,
+    tolerance_hook=_flce_tolerance,
+    make_inputs="evograd_amd.inputs:make_flce_inputs",
+    memory_inputs=("x", "weight"),
+    regime_feature=_rows_feature,
+    regime_split=LLAMA_VOCAB_REGIME_SPLIT,
+)
+
 OPS: dict[str, OpDecl] = {
     op.name: op
     for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM,
-               CAUSAL_ATTENTION_GQA, CROSS_ENTROPY)
+               CAUSAL_ATTENTION_GQA, CROSS_ENTROPY, FUSED_LINEAR_CROSS_ENTROPY)
 }
 
 

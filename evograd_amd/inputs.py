@@ -172,6 +172,25 @@ def make_cross_entropy_inputs(op, workload, device="cuda"):
     return {"logits": logits, "target": target, "dloss": dloss}
 
 
+def make_flce_inputs(op, workload, device="cuda"):
+    """fused_linear_cross_entropy/__init__.py:34-55: seed rows*100003 + hidden*1009 +
+    vocab; x = 0.5 N(0,1); weight = N(0,1) / sqrt(hidden) drawn in fp32 then cast;
+    target uniform in [0, vocab); dloss = 1 (0-dim, input dtype). ``extra
+    ["ignore_every"] = k`` then sets targets 0, k, 2k, ... to -100."""
+    rows, hidden, vocab = workload.dims["rows"], workload.dims["hidden"], workload.dims["vocab"]
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(rows * 100003 + hidden * 1009 + vocab)
+    x = torch.randn((rows, hidden), device=device, dtype=dt) * 0.5
+    weight = (torch.randn((vocab, hidden), device=device, dtype=torch.float32)
+              * hidden ** -0.5).to(dt)
+    target = torch.randint(0, vocab, (rows,), device=device, dtype=torch.int64)
+    dloss = torch.ones((), device=device, dtype=dt)
+    every = int(workload.extra.get("ignore_every", 0))
+    if every:
+        target[::every] = -100
+    return {"x": x, "weight": weight, "target": target, "dloss": dloss}
+
+
 RECIPES = {
     "make_softmax_inputs": make_softmax_inputs,
     "make_rmsnorm_inputs": make_rmsnorm_inputs,
@@ -182,6 +201,7 @@ RECIPES = {
     "make_attention_inputs": make_attention_inputs,
     "make_attention_gqa_inputs": make_attention_gqa_inputs,
     "make_cross_entropy_inputs": make_cross_entropy_inputs,
+    "make_flce_inputs": make_flce_inputs,
 }
 
 

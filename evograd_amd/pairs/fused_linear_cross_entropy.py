@@ -1,0 +1,133 @@
+"""Fused linear + cross entropy (FLCE) pair on gfx950.
+
+Replaces fused_linear_cross_entropy_forward_ref
+(src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35: the mean
+hard-label cross entropy of ``x @ weight.T`` against ``target``, ignore_index -100,
+projection and logsumexp accumulated in fp32) under the contract of
+fused_linear_cross_entropy/__init__.py:91-152: the ``[rows, vocab]`` logits are never
+materialised in full. The rows are processed in chunks; per chunk:
+
+1. ``logits = x_c @ weight.T`` on the library GEMM (bf16/fp16 operands, fp32
+   accumulation and fp32 output);
+2. ``eg_flce_chunk`` (HIP): per row logsumexp and loss, and the unit gradient
+   ``softmax - onehot`` in the input dtype;
+3. ``dx_c = dlogits @ weight`` and ``dweight += dlogits.T @ x_c`` on the library
+   GEMM, dweight accumulated in fp32 across chunks.
+
+The gradient is formed in the forward because the backward's only input is the
+scalar ``dloss``: the backward (``eg_scale_copy``, HIP) scales the saved unit
+gradients by ``dloss / n_valid``. The loss is fp32, as the reference's forward
+returns it. Saved state: ``(dx, dweight, n_valid)`` — the gradients in the inputs'
+dtypes and one fp32 count, nothing of size rows x vocab.
+
+Peak scratch is one chunk: ``rows_c x vocab`` fp32 logits plus the same in the input
+dtype for the gradient, with ``rows_c * vocab <= CHUNK_ELEMS``; and the fp32
+dweight accumulator (vocab x hidden).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._util import as_contiguous, tag
+
+IGNORE_INDEX = -100
+# Logits elements per chunk: 2^28 fp32 values = 1 GiB (2048 rows of Llama-3's
+# 128256-entry vocabulary).
+CHUNK_ELEMS = 1 << 28
+
+
+def chunk_rows(rows: int, vocab: int) -> int:
+    """Rows per chunk: as many as CHUNK_ELEMS allows, a multiple of 64 when that
+    is at least 64 (full GEMM tiles)."""
+    rc = max(1, min(rows, CHUNK_ELEMS // max(vocab, 1)))
+    if rc >= 64 and rc < rows:
+        rc -= rc % 64
+    return rc
+
+
+def _check(x, weight, target):
+    _lib.require_gpu("fused_linear_cross_entropy", x, weight, target)
+    if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError(f"fused_linear_cross_entropy: x {tuple(x.shape)} and weight "
+                         f"{tuple(weight.shape)} must be [rows, hidden] and [vocab, hidden]")
+    if target.dim() != 1 or target.shape[0] != x.shape[0]:
+        raise ValueError(f"fused_linear_cross_entropy: target must be [rows]={x.shape[0]}, "
+                         f"got {tuple(target.shape)}")
+    if target.dtype != torch.int64:
+        raise TypeError(f"fused_linear_cross_entropy: target must be int64, got {target.dtype}")
+    if x.dtype != weight.dtype:
+        raise TypeError(f"fused_linear_cross_entropy: x {x.dtype} and weight {weight.dtype} differ")
+    tag(x.dtype)
+
+
+def _logits(xc: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    if xc.dtype == torch.float32:
+        return torch.mm(xc, weight.t())
+    return torch.mm(xc, weight.t(), out_dtype=torch.float32)
+
+
+def fused_linear_cross_entropy_forward_with_saved(x: torch.Tensor, weight: torch.Tensor,
+                                                  target: torch.Tensor):
+    _check(x, weight, target)
+    x = as_contiguous("x", x)
+    weight = as_contiguous("weight", weight)
+    target = as_contiguous("target", target)
+    rows, hidden = x.shape
+    vocab = weight.shape[0]
+    dev, dt = x.device, x.dtype
+    stream = _lib.stream_of(x)
+    stats = torch.empty(2 * rows + 1, dtype=torch.float32, device=dev)  # lse | rowloss | n
+    lse, rowloss, n_valid = stats[:rows], stats[rows:2 * rows], stats[2 * rows:]
+    dx = torch.empty_like(x)
+    dw32 = torch.empty((vocab, hidden), dtype=torch.float32, device=dev)
+    rc = chunk_rows(rows, vocab)
+    dl_buf = torch.empty((rc, vocab), dtype=dt, device=dev) if rows else None
+    for r0 in range(0, rows, rc):
+        r1 = min(rows, r0 + rc)
+        n = r1 - r0
+        xc = x[r0:r1]
+        logits = _logits(xc, weight)
+        dl = dl_buf[:n]
+        _lib.call("eg_flce_chunk", logits.data_ptr(), target[r0:].data_ptr(), lse[r0:].data_ptr(),
+                  rowloss[r0:].data_ptr(), dl.data_ptr(), n, vocab, IGNORE_INDEX, tag(dt), stream)
+        del logits
+        torch.mm(dl, weight, out=dx[r0:r1])
+        # the first chunk overwrites the accumulator (beta = 0 never reads it)
+        beta = 0.0 if r0 == 0 else 1.0
+        if dt == torch.float32:
+            torch.addmm(dw32, dl.t(), xc, beta=beta, out=dw32)
+        else:
+            torch.addmm(dw32, dl.t(), xc, beta=beta, out_dtype=torch.float32, out=dw32)
+    if rows == 0:
+        dw32.zero_()
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    _lib.call("eg_cross_entropy_mean", _lib.ptr(target), rowloss.data_ptr(), _lib.ptr(loss),
+              n_valid.data_ptr(), rows, IGNORE_INDEX, _lib.EG_F32, stream)
+    if dt == torch.float32:
+        dw = dw32
+    else:
+        dw = torch.empty_like(weight)
+        _lib.call("eg_scale_copy", dw32.data_ptr(), _lib.EG_F32, dw.data_ptr(), tag(dt),
+                  dw.numel(), None, _lib.EG_F32, None, stream)
+    del dw32
+    n_saved = n_valid.clone()
+    return loss, (dx, dw, n_saved)
+
+
+def fused_linear_cross_entropy_backward_from_saved(dloss: torch.Tensor, saved):
+    dx_u, dw_u, n_valid = saved
+    _lib.require_gpu("fused_linear_cross_entropy_backward_from_saved", dloss, dx_u)
+    if dloss.numel() != 1:
+        raise ValueError(f"fused_linear_cross_entropy: dloss must hold one element, "
+                         f"got {tuple(dloss.shape)}")
+    dloss = as_contiguous("dloss", dloss)
+    stream = _lib.stream_of(dx_u)
+    outs = []
+    for g in (dx_u, dw_u):
+        o = torch.empty_like(g)
+        _lib.call("eg_scale_copy", g.data_ptr(), tag(g.dtype), o.data_ptr(), tag(o.dtype),
+                  g.numel(), dloss.data_ptr(), tag(dloss.dtype), n_valid.data_ptr(), stream)
+        outs.append(o)
+    return tuple(outs)

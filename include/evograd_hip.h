@@ -227,6 +227,37 @@ int eg_cross_entropy_bwd(const void* dloss, const void* logits, const int64_t* t
                          const float* lse, const float* n_valid, void* dlogits, int64_t rows,
                          int64_t cols, int64_t ignore_index, int dtype, void* stream);
 
+/* Mean of per-row losses: loss = sum(rowloss[r] over rows with target[r] !=
+ * ignore_index) / n_valid, written in loss_dtype; n_valid (one fp32) is the count.
+ * Ignored rows must hold rowloss 0 (as eg_flce_chunk writes them). The reduction
+ * of cross_entropy_forward_ref (src/evograd/ops/level1/cross_entropy/forward_ref.py:9-11)
+ * over rows whose losses were produced chunk by chunk. */
+int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* loss,
+                          float* n_valid, int64_t rows, int64_t ignore_index, int loss_dtype,
+                          void* stream);
+
+/* --------------------------------------------- fused linear cross entropy
+ * One row chunk of the fused linear cross entropy
+ * (src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152; forward
+ * fused_linear_cross_entropy/forward_ref.py:23-35). Given the chunk's fp32 logits
+ * [rows, cols] (x_chunk @ weight.T, accumulated in fp32 by the caller's GEMM):
+ *   lse[r] = logsumexp(logits[r]); rowloss[r] = lse[r] - logits[r, target[r]]
+ *   dlogits = softmax(logits) - onehot(target)   (grad_dtype; unscaled)
+ * Rows whose target is ignore_index get rowloss 0 and zero dlogits; a target
+ * outside [0, cols) gives NaN. The caller then forms dx = dlogits @ weight and
+ * dweight += dlogits.T @ x_chunk and scales both by dloss / n_valid. */
+int eg_flce_chunk(const float* logits, const int64_t* target, float* lse, float* rowloss,
+                  void* dlogits, int64_t rows, int64_t cols, int64_t ignore_index,
+                  int grad_dtype, void* stream);
+
+/* dst[i] = src[i] * mul[0] / div[0] for n elements, with conversion from src_dtype
+ * to dst_dtype; mul (of mul_dtype) and div (fp32) are device scalars and either
+ * may be NULL (factor 1). Applies dloss / n_valid to the fused linear cross
+ * entropy's saved gradients (the chain rule of
+ * src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:116-123). */
+int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+                  const void* mul, int mul_dtype, const float* div, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -149,6 +149,15 @@ def cross_entropy_forward_ref(logits: torch.Tensor, target: torch.Tensor) -> tor
     return loss.to(logits.dtype)
 
 
+def fused_linear_cross_entropy_forward_ref(x: torch.Tensor, weight: torch.Tensor,
+                                           target: torch.Tensor) -> torch.Tensor:
+    """src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35: fp32
+    logits x @ weight.T, then the mean cross entropy (ignore_index -100 by default);
+    the loss stays fp32."""
+    logits = torch.matmul(x.float(), weight.float().t())
+    return F.cross_entropy(logits, target, reduction="mean")
+
+
 FORWARDS = {
     "softmax_forward_ref": softmax_forward_ref,
     "rmsnorm_forward_ref": rmsnorm_forward_ref,
@@ -164,4 +173,5 @@ FORWARDS = {
     "causal_attention_gqa_forward_ref": causal_attention_gqa_forward_ref,
     "causal_attention_gqa_runtime_ref": causal_attention_gqa_runtime_ref,
     "cross_entropy_forward_ref": cross_entropy_forward_ref,
+    "fused_linear_cross_entropy_forward_ref": fused_linear_cross_entropy_forward_ref,
 }

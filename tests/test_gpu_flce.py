@@ -1,0 +1,110 @@
+"""Parity of the fused linear cross-entropy pair (library GEMMs + HIP chunk kernels).
+
+The declaration's cases run the reference's gate (oracle: fp32 logits, autograd).
+Beyond it: the chunked result equals the single-chunk one and an fp64 evaluation
+to within the roundings the pair performs (the unit gradient to the input dtype,
+dx and dweight each rounded at the end of the forward and again after the dloss
+scaling), the saved state holds nothing of size rows x vocab, and the BASELINE
+Llama-3-8B size passes the gate.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from evograd_amd import decls, pair_module
+from evograd_amd.bind import bind
+from evograd_amd.inputs import make_case_inputs
+from evograd_amd.opdecl import Workload
+from oracle.verify import verify
+
+pytestmark = pytest.mark.gpu
+OP = decls.FUSED_LINEAR_CROSS_ENTROPY
+
+
+def _note(*parts):
+    print("\n[gpu-flce]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("w", OP.correctness, ids=lambda w: w.key())
+def test_flce_correctness_workloads(w):
+    _note(w.dims, w.dtype, w.extra)
+    rep = verify(OP, pair_module("fused_linear_cross_entropy"), device="cuda", workloads=(w,))
+    torch.cuda.synchronize()
+    assert rep.ok, "\n".join(rep.failures())
+
+
+def _ref64(inp):
+    x = inp["x"].double().requires_grad_(True)
+    wt = inp["weight"].double().requires_grad_(True)
+    loss = torch.nn.functional.cross_entropy(x @ wt.t(), inp["target"], ignore_index=-100)
+    gx, gw = torch.autograd.grad(loss, (x, wt), grad_outputs=inp["dloss"].double())
+    return loss.detach(), gx, gw
+
+
+def _close(a, ref, rel):
+    err = (a.double() - ref).abs()
+    bound = rel * ref.abs() + rel * ref.abs().mean()
+    return float((err - bound).max()) <= 0, float(err.max())
+
+
+def test_flce_chunked_equals_single_chunk_and_fp64():
+    mod = pair_module("fused_linear_cross_entropy")
+    w = Workload(dims=dict(rows=300, hidden=256, vocab=4096), dtype="bfloat16",
+                 extra={"ignore_every": 7})
+    _note("chunking", w.dims)
+    inp = make_case_inputs(OP, w, "cuda")
+    args = (inp["x"], inp["weight"], inp["target"])
+    one_loss, one_saved = mod.fused_linear_cross_entropy_forward_with_saved(*args)
+    one = mod.fused_linear_cross_entropy_backward_from_saved(inp["dloss"], one_saved)
+    old = mod.CHUNK_ELEMS
+    mod.CHUNK_ELEMS = 64 * 4096  # 64-row chunks: 5 chunks, the last one ragged
+    try:
+        assert mod.chunk_rows(300, 4096) == 64
+        many_loss, many_saved = mod.fused_linear_cross_entropy_forward_with_saved(*args)
+        many = mod.fused_linear_cross_entropy_backward_from_saved(inp["dloss"], many_saved)
+    finally:
+        mod.CHUNK_ELEMS = old
+    torch.cuda.synchronize()
+    ref_loss, ref_dx, ref_dw = _ref64(inp)
+    for loss in (one_loss, many_loss):
+        assert loss.dtype == torch.float32
+        assert abs(float(loss) - float(ref_loss)) <= 1e-5 * abs(float(ref_loss))
+    for dx, dw in (one, many):
+        ok, e = _close(dx, ref_dx, 2.0 ** -6)
+        assert ok, f"dx max err {e:.3g}"
+        ok, e = _close(dw, ref_dw, 2.0 ** -6)
+        assert ok, f"dweight max err {e:.3g}"
+    # the chunk split only reorders fp32 accumulations
+    assert torch.allclose(one[0].float(), many[0].float(), rtol=2 ** -7, atol=1e-7)
+    assert torch.allclose(one[1].float(), many[1].float(), rtol=2 ** -7, atol=1e-7)
+    # saved state: the two gradients and one count, nothing rows x vocab
+    assert [tuple(t.shape) for t in many_saved] == [(300, 256), (4096, 256), (1,)]
+
+
+def test_flce_through_autograd_binding():
+    mod = pair_module("fused_linear_cross_entropy")
+    w = OP.correctness[1]
+    _note("bind", w.dims, w.dtype)
+    inp = make_case_inputs(OP, w, "cuda")
+    x = inp["x"].detach().clone().requires_grad_(True)
+    wt = inp["weight"].detach().clone().requires_grad_(True)
+    loss = bind(OP, mod)(x, wt, inp["target"])
+    loss.backward()
+    _, saved = mod.fused_linear_cross_entropy_forward_with_saved(inp["x"], inp["weight"],
+                                                                 inp["target"])
+    gx, gw = mod.fused_linear_cross_entropy_backward_from_saved(
+        torch.ones((), device="cuda", dtype=torch.float32), saved)
+    assert torch.allclose(x.grad.float(), gx.float(), rtol=1e-2, atol=1e-6)
+    assert torch.allclose(wt.grad.float(), gw.float(), rtol=1e-2, atol=1e-6)
+
+
+def test_flce_llama_size_gate():
+    w = OP.benchmark[0]
+    _note("llama size", w.dims, w.dtype)
+    rep = verify(OP, pair_module("fused_linear_cross_entropy"), device="cuda", workloads=(w,))
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    assert rep.ok, "\n".join(rep.failures())

@@ -42,7 +42,14 @@ def test_tolerances_match_the_gate():
                 expect = (2e-2, 2e-2)
                 if op.name == "cross_entropy" and name == "dlogits":
                     expect = (2e-2 / (4 * 8), 2e-2)  # atol scaled to the entry size
+                if op.name == "fused_linear_cross_entropy":
+                    continue  # its own dims; checked below
                 assert op.tolerance_for(w, name) == pytest.approx(expect)
+    wf = Workload(dims=dict(rows=8, hidden=64, vocab=512), dtype="bfloat16")
+    flce = decls.FUSED_LINEAR_CROSS_ENTROPY
+    assert flce.tolerance_for(wf, "loss") == (2e-2, 2e-2)
+    assert flce.tolerance_for(wf, "dx") == pytest.approx((2e-2 / 8, 2e-2))
+    assert flce.tolerance_for(wf, "dweight") == pytest.approx((2e-2 / 512, 2e-2))
     w32 = Workload(dims=dict(rows=4, cols=8), dtype="float32")
     assert decls.SOFTMAX.tolerance_for(w32, "dx") == (1e-5, 1e-5)
     override = Workload(dims=dict(rows=4, cols=8), dtype="float32", atol=1.0, rtol=2.0)

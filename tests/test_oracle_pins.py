@@ -482,3 +482,52 @@ def test_cross_entropy_inputs_and_declaration():
     atol, rtol = op.tolerance_for(w, "dlogits")
     assert atol == pytest.approx(1e-5 / (8 * 512)) and rtol == 1e-5
     assert op.tolerance_for(w, "loss") == (1e-5, 1e-5)
+
+
+# ------------------------------------------------- fused linear cross entropy
+def test_flce_forward_brute_force_and_dtypes():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(5, 6, generator=g, dtype=torch.float64)
+    w = torch.randn(7, 6, generator=g, dtype=torch.float64)
+    t = torch.tensor([0, 6, -100, 3, 3])
+    logits = torch.tensor([[sum(a * b for a, b in zip(xr, wr)) for wr in w.tolist()]
+                           for xr in x.tolist()], dtype=torch.float64)
+    ref = _xent_brute(logits, t)
+    assert math.isclose(float(fr.fused_linear_cross_entropy_forward_ref(x, w, t)), ref,
+                        rel_tol=1e-5)
+    # reduced-precision inputs: widened inside, the loss stays fp32
+    out = fr.fused_linear_cross_entropy_forward_ref(x.bfloat16(), w.bfloat16(), t)
+    assert out.dtype == torch.float32
+
+
+def test_flce_gradients_fd_and_chain_rule():
+    op = decls.FUSED_LINEAR_CROSS_ENTROPY
+    w = Workload(dims=dict(rows=6, hidden=8, vocab=11), dtype="float32", extra={"ignore_every": 4})
+    inputs = _f64(make_case_inputs(op, w, "cpu"))
+    _fd_check(op, inputs)
+    _, g = oracle(op, inputs)
+    assert list(g) == ["dx", "dweight"]
+    # the chain rule through the (separately pinned) cross-entropy gradient
+    logits = inputs["x"] @ inputs["weight"].t()
+    _, gce = oracle(decls.CROSS_ENTROPY, {"logits": logits, "target": inputs["target"],
+                                          "dloss": inputs["dloss"]}, use_reference_dtype=False)
+    dl = gce["dlogits"]
+    assert torch.allclose(g["dx"], (dl @ inputs["weight"]).to(g["dx"].dtype), atol=1e-6)
+    assert torch.allclose(g["dweight"], (dl.t() @ inputs["x"]).to(g["dweight"].dtype), atol=1e-6)
+    # bf16 inputs: gradients come back in bf16, the loss in fp32
+    wb = Workload(dims=dict(rows=4, hidden=8, vocab=16), dtype="bfloat16")
+    yb, gb = oracle(op, make_case_inputs(op, wb, "cpu"))
+    assert yb.dtype == torch.float32
+    assert gb["dx"].dtype == torch.bfloat16 and gb["dweight"].dtype == torch.bfloat16
+
+
+def test_flce_inputs_follow_recipe():
+    op = decls.FUSED_LINEAR_CROSS_ENTROPY
+    w = Workload(dims=dict(rows=8, hidden=64, vocab=512), dtype="float32")
+    a = make_case_inputs(op, w, "cpu")
+    torch.manual_seed(8 * 100003 + 64 * 1009 + 512)
+    assert torch.equal(a["x"], torch.randn(8, 64) * 0.5)
+    assert torch.equal(a["weight"], torch.randn(512, 64) * 64 ** -0.5)
+    assert torch.equal(a["target"], torch.randint(0, 512, (8,)))
+    assert float(a["dloss"]) == 1.0
+    assert op.memory_input_names() == ("x", "weight")
