@@ -41,9 +41,9 @@
 //               delta = rowsum(do * o) for its rows into the workspace;
 //               double-buffered 64-key K, V tiles; S^T = K Q^T, dP^T = V dO^T,
 //               dQ^T += K^T dS^T.
-//   attn_dkdv:  workgroup = NW waves x 32 keys (K, V in registers); double-buffered
-//               32-row Q and dO tiles from the diagonal down; S = Q K^T,
-//               dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
+//   attn_dkdv:  workgroup = NW waves x 32 keys (K in registers, the workgroup's V
+//               in LDS); double-buffered 32-row Q and dO tiles from the diagonal
+//               down; S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
 // The dQ pass recomputes S and dP (7 products executed where the causal
 // FLOP convention counts 5) so that no atomics are needed.
 //
@@ -360,6 +360,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   constexpr int KSTEPS = D / 16, DT = D / 32, MT = BQ / 32;
   __shared__ __align__(16) uint16_t Qs[2][BQ * D];
   __shared__ __align__(16) uint16_t Ds[2][BQ * D];
+  // V of the workgroup's keys: the B operand of dP = dO V^T, read from LDS so
+  // that its 64 registers per wave stay free for operand staging.
+  __shared__ __align__(16) uint16_t Vk[BK * D];
   __shared__ __align__(16) float Ls[2][BQ];
   __shared__ __align__(16) float Es[2][BQ];
 
@@ -373,18 +376,17 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
 
   const int key = k0 + 32 * w + l32;
   const int krc = key < S ? key : S - 1;
-  v8 kf[KSTEPS], vf[KSTEPS];
+  v8 kf[KSTEPS];
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) {
+  for (int kk = 0; kk < KSTEPS; ++kk)
     kf[kk] = *reinterpret_cast<const v8*>(k + base + (int64_t)krc * D + kk * 16 + 8 * hh);
-    vf[kk] = *reinterpret_cast<const v8*>(v + base + (int64_t)krc * D + kk * 16 + 8 * hh);
-  }
   f32x16 dka[DT], dva[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) { dka[t] = f32x16{}; dva[t] = f32x16{}; }
 
   zero_lds<NW * 64>(Qs, sizeof(Qs));
   zero_lds<NW * 64>(Ds, sizeof(Ds));
+  zero_lds<NW * 64>(Vk, sizeof(Vk));
   // The walk: for each query head of the group (in order), the q tiles from the
   // diagonal block to S. dK and dV accumulate over all of them in registers, so
   // the kv-head gradient is the group sum without atomics or a second pass.
@@ -415,6 +417,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     ld.load(dout + hb, qtile(step) * BQ, S, Ds[buf]);
   };
   __syncthreads();
+  {
+    TileLoader<BK, D, NW> lv;  // keys past S stay zero
+    lv.init();
+    lv.load(v + base, k0, S, Vk);
+  }
   if (nsteps > 0) {
     load_tiles(0, 0);
     load_stats(0);
@@ -441,7 +448,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           s[mt] = MM<T>::mma(rd_rows<v8, D>(Qb, 32 * mt + l32, kk, hh), kf[kk], s[mt]);
-          dp[mt] = MM<T>::mma(rd_rows<v8, D>(Db, 32 * mt + l32, kk, hh), vf[kk], dp[mt]);
+          dp[mt] = MM<T>::mma(rd_rows<v8, D>(Db, 32 * mt + l32, kk, hh),
+                              rd_rows<v8, D>(Vk, 32 * w + l32, kk, hh), dp[mt]);
         }
       // Masking: the diagonal tiles (keys past a row) and a tail tile past S.
       const bool edge = qi0 < wave_first_key + 31 || qi0 + BQ > S;
