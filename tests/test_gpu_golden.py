@@ -1,0 +1,43 @@
+"""The HIP pairs against the golden fixtures (GPU): every operator's output and
+gradients on the committed fp64 cases, in fp32 where the kernels take it and in
+bf16 (exact inputs: the fixtures hold bf16-representable values)."""
+
+import sys
+
+import pytest
+import torch
+
+from evograd_amd import decls, pair_module
+from evograd_amd.bind import backward_inactive_kwargs, lookup_pair
+from tests.golden_cases import OPS, assert_close, case_inputs
+
+pytestmark = pytest.mark.gpu
+
+MFMA_ONLY = ("causal_attention", "causal_attention_gqa")
+# (output/gradient rtol, atol as a fraction of the largest expected magnitude)
+BOUNDS = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 1e-2)}
+
+
+def _cases():
+    for name in OPS:
+        for dt in (torch.float32, torch.bfloat16):
+            if dt == torch.float32 and name in MFMA_ONLY:
+                continue
+            yield pytest.param(name, dt, id=f"{name}-{str(dt).split('.')[-1]}")
+
+
+@pytest.mark.parametrize("name,dtype", list(_cases()))
+def test_pair_matches_golden(name, dtype):
+    print(f"\n[gpu-golden] {name} {dtype}", flush=True)
+    sys.stdout.flush()
+    op = decls.get_op(name)
+    inputs, expected, grads = case_inputs(name, dtype, "cuda")
+    fwd, bwd = lookup_pair(op, pair_module(name))
+    y, saved = fwd(*[inputs.get(a.name, getattr(a, "default", None)) for a in op.args])
+    got = bwd(inputs[op.upstream_grad_name], saved, **backward_inactive_kwargs(op, bwd, inputs))
+    got = (got,) if torch.is_tensor(got) else tuple(got)
+    torch.cuda.synchronize()
+    rtol, atol = BOUNDS[dtype]
+    assert_close(f"{name}.{op.output.name}", y, expected, rtol, atol)
+    for gname, g in zip(op.grad_names(), got):
+        assert_close(f"{name}.{gname}", g, grads[gname], rtol, atol)
