@@ -290,6 +290,61 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
   if (lane == 0) rstd_out[row] = rs;
 }
 
+// LayerNorm forward, one wave per row (rows of ITEMS x 64 lanes x VEC elements):
+// the row stays in registers; mean, then the centred sum of squares, each one
+// wave butterfly; no barrier.
+template <typename T, int VEC, int ITEMS>
+__global__ __launch_bounds__(256) void layernorm_fwd_wave(const T* __restrict__ x,
+                                                          const T* __restrict__ w,
+                                                          const T* __restrict__ b,
+                                                          T* __restrict__ y,
+                                                          float* __restrict__ mean_out,
+                                                          float* __restrict__ rstd_out,
+                                                          int64_t rows, float eps) {
+  constexpr int H = ITEMS * kWave * VEC;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * H;
+  Pack<T, VEC> xp[ITEMS];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) xp[it] = ld_raw<T, VEC>(xr + (it * kWave + lane) * VEC);
+  float sv[ITEMS][VEC];
+  float s = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      sv[it][i] = to_f32(xp[it].v[i]);
+      s += sv[it][i];
+    }
+  const float mean = wave_reduce(s, SumOp()) * (1.0f / (float)H);
+  float q = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      sv[it][i] -= mean;
+      q += sv[it][i] * sv[it][i];
+    }
+  const float rs = rsqrtf(wave_reduce(q, SumOp()) * (1.0f / (float)H) + eps);
+  T* yr = y + row * H;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * kWave + lane) * VEC;
+    const Pack<T, VEC> wp = *reinterpret_cast<const Pack<T, VEC>*>(w + c);
+    const Pack<T, VEC> bp = *reinterpret_cast<const Pack<T, VEC>*>(b + c);
+    float o[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) o[i] = (sv[it][i] * rs) * to_f32(wp.v[i]) + to_f32(bp.v[i]);
+    st_vec<T, VEC>(yr + c, o);
+  }
+  if (lane == 0) {
+    rstd_out[row] = rs;
+    mean_out[row] = mean;
+  }
+}
+
 // -------------------------------------------------------------- backward
 // RMSNorm:   xhat = x * rstd, g = dy * w, dx = (g - xhat * mean(g * xhat)) * rstd
 // LayerNorm: xhat = (x - mean) * rstd, dx = rstd * (g - mean(g) - xhat * mean(g * xhat))
@@ -686,8 +741,23 @@ extern "C" int eg_layernorm_fwd(const void* x, const void* weight, const void* b
     using T = scalar_t;
     constexpr int V = 16 / sizeof(T);
     const int h = (int)hidden;
-    bool ok;
-    if (vec_ok<T>(h, {x, weight, bias, y})) {
+    bool ok = true;
+    const int wave_items = h / (kWave * V);
+    const bool vec = vec_ok<T>(h, {x, weight, bias, y});
+    if (vec && h % (kWave * V) == 0 &&
+        (wave_items == 1 || wave_items == 2 || wave_items == 4 || wave_items == 8)) {
+      const unsigned grid = (unsigned)((rows + 3) / 4);
+      const T* xp = (const T*)x;
+      const T* wp = (const T*)weight;
+      const T* bp = (const T*)bias;
+      T* yp = (T*)y;
+      switch (wave_items) {
+        case 1: EG_LAUNCH((layernorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
+        case 2: EG_LAUNCH((layernorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
+        case 4: EG_LAUNCH((layernorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
+        default: EG_LAUNCH((layernorm_fwd_wave<T, V, 8>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
+      }
+    } else if (vec) {
       FwdRing<T, V, true> f{(const T*)x, nullptr, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
       ok = pick_ring((h + V - 1) / V, f);
     } else {
