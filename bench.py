@@ -462,8 +462,9 @@ def main() -> int:
                     help="rocprofv3 workload: STEPS x (flush, fwd, bwd) of OP plus copy calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: every operator's work shards with no or one "
-              "16 KB exchange (see DESIGN.md), and no multi-GPU run is part of this build.",
+        print("bench.py measures one GPU only: every operator's work shards by rows, tokens or "
+              "heads with no exchange or one 16 KB all-reduce of the norm parameter gradients, "
+              "and no multi-GPU run is part of this build.",
               file=sys.stderr)
         return 2
 

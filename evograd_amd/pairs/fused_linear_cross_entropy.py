@@ -33,17 +33,19 @@ from .. import _lib
 from ._util import as_contiguous, tag
 
 IGNORE_INDEX = -100
-# Logits elements per chunk: 2^28 fp32 values = 1 GiB (2048 rows of Llama-3's
-# 128256-entry vocabulary).
-CHUNK_ELEMS = 1 << 28
+# Logits elements per chunk: 2^29 fp32 values = 2 GiB (4096 rows of Llama-3's
+# 128256-entry vocabulary). Measured at 8192 x 4096 x 128256: 2048-row chunks
+# 25.6 ms, 4096-row chunks 23.6 ms per forward (fewer fp32 dweight read-modify-
+# write passes), single chunk 22.9 ms (but the whole logits).
+CHUNK_ELEMS = 1 << 29
 
 
 def chunk_rows(rows: int, vocab: int) -> int:
-    """Rows per chunk: as many as CHUNK_ELEMS allows, a multiple of 64 when that
-    is at least 64 (full GEMM tiles)."""
+    """Rows per chunk: as many as CHUNK_ELEMS allows, rounded down to a power of
+    two when that splits the rows (GEMM shapes of whole tiles)."""
     rc = max(1, min(rows, CHUNK_ELEMS // max(vocab, 1)))
-    if rc >= 64 and rc < rows:
-        rc -= rc % 64
+    if rc < rows:
+        rc = 1 << (rc.bit_length() - 1)
     return rc
 
 
