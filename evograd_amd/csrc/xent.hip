@@ -29,7 +29,6 @@
 // gradient NaN (torch raises there); it is never used as an index.
 #include "eg_common.hpp"
 
-#include <algorithm>
 
 namespace eg {
 namespace {
@@ -259,21 +258,32 @@ __global__ __launch_bounds__(kBwdBlock) void xent_bwd_rows_kernel(
   }
 }
 
-// dst[i] = src[i] * mul[0] / div[0] (either factor optional), 16-byte loads when
-// the source allows them.
+// dst[i] = src[i] * mul[0] / div[0] (either factor optional). Workgroups cover
+// consecutive runs of kScaleUnroll x 256 packs in address order, every load of a
+// thread issued before its first store.
+constexpr int kScaleUnroll = 4;
+
 template <typename TS, typename TO, typename TM, int VEC>
 __global__ __launch_bounds__(256) void scale_copy_kernel(const TS* __restrict__ src,
                                                          TO* __restrict__ dst, int64_t npack,
                                                          const TM* __restrict__ mul,
                                                          const float* __restrict__ div) {
   const float f = (mul ? to_f32(mul[0]) : 1.f) / (div ? div[0] : 1.f);
-  for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < npack;
-       p += (int64_t)gridDim.x * 256) {
-    float v[VEC];
-    load_vec<TS, VEC, VEC * sizeof(TS) == 16>(src + p * VEC, v);
+  const int64_t p0 = (int64_t)blockIdx.x * (256 * kScaleUnroll) + threadIdx.x;
+  float v[kScaleUnroll][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) v[i] *= f;
-    store_vec<TO, VEC, VEC * sizeof(TO) == 16>(dst + p * VEC, v);
+  for (int u = 0; u < kScaleUnroll; ++u) {
+    const int64_t p = p0 + u * 256;
+    if (p < npack) load_vec<TS, VEC, VEC * sizeof(TS) == 16>(src + p * VEC, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kScaleUnroll; ++u) {
+    const int64_t p = p0 + u * 256;
+    if (p < npack) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[u][i] *= f;
+      store_vec<TO, VEC, VEC * sizeof(TO) == 16>(dst + p * VEC, v[u]);
+    }
   }
 }
 
@@ -500,8 +510,11 @@ extern "C" int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_
     set_error("eg_scale_copy: null pointer");
     return 1;
   }
+  if (n / (256 * kScaleUnroll) >= 0x7fffffffLL) {
+    set_error("eg_scale_copy: n=%lld exceeds the launch grid", (long long)n);
+    return 1;
+  }
   hipStream_t st = as_stream(stream);
-  const int blocks = device_cus() * 8;
   return dispatch_type(src_dtype, "eg_scale_copy", [&](auto stag) {
     using TS = decltype(stag);
     return dispatch_type(dst_dtype, "eg_scale_copy", [&](auto dtag) {
@@ -512,15 +525,14 @@ extern "C" int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_
         const TS* sp = static_cast<const TS*>(src);
         TO* dp = static_cast<TO*>(dst);
         const TM* mp = static_cast<const TM*>(mul);
+        constexpr int64_t per = 256 * kScaleUnroll;
         if (n % V == 0 && aligned16(src) && ((uintptr_t)dst % (V * sizeof(TO))) == 0) {
           const int64_t np = n / V;
-          const unsigned g = (unsigned)std::min<int64_t>(blocks, (np + 255) / 256);
-          EG_LAUNCH((scale_copy_kernel<TS, TO, TM, V>), dim3(g), dim3(256), 0, st, sp, dp, np, mp,
-                    div);
+          EG_LAUNCH((scale_copy_kernel<TS, TO, TM, V>), dim3((unsigned)((np + per - 1) / per)),
+                    dim3(256), 0, st, sp, dp, np, mp, div);
         } else {
-          const unsigned g = (unsigned)std::min<int64_t>(blocks, (n + 255) / 256);
-          EG_LAUNCH((scale_copy_kernel<TS, TO, TM, 1>), dim3(g), dim3(256), 0, st, sp, dp, n, mp,
-                    div);
+          EG_LAUNCH((scale_copy_kernel<TS, TO, TM, 1>), dim3((unsigned)((n + per - 1) / per)),
+                    dim3(256), 0, st, sp, dp, n, mp, div);
         }
         return check_launch("eg_scale_copy");
       });
