@@ -40,11 +40,11 @@ def test_library_loads_and_exports_every_symbol():
     assert lib.eg_abi_version() == _lib.ABI_VERSION
     assert lib.eg_last_error() is not None
     # size queries are pure host arithmetic
-    # partial rows: 256 (RMSNorm) / 384 (LayerNorm) per 512 threads of workgroup
-    # width, at most one per row
-    assert lib.eg_rmsnorm_workspace_bytes(16384, 4096) == 256 * 4096 * 4
-    assert lib.eg_layernorm_workspace_bytes(16384, 4096) == 2 * 384 * 4096 * 4
-    assert lib.eg_rmsnorm_workspace_bytes(16384, 64) == 2048 * 64 * 4
+    # partial rows: 512 per 512 threads of workgroup width (the widest case is the
+    # 16-bit vector path's narrowest workgroup), at most one per row
+    assert lib.eg_rmsnorm_workspace_bytes(16384, 4096) == 512 * 4096 * 4
+    assert lib.eg_layernorm_workspace_bytes(16384, 4096) == 2 * 512 * 4096 * 4
+    assert lib.eg_rmsnorm_workspace_bytes(16384, 64) == 4096 * 64 * 4
     assert lib.eg_layernorm_workspace_bytes(3, 64) == 2 * 3 * 64 * 4
     assert lib.eg_rmsnorm_workspace_bytes(0, 64) == 0
     assert lib.eg_cross_entropy_workspace_bytes(8192) == 8192 * 4
