@@ -532,12 +532,84 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ p
       if (c + i < hidden) o[c + i] = from_f32<T>(acc[i]);
 }
 
+// Column sums of G partial rows when hidden % 4 == 0: a 1024-thread workgroup per
+// 4 * CQ columns. Lane (row group rg = lane / CQ, column quad cq = lane % CQ) of
+// wave w adds rows w * RG + rg, + 16 RG, + 32 RG, ... (RG = 64 / CQ row groups per
+// wave; all of a lane's loads issued together, each wave instruction reading RG
+// rows x 16 CQ contiguous bytes); the row groups are combined by lane exchanges
+// and the 16 waves through LDS, in a fixed order.
+template <typename T, int CQ>
+__global__ __launch_bounds__(1024) void colsum_wide_kernel(const float* __restrict__ p0,
+                                                           const float* __restrict__ p1,
+                                                           T* __restrict__ o0, T* __restrict__ o1,
+                                                           int G, int hidden) {
+  constexpr int RG = kWave / CQ, kBatch = 8;
+  __shared__ float4 red[16][CQ];
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+  const int cq = lane % CQ, rg = lane / CQ;
+  const int c = ((int)blockIdx.x * CQ + cq) * 4;
+  const float* p = blockIdx.y == 0 ? p0 : p1;
+  T* o = blockIdx.y == 0 ? o0 : o1;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < hidden) {
+    for (int g0 = w * RG + rg; g0 < G; g0 += 16 * RG * kBatch) {
+      float4 v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = g0 + 16 * RG * i;
+        v[i] = g < G ? *reinterpret_cast<const float4*>(p + (int64_t)g * hidden + c)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        acc.x += v[i].x; acc.y += v[i].y; acc.z += v[i].z; acc.w += v[i].w;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = CQ; off < kWave; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off, kWave);
+    acc.y += __shfl_xor(acc.y, off, kWave);
+    acc.z += __shfl_xor(acc.z, off, kWave);
+    acc.w += __shfl_xor(acc.w, off, kWave);
+  }
+  if (rg == 0) red[w][cq] = acc;
+  __syncthreads();
+  if (threadIdx.x < CQ) {
+    const int cc = ((int)blockIdx.x * CQ + (int)threadIdx.x) * 4;
+    float4 s = red[0][threadIdx.x];
+#pragma unroll
+    for (int ww = 1; ww < 16; ++ww) {
+      const float4 t = red[ww][threadIdx.x];
+      s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+    }
+    if (cc < hidden) {
+      o[cc + 0] = from_f32<T>(s.x);
+      o[cc + 1] = from_f32<T>(s.y);
+      o[cc + 2] = from_f32<T>(s.z);
+      o[cc + 3] = from_f32<T>(s.w);
+    }
+  }
+}
+
+// 32 columns per workgroup (measured at 512 x 4096 partial rows: 7.9 us cold for
+// one parameter, 10.3 us for two, against 8.8 and 14.0 us for colsum_kernel).
+constexpr int kColsumQuads = 8;
+
 template <typename T>
 int launch_colsum(const float* p0, const float* p1, T* o0, T* o1, int nparams, int G,
                   int hidden, hipStream_t st, const char* what) {
   const int quads = (hidden + 3) / 4;
-  EG_LAUNCH((colsum_kernel<T>), dim3((unsigned)((quads + 3) / 4), (unsigned)nparams),
-                     dim3(256), 0, st, p0, p1, o0, o1, G, hidden);
+  // The partial rows come from the same workspace base, so 16-byte alignment of
+  // p0 and a hidden divisible by 4 make every row's float4 loads aligned.
+  if (hidden % 4 == 0 && aligned16(p0) && aligned16(p1)) {
+    EG_LAUNCH((colsum_wide_kernel<T, kColsumQuads>),
+              dim3((unsigned)((quads + kColsumQuads - 1) / kColsumQuads), (unsigned)nparams),
+              dim3(1024), 0, st, p0, p1, o0, o1, G, hidden);
+  } else {
+    EG_LAUNCH((colsum_kernel<T>), dim3((unsigned)((quads + 3) / 4), (unsigned)nparams),
+              dim3(256), 0, st, p0, p1, o0, o1, G, hidden);
+  }
   return check_launch(what);
 }
 
