@@ -23,12 +23,16 @@
 //                     dlogits, workgroups in address order over the flattened
 //                     matrix; dloss read from device memory.
 //   xent_bwd_rows_kernel  narrow rows: one workgroup per row.
+//   scale_copy_kernel dst = src * mul / div with a dtype conversion (the fused
+//                     linear cross entropy's dweight conversion and its dloss / n
+//                     scaling).
+// The fused linear cross entropy (eg_flce_chunk) runs xent_lse_kernel and the
+// backward kernels on a chunk's fp32 logits, the backward with unit scale.
 // No atomics: every sum has a fixed order, so results are bitwise repeatable.
 //
 // A target outside [0, cols) that is not ignore_index makes that row's loss and
 // gradient NaN (torch raises there); it is never used as an index.
 #include "eg_common.hpp"
-
 
 namespace eg {
 namespace {
