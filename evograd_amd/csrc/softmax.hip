@@ -8,8 +8,10 @@
 // One workgroup per row. When the row fits in registers (BLOCK threads x ITEMS
 // packs x VEC elements >= cols) it is read from HBM exactly once with 16-byte
 // loads, reduced with wave butterflies + one LDS exchange, and written once.
-// Wider rows (vocabulary-sized) take a two-read online path.
-#include "eg_common.hpp"
+// Wider rows (vocabulary-sized) take a two-read path: the row's logsumexp (forward)
+// or sum(dy * y) (backward) in one read, then y = exp(x - lse) or
+// dx = y * (dy - sum) in a second read and the write.
+#include "rowwise.hpp"
 
 namespace eg {
 namespace {
@@ -91,63 +93,72 @@ __global__ __launch_bounds__(BLOCK) void softmax_bwd_reg(const T* __restrict__ y
   store_row<T, VEC, ITEMS, BLOCK, NT>(dx + off, cols, gv);
 }
 
-// ---- wide rows: online (max, sum) in one read, then a second read to write.
-template <typename T, int VEC, int BLOCK>
+// ---- wide rows: one read for the row statistic (lse, or sum(dy * y)), a second
+// read to write, each with kUnroll 16-byte packs in flight per thread.
+template <typename T, int VEC, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void softmax_fwd_loop(const T* __restrict__ x,
                                                           T* __restrict__ y, int cols) {
   __shared__ float lds[BLOCK / kWave];
+  constexpr int STEP = BLOCK * VEC;
   const int64_t off = (int64_t)blockIdx.x * cols;
-  const T* xr = x + off;
-  float m = -INFINITY, s = 0.f;
-  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
-    float v[VEC];
-    load_f32<T, VEC>(xr + c, v);
-    float cm = v[0];
+  const T* __restrict__ xr = x + off;
+  T* __restrict__ yr = y + off;
+  // y = exp(x - lse): the max and the normaliser folded into one reference point.
+  // The statistic's read is a temporal load, so that the rows in flight (256 KB
+  // each at bf16 x 128K columns) can serve the second read from the device cache;
+  // the second read is the last use.
+  const float ll = rowwise::row_lse<T, VEC, BLOCK, false>(xr, cols, lds) * rowwise::kLog2e;
+  for (int base = (int)threadIdx.x * VEC; base < cols; base += STEP * rowwise::kUnroll) {
+    float v[rowwise::kUnroll][VEC];
 #pragma unroll
-    for (int i = 1; i < VEC; ++i) cm = fmaxf(cm, v[i]);
-    const float nm = fmaxf(m, cm);
-    float cs = 0.f;
+    for (int u = 0; u < rowwise::kUnroll; ++u) {
+      const int c = base + u * STEP;
+      if (c < cols) load_vec<T, VEC, NT>(xr + c, v[u]);
+    }
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) cs += expf(v[i] - nm);
-    s = (m == -INFINITY ? 0.f : s * expf(m - nm)) + cs;
-    m = nm;
-  }
-  const float gm = block_reduce<BLOCK>(m, MaxOp(), lds);
-  float part = (m == -INFINITY) ? 0.f : s * expf(m - gm);
-  const float gs = block_reduce<BLOCK>(part, SumOp(), lds);
-  const float inv = 1.0f / gs;
-  T* yr = y + off;
-  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
-    float v[VEC];
-    load_f32<T, VEC>(xr + c, v);
+    for (int u = 0; u < rowwise::kUnroll; ++u) {
+      const int c = base + u * STEP;
+      if (c < cols) {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) v[i] = expf(v[i] - gm) * inv;
-    store_f32<T, VEC>(yr + c, v);
+        for (int i = 0; i < VEC; ++i)
+          v[u][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[u][i], rowwise::kLog2e, -ll));
+        store_vec<T, VEC, NT>(yr + c, v[u]);
+      }
+    }
   }
 }
 
-template <typename T, int VEC, int BLOCK>
+template <typename T, int VEC, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void softmax_bwd_loop(const T* __restrict__ y,
                                                           const T* __restrict__ dy,
                                                           T* __restrict__ dx, int cols) {
   __shared__ float lds[BLOCK / kWave];
+  constexpr int STEP = BLOCK * VEC;
   const int64_t off = (int64_t)blockIdx.x * cols;
-  float d = 0.f;
-  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
-    float a[VEC], b[VEC];
-    load_f32<T, VEC>(y + off + c, a);
-    load_f32<T, VEC>(dy + off + c, b);
+  const T* __restrict__ yr = y + off;
+  const T* __restrict__ gr = dy + off;
+  T* __restrict__ dr = dx + off;
+  // temporal first read, as in the forward
+  const float d = rowwise::row_dot<T, VEC, BLOCK, false>(yr, gr, cols, lds);
+  for (int base = (int)threadIdx.x * VEC; base < cols; base += STEP * rowwise::kUnroll) {
+    float a[rowwise::kUnroll][VEC], b[rowwise::kUnroll][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) d += a[i] * b[i];
-  }
-  d = block_reduce<BLOCK>(d, SumOp(), lds);
-  for (int c = (int)threadIdx.x * VEC; c < cols; c += BLOCK * VEC) {
-    float a[VEC], b[VEC];
-    load_f32<T, VEC>(y + off + c, a);
-    load_f32<T, VEC>(dy + off + c, b);
+    for (int u = 0; u < rowwise::kUnroll; ++u) {
+      const int c = base + u * STEP;
+      if (c < cols) {
+        load_vec<T, VEC, NT>(yr + c, a[u]);
+        load_vec<T, VEC, NT>(gr + c, b[u]);
+      }
+    }
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) b[i] = a[i] * (b[i] - d);
-    store_f32<T, VEC>(dx + off + c, b);
+    for (int u = 0; u < rowwise::kUnroll; ++u) {
+      const int c = base + u * STEP;
+      if (c < cols) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) b[u][i] = a[u][i] * (b[u][i] - d);
+        store_vec<T, VEC, NT>(dr + c, b[u]);
+      }
+    }
   }
 }
 
@@ -190,16 +201,16 @@ template <typename T, int VEC>
 void softmax_fwd_vec(const T* x, T* y, int64_t rows, int cols, hipStream_t st) {
   FwdLaunch<T, VEC> l{x, y, rows, cols, st};
   if (!pick_row_config((cols + VEC - 1) / VEC, l))
-    EG_LAUNCH((softmax_fwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
-                       st, x, y, cols);
+    EG_LAUNCH((softmax_fwd_loop<T, VEC, 1024, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+              dim3(1024), 0, st, x, y, cols);
 }
 
 template <typename T, int VEC>
 void softmax_bwd_vec(const T* y, const T* dy, T* dx, int64_t rows, int cols, hipStream_t st) {
   BwdLaunch<T, VEC> l{y, dy, dx, rows, cols, st};
   if (!pick_row_config((cols + VEC - 1) / VEC, l))
-    EG_LAUNCH((softmax_bwd_loop<T, VEC, 1024>), dim3((unsigned)rows), dim3(1024), 0,
-                       st, y, dy, dx, cols);
+    EG_LAUNCH((softmax_bwd_loop<T, VEC, 1024, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+              dim3(1024), 0, st, y, dy, dx, cols);
 }
 
 int check_dims(const char* what, int64_t rows, int64_t cols) {

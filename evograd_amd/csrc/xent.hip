@@ -32,20 +32,19 @@
 //
 // A target outside [0, cols) that is not ignore_index makes that row's loss and
 // gradient NaN (torch raises there); it is never used as an index.
-#include "eg_common.hpp"
+#include "rowwise.hpp"
 
 namespace eg {
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kUnroll = 4;        // packs in flight per thread
+using rowwise::kFlatBlock;
+using rowwise::kFlatPer;
+using rowwise::kFlatUnroll;
+using rowwise::kLog2e;
+using rowwise::kUnroll;
+using rowwise::pick_row_block;
 constexpr int kBwdBlock = 256;
 constexpr int kMeanBlock = 1024;
-
-// Reference point of a running max, as torch's logsumexp takes it: an infinite
-// max is replaced by 0 so that exp(x - ref) stays defined.
-__device__ __forceinline__ float lse_ref(float m) { return __builtin_isinf(m) ? 0.f : m; }
 
 template <typename T, int VEC, int BLOCK, bool NT>
 __global__ __launch_bounds__(BLOCK) void xent_lse_kernel(const T* __restrict__ x,
@@ -54,7 +53,6 @@ __global__ __launch_bounds__(BLOCK) void xent_lse_kernel(const T* __restrict__ x
                                                          float* __restrict__ rowloss, int cols,
                                                          int64_t ignore_index) {
   __shared__ float red[BLOCK / kWave];
-  constexpr int STEP = BLOCK * VEC;
   const int64_t row = blockIdx.x;
   const T* __restrict__ xr = x + row * cols;
   // The target logit is gathered before the row stream starts, so its latency
@@ -65,47 +63,8 @@ __global__ __launch_bounds__(BLOCK) void xent_lse_kernel(const T* __restrict__ x
     t = target[row];
     if (t != ignore_index) picked = (t >= 0 && t < cols) ? to_f32(xr[t]) : NAN;
   }
-  float m = -INFINITY;  // running max of this thread's elements
-  float s = 0.f;        // sum of exp(v - lse_ref(m)) over them
-  for (int base = (int)threadIdx.x * VEC; base < cols; base += STEP * kUnroll) {
-    float v[kUnroll][VEC];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int c = base + u * STEP;
-      if (c < cols) {
-        load_vec<T, VEC, NT>(xr + c, v[u]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) v[u][i] = -INFINITY;
-      }
-    }
-    float bm = m;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) bm = fmaxf(bm, v[u][i]);
-    const float r_new = lse_ref(bm);
-    const float rl = r_new * kLog2e;
-    float acc = 0.f;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i)
-        acc += __builtin_amdgcn_exp2f(__builtin_fmaf(v[u][i], kLog2e, -rl));
-    // s == 0 also covers the first batch (m = -inf), where the rescale factor
-    // could overflow.
-    s = (s == 0.f) ? acc
-                   : __builtin_fmaf(s, __builtin_amdgcn_exp2f((lse_ref(m) - r_new) * kLog2e),
-                                    acc);
-    m = bm;
-  }
-  const float gm = block_reduce<BLOCK>(m, MaxOp(), red);
-  const float gref = lse_ref(gm);
-  const float part =
-      (s == 0.f) ? 0.f : s * __builtin_amdgcn_exp2f((lse_ref(m) - gref) * kLog2e);
-  const float total = block_reduce<BLOCK>(part, SumOp(), red);
+  const float l = rowwise::row_lse<T, VEC, BLOCK, NT>(xr, cols, red);
   if (threadIdx.x == 0) {
-    const float l = gref + log2f(total) * kLn2;
     lse[row] = l;
     rowloss[row] = (t == ignore_index) ? 0.f : l - picked;
   }
@@ -192,14 +151,10 @@ __device__ __forceinline__ void grad_pack(const RowGrad& rg, int c, const float 
 }
 
 // Wide rows: the matrix as one flat sequence of packs, workgroup b covering
-// packs [b * PER, (b + 1) * PER) in address order, so the workgroups in flight
-// stream through contiguous memory. A workgroup spans at most two rows
-// (packs per row >= PER, checked by the host). TI is the logits type, TO the
+// packs [b * kFlatPer, (b + 1) * kFlatPer) in address order, so the workgroups in
+// flight stream through contiguous memory. A workgroup spans at most two rows
+// (packs per row >= kFlatPer, checked by the host). TI is the logits type, TO the
 // gradient's, TD the type of dloss.
-constexpr int kFlatBlock = 512;
-constexpr int kFlatUnroll = 2;
-constexpr int kFlatPer = kFlatBlock * kFlatUnroll;
-
 template <typename TI, typename TO, typename TD, int VEC, bool NT>
 __global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
     const TD* __restrict__ dloss, const TI* __restrict__ x, const int64_t* __restrict__ target,
@@ -291,18 +246,6 @@ __global__ __launch_bounds__(256) void scale_copy_kernel(const TS* __restrict__ 
   }
 }
 
-// Smallest power-of-two workgroup (64..1024 threads) whose threads cover a row
-// of `npack` packs in one pass of kUnroll packs each.
-template <typename Launch>
-void pick_lse_block(int64_t npack, Launch&& launch) {
-  const int64_t per = (npack + kUnroll - 1) / kUnroll;
-  if (per <= 64) launch.template go<64>();
-  else if (per <= 128) launch.template go<128>();
-  else if (per <= 256) launch.template go<256>();
-  else if (per <= 512) launch.template go<512>();
-  else launch.template go<1024>();
-}
-
 template <typename T, int VEC>
 struct LseLaunch {
   const T* x; const int64_t* target; float* lse; float* rowloss; int64_t rows; int cols;
@@ -375,10 +318,10 @@ extern "C" int eg_cross_entropy_fwd(const void* logits, const int64_t* target, v
     const T* xp = static_cast<const T*>(logits);
     if (rows > 0) {
       if (cols % V == 0 && aligned16(logits)) {
-        pick_lse_block(cols / V, LseLaunch<T, V>{xp, target, lse, rowloss, rows, (int)cols,
+        pick_row_block(cols / V, LseLaunch<T, V>{xp, target, lse, rowloss, rows, (int)cols,
                                                  ignore_index, st});
       } else {
-        pick_lse_block(cols, LseLaunch<T, 1>{xp, target, lse, rowloss, rows, (int)cols,
+        pick_row_block(cols, LseLaunch<T, 1>{xp, target, lse, rowloss, rows, (int)cols,
                                              ignore_index, st});
       }
     }
@@ -466,12 +409,12 @@ extern "C" int eg_flce_chunk(const float* logits, const int64_t* target, float* 
     TO* dp = static_cast<TO*>(dlogits);
     const float* none = nullptr;
     if (cols % 4 == 0 && aligned16(logits)) {
-      pick_lse_block(cols / 4, LseLaunch<float, 4>{logits, target, lse, rowloss, rows, (int)cols,
-                                                   ignore_index, st});
+      pick_row_block(cols / 4, LseLaunch<float, 4>{logits, target, lse, rowloss, rows,
+                                                   (int)cols, ignore_index, st});
       launch_bwd<float, TO, float, 4>(none, logits, target, lse, nullptr, dp, rows, (int)cols,
                                       ignore_index, st);
     } else {
-      pick_lse_block(cols, LseLaunch<float, 1>{logits, target, lse, rowloss, rows, (int)cols,
+      pick_row_block(cols, LseLaunch<float, 1>{logits, target, lse, rowloss, rows, (int)cols,
                                                ignore_index, st});
       launch_bwd<float, TO, float, 1>(none, logits, target, lse, nullptr, dp, rows, (int)cols,
                                       ignore_index, st);
