@@ -406,7 +406,8 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
     for (int k = 0; k < DEPTH; ++k) {
       const int64_t row = base + k * G;
       if (row >= rows) break;
-      const float r = rb[k], mu = mb[k];
+      const float r = rb[k];
+      const float mr = LN ? -mb[k] * r : 0.f;  // xhat = x * r + mr
       float xh[ITEMS][VEC], g[ITEMS][VEC];
       float s[NS];
 #pragma unroll
@@ -428,13 +429,13 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
         }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          // Padding columns (dy = 0 there) must also give xhat = 0 for LayerNorm.
-          const bool in = live[it] && (col[it] + i < hidden);
-          const float h = LN ? (in ? (xv[i] - mu) * r : 0.f) : xv[i] * r;
-          aw[it][i] += gv[i] * h;
+          // Columns past the row (whole dead packs) hold dy = 0 and a finite xhat,
+          // so they add nothing to the sums; their outputs are not stored.
+          const float h = LN ? __builtin_fmaf(xv[i], r, mr) : xv[i] * r;
+          aw[it][i] = __builtin_fmaf(gv[i], h, aw[it][i]);
           if (LN) ab[it][i] += gv[i];
           const float gg = gv[i] * wv[it][i];
-          s[0] += gg * h;
+          s[0] = __builtin_fmaf(gg, h, s[0]);
           if (LN) s[1] += gg;
           xh[it][i] = h;
           g[it][i] = gg;
@@ -453,8 +454,9 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
         if (LN) mb[k] = mean[nrow];
       }
       bsum(s);
-      const float dgx = s[0] * inv_h;
-      const float dg = LN ? s[1] * inv_h : 0.f;
+      // dx = r * (g - mean(g) - xhat * mean(g * xhat)) = g * r + (xhat * c2 + c1)
+      const float c2 = -(s[0] * inv_h) * r;
+      const float c1 = LN ? -(s[1] * inv_h) * r : 0.f;
       T* dxr = dx + row * hidden;
 #pragma unroll
       for (int it = 0; it < ITEMS; ++it) {
@@ -462,7 +464,7 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
         float o[VEC];
 #pragma unroll
         for (int i = 0; i < VEC; ++i)
-          o[i] = LN ? r * ((g[it][i] - dg) - xh[it][i] * dgx) : (g[it][i] - xh[it][i] * dgx) * r;
+          o[i] = __builtin_fmaf(g[it][i], r, __builtin_fmaf(xh[it][i], c2, c1));
         st_vec<T, VEC>(dxr + col[it], o);
       }
     }
