@@ -451,8 +451,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
           dp[mt] = MM<T>::mma(rd_rows<v8, D>(Db, 32 * mt + l32, kk, hh),
                               rd_rows<v8, D>(Vk, 32 * w + l32, kk, hh), dp[mt]);
         }
-      // Masking: the diagonal tiles (keys past a row) and a tail tile past S.
-      const bool edge = qi0 < wave_first_key + 31 || qi0 + BQ > S;
+      // Causal mask: row qi0 + 32mt + 8g + 4hh + i4 sees this lane's key iff
+      // 32mt + 8g + i4 >= key - qi0 - 4hh (never true off the diagonal tiles, where
+      // that bound is <= 0). Rows past S have lse = +inf, so their p is 0 already.
+      const int mask_below = key - qi0 - 4 * hh;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -466,7 +468,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
           for (int i4 = 0; i4 < 4; ++i4) {
             const int r = 4 * g + i4;
             float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][r], scale_log2, -lv[i4]));
-            if (edge && (key > qi0 + rr + i4 || qi0 + rr + i4 >= S)) p = 0.f;
+            if (32 * mt + 8 * g + i4 < mask_below) p = 0.f;
             s[mt][r] = p;
             dp[mt][r] = p * (dp[mt][r] - ev[i4]);
           }
@@ -584,18 +586,26 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
         s[T2] = MM<T>::mma(rd_rows<v8, D>(Kb, 32 * T2 + l32, kk, hh), qf[kk], s[T2]);
         dp[T2] = MM<T>::mma(rd_rows<v8, D>(Vb, 32 * T2 + l32, kk, hh), df[kk], dp[T2]);
       }
-    const bool diag = k0 + BN - 1 > wave_first_row;
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[T2][r], scale_log2, -l2));
-        if (diag) {
+      for (int r = 0; r < 16; ++r)
+        s[T2][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[T2][r], scale_log2, -l2));
+    // Keys past the diagonal only in the diagonal tiles: a wave-uniform branch
+    // around the per-element selects, so the other tiles skip them.
+    if (k0 + BN - 1 > wave_first_row) {
+#pragma unroll
+      for (int T2 = 0; T2 < 2; ++T2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
           const int kkey = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
-          if (kkey > qrow) p = 0.f;
+          if (kkey > qrow) s[T2][r] = 0.f;
         }
-        dp[T2][r] = p * (dp[T2][r] - dl);
-      }
+    }
+#pragma unroll
+    for (int T2 = 0; T2 < 2; ++T2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[T2][r] = s[T2][r] * (dp[T2][r] - dl);
 #pragma unroll
     for (int ms = 0; ms < BN / 16; ++ms) {
       const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
