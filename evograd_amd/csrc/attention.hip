@@ -80,6 +80,7 @@ template <> struct MM<f16_t> {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: refresh the max past 2^8 growth
+constexpr int kFwdPrefetch = 6;            // forward S operand reads in flight
 
 // Eight fp32 values (registers off..off+7 of a result tile) rounded and packed
 // as one MFMA operand.
@@ -284,11 +285,29 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     const uint16_t* Kb = Ks[buf];
     const uint16_t* Vb = Vs[buf];
     f32x16 s[2] = {f32x16{}, f32x16{}};
+    // S^T = K Q^T with the K operand reads kFwdPrefetch MFMAs ahead of their use
+    // (MFMA i takes (kk, T2) = (i / 2, i % 2)); the scheduling groups keep that
+    // order, which the default schedule would collapse to one read ahead.
+    {
+      constexpr int NM = 2 * KSTEPS, PF = kFwdPrefetch;
+      v8 ring[PF];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
+      for (int i = 0; i < PF; ++i) ring[i] = rd_rows<v8, D>(Kb, 32 * (i & 1) + l32, i >> 1, hh);
 #pragma unroll
-      for (int T2 = 0; T2 < 2; ++T2)
-        s[T2] = MM<T>::mma(rd_rows<v8, D>(Kb, 32 * T2 + l32, kk, hh), qf[kk], s[T2]);
+      for (int i = 0; i < NM; ++i) {
+        s[i & 1] = MM<T>::mma(ring[i % PF], qf[i >> 1], s[i & 1]);
+        if (i + PF < NM)
+          ring[i % PF] = rd_rows<v8, D>(Kb, 32 * ((i + PF) & 1) + l32, (i + PF) >> 1, hh);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);  // the first PF LDS reads
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        if (i + PF < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     // Raw scores: keys past the diagonal (and past S) are -inf; max in raw units.
     float mt = -INFINITY;
