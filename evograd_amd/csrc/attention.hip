@@ -492,16 +492,36 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
             dp[mt][r] = p * (dp[mt][r] - ev[i4]);
           }
         }
+      // dV^T += dO^T P and dK^T += Q^T dS in the order (ms, t, dV then dK), each
+      // MFMA's transposed operand read one MFMA ahead (two ds_read_b64_tr_b16); the
+      // scheduling groups keep that order, which the default schedule collapses to
+      // a wait before every MFMA.
+      constexpr int NM = 2 * DT * (BQ / 16);
+      auto rd = [&](int i) {
+        const int ms = i / (2 * DT), t = (i / 2) % DT;
+        return rd_tr<v8, D>((i & 1) ? Qb : Db, 16 * ms, 32 * t, lane);
+      };
+      v8 op[2], pb, sb;
+      __builtin_amdgcn_sched_barrier(0);
+      op[0] = rd(0);
 #pragma unroll
-      for (int ms = 0; ms < BQ / 16; ++ms) {
-        const v8 pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
-        const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          dva[t] = MM<T>::mma(rd_tr<v8, D>(Db, 16 * ms, 32 * t, lane), pb, dva[t]);
-          dka[t] = MM<T>::mma(rd_tr<v8, D>(Qb, 16 * ms, 32 * t, lane), sb, dka[t]);
+      for (int i = 0; i < NM; ++i) {
+        if (i + 1 < NM) op[(i + 1) & 1] = rd(i + 1);
+        const int ms = i / (2 * DT), t = (i / 2) % DT;
+        if (i % (2 * DT) == 0) {
+          pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
+          sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
         }
+        if (i & 1) dka[t] = MM<T>::mma(op[i & 1], sb, dka[t]);
+        else dva[t] = MM<T>::mma(op[i & 1], pb, dva[t]);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        if (i + 1 < NM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (more && w == 0 && lane < BQ) { Ls[buf ^ 1][lane] = lreg; Es[buf ^ 1][lane] = ereg; }
   }
