@@ -42,7 +42,23 @@ BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
 ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
            "fused_add_rms_norm", "causal_attention_gqa", "cross_entropy",
-           "fused_linear_cross_entropy")
+           "fused_linear_cross_entropy", "softmax@vocab")
+
+
+def split_name(name: str) -> tuple:
+    """``op`` or ``op@label``: the operator and the label of its benchmark workload
+    (the first benchmark workload when no label is given)."""
+    base, _, label = name.partition("@")
+    return base, label
+
+
+def bench_workload(op, label: str):
+    if not label:
+        return op.benchmark[0]
+    for w in op.benchmark:
+        if w.label == label:
+            return w
+    raise KeyError(f"{op.name} has no benchmark workload labelled {label!r}")
 
 
 def log(msg: str) -> None:
@@ -119,6 +135,9 @@ KERNELS = {
     # first chunk's launches of the forward; the backward's dx scaling
     "fused_linear_cross_entropy": {"fwd": ["xent_lse_kernel", "xent_bwd_flat_kernel"],
                                    "bwd": ["scale_copy_kernel"]},
+    # bf16 rows of 128256: forward row in registers as raw packs; backward
+    # statistic pass then write pass, one kernel each
+    "softmax@vocab": {"fwd": ["softmax_fwd_raw"], "bwd": ["softmax_bwd_loop"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.
@@ -128,6 +147,7 @@ DOMINANT = {
     "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
     "cross_entropy": ("bwd", 0),
     "fused_linear_cross_entropy": ("fwd", 1),
+    "softmax@vocab": ("bwd", 0),
 }
 
 
@@ -195,9 +215,10 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     from evograd_amd.harness import saved_state_report, summarize, time_regions
     from evograd_amd.inputs import make_case_inputs
 
-    op = decls.get_op(name)
-    mod = pair_module(name)
-    w = op.benchmark[0]
+    base, label = split_name(name)
+    op = decls.get_op(base)
+    mod = pair_module(base)
+    w = bench_workload(op, label)
     inputs = make_case_inputs(op, w, "cuda")
     k_heads = 0
     if name == "rope":
@@ -248,7 +269,7 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     ag = None
     if autograd_fn is not None:
         ag = summarize(time_regions(autograd_fn, reps=steps, warmup=warmup, flush=flush))
-    work = algorithmic_work(name, w, k_heads)
+    work = algorithmic_work(base, w, k_heads)
     kt = kernel_times(name, fwd, bwd_call, setup_bwd, state, flush, steps)
     sf, sb, sfull = summarize(fwd_ms), summarize(bwd_ms), summarize(full_ms)
     out = {
@@ -266,8 +287,8 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     phase, idx = DOMINANT[name]
     kname = KERNELS[name][phase][idx]
     k_us = kt[f"{phase}:{kname}"]
-    k_work = dominant_work(name, w, work)
-    k_unit = "bytes" if name == "fused_linear_cross_entropy" else work["unit"]
+    k_work = dominant_work(base, w, work)
+    k_unit = "bytes" if base == "fused_linear_cross_entropy" else work["unit"]
     if k_unit == "bytes":
         k_rate = k_work / (k_us * 1e-6) / 1e9
         out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "bytes": k_work,
@@ -309,8 +330,9 @@ def cpu_baseline(name: str) -> dict:
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    name, label = split_name(name)
     op = decls.get_op(name)
-    w = op.benchmark[0]
+    w = bench_workload(op, label)
     d = dict(w.dims)
     if name == "fused_linear_cross_entropy":
         full_rows = d["rows"]
@@ -401,9 +423,10 @@ def profile_run(name: str, steps: int) -> dict:
     from evograd_amd.harness import CacheFlusher
     from evograd_amd.inputs import make_case_inputs
 
-    op = decls.get_op(name)
-    mod = pair_module(name)
-    w = op.benchmark[0]
+    base, label = split_name(name)
+    op = decls.get_op(base)
+    mod = pair_module(base)
+    w = bench_workload(op, label)
     inputs = make_case_inputs(op, w, "cuda")
     f, b = lookup_pair(op, mod)
     args = [inputs.get(a.name, getattr(a, "default", None)) for a in op.args]

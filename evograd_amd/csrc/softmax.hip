@@ -8,8 +8,9 @@
 // One workgroup per row. When the row fits in registers (BLOCK threads x ITEMS
 // packs x VEC elements >= cols) it is read from HBM exactly once with 16-byte
 // loads, reduced with wave butterflies + one LDS exchange, and written once.
-// Wider rows (vocabulary-sized) take a two-read path: the row's logsumexp (forward)
-// or sum(dy * y) (backward) in one read, then y = exp(x - lse) or
+// 16-bit rows up to 131072 columns keep the forward in registers as raw packs
+// (softmax_fwd_raw). Wider rows take a two-read path: the row's logsumexp
+// (forward) or sum(dy * y) (backward) in one read, then y = exp(x - lse) or
 // dx = y * (dy - sum) in a second read and the write.
 #include "rowwise.hpp"
 
@@ -162,6 +163,81 @@ __global__ __launch_bounds__(BLOCK) void softmax_bwd_loop(const T* __restrict__ 
   }
 }
 
+// ---- 16-bit rows up to 16 packs x 1024 threads (131072 columns, the Llama-3
+// vocabulary): the row stays in registers as raw 16-byte packs (64 VGPRs) and is
+// converted again in each pass, so it is read from HBM once. The empty asm
+// statements keep the compiler from hoisting fp32 copies of the row (128 VGPRs,
+// which would spill at 1024 threads).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4& raw, float (&f)[8]) {
+  Pack<T, 8> pk;
+  __builtin_memcpy(&pk, &raw, 16);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = to_f32(pk.v[i]);
+}
+
+template <typename T, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_fwd_raw(const T* __restrict__ x,
+                                                         T* __restrict__ y, int cols) {
+  static_assert(sizeof(T) == 2, "raw rows hold 16-bit elements");
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  u32x4 raw[ITEMS];
+  u32x4 fill;
+  {
+    Pack<T, 8> pk;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pk.v[i] = from_f32<T>(-INFINITY);
+    __builtin_memcpy(&fill, &pk, 16);
+  }
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+    raw[it] = c < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + off + c))
+                       : fill;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    float f[8];
+    unpack8<T>(raw[it], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, f[i]);
+  }
+  m = block_reduce<BLOCK>(m, MaxOp(), lds);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(raw[it]));
+  const float ml = m * rowwise::kLog2e;
+  float s = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    float f[8];
+    unpack8<T>(raw[it], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      s += __builtin_amdgcn_exp2f(__builtin_fmaf(f[i], rowwise::kLog2e, -ml));
+  }
+  s = block_reduce<BLOCK>(s, SumOp(), lds);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(raw[it]));
+  const float ll = ml + log2f(s);  // log2 of the row's normaliser, max included
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+    if (c < cols) {
+      float f[8];
+      unpack8<T>(raw[it], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        f[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(f[i], rowwise::kLog2e, -ll));
+      store_vec<T, 8, true>(y + off + c, f);
+    }
+  }
+}
+constexpr int kRawItems = 16, kRawBlock = 1024;
+
 // Picks (BLOCK, ITEMS) so that BLOCK * ITEMS packs cover the row; returns false
 // when the row is too wide for the register path.
 template <typename Launch>
@@ -200,9 +276,17 @@ struct BwdLaunch {
 template <typename T, int VEC>
 void softmax_fwd_vec(const T* x, T* y, int64_t rows, int cols, hipStream_t st) {
   FwdLaunch<T, VEC> l{x, y, rows, cols, st};
-  if (!pick_row_config((cols + VEC - 1) / VEC, l))
-    EG_LAUNCH((softmax_fwd_loop<T, VEC, 1024, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
-              dim3(1024), 0, st, x, y, cols);
+  const int64_t npack = (cols + VEC - 1) / VEC;
+  if (pick_row_config(npack, l)) return;
+  if constexpr (sizeof(T) == 2 && VEC == 8) {
+    if (npack <= (int64_t)kRawItems * kRawBlock) {
+      EG_LAUNCH((softmax_fwd_raw<T, kRawItems, kRawBlock>), dim3((unsigned)rows), dim3(kRawBlock),
+                0, st, x, y, cols);
+      return;
+    }
+  }
+  EG_LAUNCH((softmax_fwd_loop<T, VEC, 1024, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+            dim3(1024), 0, st, x, y, cols);
 }
 
 template <typename T, int VEC>

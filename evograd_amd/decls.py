@@ -88,10 +88,17 @@ SOFTMAX = declare_op(
         _w2(((8, 512), (16, 1024)), ("float32",))
         + _w2(((32, 4096), (64, 2048)), ("float16", "bfloat16"))
         # ragged widths (scalar path), a single row and a vocabulary-wide row
-        # (two-read path)
+        # (16-bit: row in registers as raw packs; fp32: two-read path)
         + _w2(((17, 1000), (5, 127), (1, 4096), (3, 131072)), ("float32", "bfloat16"))
+        # a partly filled register row (fp16, bf16) and a row past the register
+        # path (two-read path for 16-bit types)
+        + _w2(((3, 100000),), ("float16", "bfloat16"))
+        + _w2(((2, 262144),), ("bfloat16",))
     ),
-    benchmark=_w2(((4096, 4096),), ("float32",), label="baseline"),
+    # BASELINE's fp32 [4096, 4096], and the reference's timed default width (bf16
+    # rows of the Llama-3 vocabulary, src/evograd/ops/level1/softmax/__init__.py:31-37)
+    benchmark=(_w2(((4096, 4096),), ("float32",), label="baseline")
+               + _w2(((4096, 128256),), ("bfloat16",), label="vocab")),
     tolerances=TOLERANCES,
     make_inputs="evograd_amd.inputs:make_softmax_inputs",
     regime_feature=_rows_feature,
