@@ -135,9 +135,9 @@ KERNELS = {
     # first chunk's launches of the forward; the backward's dx scaling
     "fused_linear_cross_entropy": {"fwd": ["xent_lse_kernel", "xent_bwd_flat_kernel"],
                                    "bwd": ["scale_copy_kernel"]},
-    # bf16 rows of 128256: forward row in registers as raw packs; backward
-    # statistic pass then write pass, one kernel each
-    "softmax@vocab": {"fwd": ["softmax_fwd_raw"], "bwd": ["softmax_bwd_loop"]},
+    # bf16 rows of 128256: the forward's x and the backward's y held in registers
+    # as raw packs, one kernel each
+    "softmax@vocab": {"fwd": ["softmax_fwd_raw"], "bwd": ["softmax_bwd_raw"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.

@@ -8,8 +8,9 @@
 // One workgroup per row. When the row fits in registers (BLOCK threads x ITEMS
 // packs x VEC elements >= cols) it is read from HBM exactly once with 16-byte
 // loads, reduced with wave butterflies + one LDS exchange, and written once.
-// 16-bit rows up to 131072 columns keep the forward in registers as raw packs
-// (softmax_fwd_raw). Wider rows take a two-read path: the row's logsumexp
+// 16-bit rows up to 131072 columns keep the forward's x, and the backward's y, in
+// registers as raw packs (softmax_fwd_raw / softmax_bwd_raw). Wider rows take a
+// two-read path: the row's logsumexp
 // (forward) or sum(dy * y) (backward) in one read, then y = exp(x - lse) or
 // dx = y * (dy - sum) in a second read and the write.
 #include "rowwise.hpp"
@@ -238,6 +239,52 @@ __global__ __launch_bounds__(BLOCK) void softmax_fwd_raw(const T* __restrict__ x
 }
 constexpr int kRawItems = 16, kRawBlock = 1024;
 
+// Backward for the same rows: y stays in registers as raw packs, dy is read twice
+// (the first read temporal, so the rows in flight serve the second from the
+// device cache): sum(dy * y), then dx = y * (dy - sum).
+template <typename T, int ITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_bwd_raw(const T* __restrict__ y,
+                                                         const T* __restrict__ dy,
+                                                         T* __restrict__ dx, int cols) {
+  static_assert(sizeof(T) == 2, "raw rows hold 16-bit elements");
+  __shared__ float lds[BLOCK / kWave];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  u32x4 raw[ITEMS];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+    raw[it] = c < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(y + off + c))
+                       : u32x4{0u, 0u, 0u, 0u};
+  }
+  float d = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+    if (c < cols) {
+      float f[8], g[8];
+      unpack8<T>(raw[it], f);
+      load_vec<T, 8, false>(dy + off + c, g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d += f[i] * g[i];
+    }
+  }
+  d = block_reduce<BLOCK>(d, SumOp(), lds);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(raw[it]));
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+    if (c < cols) {
+      float f[8], g[8];
+      unpack8<T>(raw[it], f);
+      load_vec<T, 8, true>(dy + off + c, g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g[i] = f[i] * (g[i] - d);
+      store_vec<T, 8, true>(dx + off + c, g);
+    }
+  }
+}
+
 // Picks (BLOCK, ITEMS) so that BLOCK * ITEMS packs cover the row; returns false
 // when the row is too wide for the register path.
 template <typename Launch>
@@ -292,9 +339,17 @@ void softmax_fwd_vec(const T* x, T* y, int64_t rows, int cols, hipStream_t st) {
 template <typename T, int VEC>
 void softmax_bwd_vec(const T* y, const T* dy, T* dx, int64_t rows, int cols, hipStream_t st) {
   BwdLaunch<T, VEC> l{y, dy, dx, rows, cols, st};
-  if (!pick_row_config((cols + VEC - 1) / VEC, l))
-    EG_LAUNCH((softmax_bwd_loop<T, VEC, 1024, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
-              dim3(1024), 0, st, y, dy, dx, cols);
+  const int64_t npack = (cols + VEC - 1) / VEC;
+  if (pick_row_config(npack, l)) return;
+  if constexpr (sizeof(T) == 2 && VEC == 8) {
+    if (npack <= (int64_t)kRawItems * kRawBlock) {
+      EG_LAUNCH((softmax_bwd_raw<T, kRawItems, kRawBlock>), dim3((unsigned)rows), dim3(kRawBlock),
+                0, st, y, dy, dx, cols);
+      return;
+    }
+  }
+  EG_LAUNCH((softmax_bwd_loop<T, VEC, 1024, VEC * sizeof(T) == 16>), dim3((unsigned)rows),
+            dim3(1024), 0, st, y, dy, dx, cols);
 }
 
 int check_dims(const char* what, int64_t rows, int64_t cols) {
