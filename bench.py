@@ -4,7 +4,10 @@
 Metric (BASELINE.json): fwd+bwd step latency (us) + % HBM/MFMA roofline per op;
 saved bytes vs CPU. The headline ``value`` is the full-step (forward + backward)
 latency of RMSNorm bf16 x[16384, 4096], eps 1e-6; every other
-BASELINE configuration is measured the same way and reported under ``ops``.
+BASELINE configuration is measured the same way and reported under ``ops``, with the
+operators beyond BASELINE at their declared benchmark workloads. ``op@label``
+selects another labelled benchmark workload of an operator (``softmax@vocab``: bf16
+rows of the Llama-3 vocabulary, the reference's timed default width).
 
 A step is one forward_with_saved + backward_from_saved of the HIP pair over
 synthetic seeded inputs already resident in HBM. Before every timed region a
