@@ -125,7 +125,7 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
 KERNELS = {
     "softmax": {"fwd": ["softmax_fwd"], "bwd": ["softmax_bwd"]},
     "rmsnorm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
-    "layernorm": {"fwd": ["layernorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
+    "layernorm": {"fwd": ["layernorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
     "swiglu": {"fwd": ["swiglu_fwd_kernel"], "bwd": ["swiglu_bwd_kernel"]},
     "rope": {"fwd": ["rope_kernel"], "bwd": ["rope_kernel"]},
     "causal_attention": {"fwd": ["attn_fwd_kernel"],
