@@ -16,8 +16,8 @@
 // Layout: x, y, dy, dx are [rows, hidden] row-major in HBM; weight/bias [hidden];
 // the saved statistics (rstd, and mean for LayerNorm) are fp32 [rows].
 //
-// Ring kernels (every backward, the LayerNorm forward, and the RMSNorm forward
-// for widths the one-wave kernel does not take): a fixed grid of G workgroups
+// Ring kernels (every backward, and the forwards for widths the one-wave and
+// one-workgroup-per-row kernels do not take): a fixed grid of G workgroups
 // walks the rows with stride G. A thread owns the same columns on every row
 // (16-byte packs), so weight, bias and the dweight/dbias sums stay in its
 // registers. Each workgroup keeps DEPTH rows of loads in flight: a ring slot is
@@ -32,9 +32,10 @@
 // constant (not the device's CU count), so the summation order is the same on
 // every device.
 //
-// RMSNorm forward for hidden = 64 x VEC x {1, 2, 4, 8}: one wave per row, the
-// statistic reduced by wave butterflies only, so no barrier sits between a row's
-// loads and its stores.
+// RMSNorm forward for hidden = 64 x VEC x {1, 2, 4, 8}, and LayerNorm's for
+// 64 x VEC x {1, 2, 4}: one wave per row, the statistics reduced by wave
+// butterflies only, so no barrier sits between a row's loads and its stores.
+// LayerNorm rows of 512 packs take one 256-thread workgroup per row.
 #include "eg_common.hpp"
 
 #include <initializer_list>
