@@ -124,13 +124,13 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
 # Kernels each entry point launches, in launch order (index = position).
 KERNELS = {
     "softmax": {"fwd": ["softmax_fwd"], "bwd": ["softmax_bwd"]},
-    "rmsnorm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
+    "rmsnorm": {"fwd": ["rmsnorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
     "layernorm": {"fwd": ["layernorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
     "swiglu": {"fwd": ["swiglu_fwd_kernel"], "bwd": ["swiglu_bwd_kernel"]},
     "rope": {"fwd": ["rope_kernel"], "bwd": ["rope_kernel"]},
     "causal_attention": {"fwd": ["attn_fwd_kernel"],
                          "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
-    "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_wave"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
+    "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
     "causal_attention_gqa": {"fwd": ["attn_fwd_kernel"],
                              "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
     "cross_entropy": {"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
