@@ -142,6 +142,9 @@ RMSNORM = declare_op(
         Workload(dims=dict(rows=17, hidden=1000), dtype="bfloat16"),
         Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16"),
         Workload(dims=dict(rows=1024, hidden=8192), dtype="bfloat16"),
+        # rows of 512 packs (one workgroup per row in the forward) in the other dtypes
+        Workload(dims=dict(rows=33, hidden=2048), dtype="float32"),
+        Workload(dims=dict(rows=9, hidden=4096), dtype="float16"),
     ),
     benchmark=(
         Workload(dims=dict(rows=16384, hidden=4096), dtype="bfloat16", label="baseline",
@@ -187,6 +190,8 @@ FUSED_ADD_RMS_NORM = declare_op(
             Workload(dims=dict(rows=17, cols=127), dtype="float32"),
             Workload(dims=dict(rows=1500, cols=1024), dtype="bfloat16"),
             Workload(dims=dict(rows=300, cols=4096), dtype="bfloat16"),
+            Workload(dims=dict(rows=33, cols=2048), dtype="float32"),
+            Workload(dims=dict(rows=9, cols=4096), dtype="float16"),
         )
     ),
     benchmark=(
@@ -229,6 +234,9 @@ LAYERNORM = declare_op(
         Workload(dims=dict(rows=17, hidden=1000), dtype="bfloat16"),
         Workload(dims=dict(rows=17, hidden=127), dtype="float32"),
         Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16"),
+        # rows of 512 packs (one workgroup per row in the forward) in the other dtypes
+        Workload(dims=dict(rows=33, hidden=2048), dtype="float32"),
+        Workload(dims=dict(rows=9, hidden=4096), dtype="float16"),
     ),
     benchmark=(
         Workload(dims=dict(rows=16384, hidden=4096), dtype="bfloat16", label="baseline"),
