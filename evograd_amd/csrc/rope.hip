@@ -9,22 +9,27 @@
 //
 // Layout: x [batch, heads, tokens, head_dim] row-major; cos/sin [tokens, head_dim].
 // A thread owns one (token, chunk) pair, chunk = VEC consecutive lanes of the
-// first half plus the matching VEC lanes of the second half. It loads its four
-// table slices once and then walks a group of heads of one batch entry, so the
-// tables cost one read per (batch, head group) instead of one per row, and the
-// x traffic is pure 16-byte streaming.
+// first half plus the matching VEC lanes of the second half. It serves a group of
+// four heads of one batch entry with one load of its four table slices, so the
+// tables cost one read per (batch, head group) instead of one per row; the x
+// traffic is pure 16-byte streaming, all of a group's loads issued before its
+// first store.
 #include "eg_common.hpp"
 
 namespace eg {
 namespace {
 
 constexpr int kRopeBlock = 256;
+// Heads per group: enough groups to fill the chip, few enough to amortise the
+// table loads over several rows.
+constexpr int kHeadsPerGroup = 4;
 
 template <typename T, typename TT, int VEC, bool NT>
 __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     const T* __restrict__ q, const T* __restrict__ k, T* __restrict__ qo, T* __restrict__ ko,
     const TT* __restrict__ cosv, const TT* __restrict__ sinv, int heads_q, int heads_k,
-    int tokens, int head_dim, int hpg, int groups_q, int groups_k, float sgn) {
+    int tokens, int head_dim, int groups_q, int groups_k, float sgn) {
+  constexpr int HPG = kHeadsPerGroup;
   const int half = head_dim >> 1;
   const int cpr = half / VEC;  // chunks per row
   const int64_t idx = (int64_t)blockIdx.x * kRopeBlock + threadIdx.x;
@@ -34,32 +39,26 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
   const int groups = groups_q + groups_k;
   const int b = blockIdx.y / groups;
   const int g = blockIdx.y - b * groups;
-
-  const T* src;
-  T* dst;
-  int heads, h0;
-  if (g < groups_q) { src = q; dst = qo; heads = heads_q; h0 = g * hpg; }
-  else { src = k; dst = ko; heads = heads_k; h0 = (g - groups_q) * hpg; }
-  int h1 = h0 + hpg;
-  if (h1 > heads) h1 = heads;
+  const bool isq = g < groups_q;
+  const T* __restrict__ src = isq ? q : k;
+  T* __restrict__ dst = isq ? qo : ko;
+  const int heads = isq ? heads_q : heads_k;
+  const int h0 = (isq ? g : g - groups_q) * HPG;
+  const int nh = min(HPG, heads - h0);
 
   const int64_t toff = (int64_t)t * head_dim + ch * VEC;
-  float c1[VEC], c2[VEC], s1[VEC], s2[VEC];
-  load_f32<TT, VEC>(cosv + toff, c1);
-  load_f32<TT, VEC>(cosv + toff + half, c2);
-  load_f32<TT, VEC>(sinv + toff, s1);
-  load_f32<TT, VEC>(sinv + toff + half, s2);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) { s1[i] *= -sgn; s2[i] *= sgn; }
-
   const int64_t row_stride = (int64_t)tokens * head_dim;
   const int64_t off0 = ((int64_t)b * heads + h0) * row_stride + toff;
-#pragma unroll 4
-  for (int h = h0; h < h1; ++h) {
-    const int64_t off = off0 + (int64_t)(h - h0) * row_stride;
-    float x1[VEC], x2[VEC];
-    load_vec<T, VEC, NT>(src + off, x1);
-    load_vec<T, VEC, NT>(src + off + half, x2);
+  float c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+  auto load_tables = [&] {
+    load_f32<TT, VEC>(cosv + toff, c1);
+    load_f32<TT, VEC>(cosv + toff + half, c2);
+    load_f32<TT, VEC>(sinv + toff, s1);
+    load_f32<TT, VEC>(sinv + toff + half, s2);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { s1[i] *= -sgn; s2[i] *= sgn; }
+  };
+  auto rotate = [&](const float* x1, const float* x2, int64_t off) {
     float y1[VEC], y2[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
@@ -68,16 +67,35 @@ __global__ __launch_bounds__(kRopeBlock) void rope_kernel(
     }
     store_vec<T, VEC, NT>(dst + off, y1);
     store_vec<T, VEC, NT>(dst + off + half, y2);
+  };
+  if (nh == HPG) {
+    // A full group: every row's loads, then the tables, are issued before the
+    // first store (the scheduling barrier keeps the compiler from interleaving
+    // them again; 119.8 -> 114.5 us at q [8, 32, 4096, 128] + k [8, 8, 4096, 128]).
+    float x1[HPG][VEC], x2[HPG][VEC];
+#pragma unroll
+    for (int j = 0; j < HPG; ++j) {
+      load_vec<T, VEC, NT>(src + off0 + j * row_stride, x1[j]);
+      load_vec<T, VEC, NT>(src + off0 + j * row_stride + half, x2[j]);
+    }
+    load_tables();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < HPG; ++j) rotate(x1[j], x2[j], off0 + j * row_stride);
+  } else {
+    load_tables();
+    for (int j = 0; j < nh; ++j) {
+      float x1[VEC], x2[VEC];
+      load_vec<T, VEC, NT>(src + off0 + j * row_stride, x1);
+      load_vec<T, VEC, NT>(src + off0 + j * row_stride + half, x2);
+      rotate(x1, x2, off0 + j * row_stride);
+    }
   }
 }
 
 inline bool aligned_to(const void* p, size_t n) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) % n) == 0;
 }
-
-// Heads per group: enough groups to fill the chip, few enough to amortise the
-// table loads over several rows.
-constexpr int kHeadsPerGroup = 4;
 
 template <typename T, typename TT, int VEC>
 int launch_rope(const void* q, const void* k, void* qo, void* ko, const void* cosv,
@@ -95,7 +113,7 @@ int launch_rope(const void* q, const void* k, void* qo, void* ko, const void* co
   }
   EG_LAUNCH((rope_kernel<T, TT, VEC, VEC * sizeof(T) == 16>), dim3((unsigned)gx, (unsigned)gy), dim3(kRopeBlock),
                      0, st, (const T*)q, (const T*)k, (T*)qo, (T*)ko, (const TT*)cosv,
-                     (const TT*)sinv, (int)hq, (int)hk, (int)tokens, (int)head_dim, hpg, gq, gk,
+                     (const TT*)sinv, (int)hq, (int)hk, (int)tokens, (int)head_dim, gq, gk,
                      sgn);
   return check_launch("eg_rope");
 }
