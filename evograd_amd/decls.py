@@ -291,7 +291,8 @@ ROPE = declare_op(
     reference_dtype="float32",
     correctness=tuple(
         Workload(dims=dict(B=b, n_heads=h, T=t, head_dim=d), dtype=dt)
-        for b, h, t, d in ((1, 4, 16, 64), (2, 8, 128, 128), (1, 32, 129, 128), (1, 3, 7, 10))
+        for b, h, t, d in ((1, 4, 16, 64), (2, 8, 128, 128), (1, 32, 129, 128), (1, 3, 7, 10),
+                           (2, 6, 33, 128))  # 6 heads: a full and a partial group of four
         for dt in ("float32", "float16", "bfloat16")
     ),
     benchmark=(

@@ -114,6 +114,32 @@ def test_rope_joint_qk_equals_single_launches_and_oracle():
     assert torch.allclose(n_in, n_out, rtol=2e-2, atol=2e-2)
 
 
+def test_rope_joint_qk_partial_head_groups():
+    """Heads are served in groups of four: q with 6 heads (a full and a partial group)
+    and k with 2 (one partial group) in one joint launch equal two single launches and
+    the oracle."""
+    mod = pair_module("rope")
+    g = torch.Generator(device="cpu").manual_seed(99)
+    q = torch.randn((2, 6, 33, 128), generator=g).to("cuda", torch.bfloat16)
+    k = torch.randn((2, 2, 33, 128), generator=g).to("cuda", torch.bfloat16)
+    pos = torch.arange(33, dtype=torch.float32)[:, None]
+    inv = 10000.0 ** (-torch.arange(0, 64, dtype=torch.float32) / 64)
+    ang = torch.cat([pos * inv, pos * inv], dim=-1)
+    cos, sin = ang.cos().cuda(), ang.sin().cuda()
+    print("\n[gpu-parity] rope joint q[2,6,33,128] k[2,2,33,128] bf16", flush=True)
+    (qo, ko), saved = mod.rope_qk_forward_with_saved(q, k, cos, sin)
+    assert torch.equal(qo, mod.rope_forward_with_saved(q, cos, sin)[0])
+    assert torch.equal(ko, mod.rope_forward_with_saved(k, cos, sin)[0])
+    for x, y in ((q, qo), (k, ko)):
+        yr, _ = oracle(decls.ROPE, {"x": x, "cos": cos, "sin": sin, "dy": x})
+        assert torch.allclose(y.float(), yr.float(), atol=2e-2, rtol=2e-2)
+    dq, dk = mod.rope_qk_backward_from_saved((q, k), saved)
+    _, gq = oracle(decls.ROPE, {"x": q, "cos": cos, "sin": sin, "dy": q})
+    _, gk = oracle(decls.ROPE, {"x": k, "cos": cos, "sin": sin, "dy": k})
+    assert torch.allclose(dq.float(), gq["dx"].float(), atol=2e-2, rtol=2e-2)
+    assert torch.allclose(dk.float(), gk["dx"].float(), atol=2e-2, rtol=2e-2)
+
+
 def test_fused_add_rms_norm_backward_deterministic_and_grads_not_aliased():
     """Bitwise-repeatable backward at the Llama-3-8B size; through the autograd
     binding x.grad and r.grad hold equal values in separate storage (the pair
