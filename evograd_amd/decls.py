@@ -27,7 +27,7 @@ Differences from the reference declarations, all deliberate:
 * ``reference_dtype="float32"``: the oracle runs reduced-precision cases in fp32
   and casts back (the promotion of src/evograd/opdecl/oracle.py:70-110), so a
   comparison measures the kernel's error, not the oracle's own bf16 rounding.
-* Each declaration also lists the BASELINE configuration(s) of this build as
+* Each declaration also lists the benchmark configuration(s) of this build as
   ``benchmark`` workloads (label "baseline").
 
 ``forward``/``runtime_forward`` are "module:function" strings naming the
@@ -95,7 +95,7 @@ SOFTMAX = declare_op(
         + _w2(((3, 100000),), ("float16", "bfloat16"))
         + _w2(((2, 262144),), ("bfloat16",))
     ),
-    # BASELINE's fp32 [4096, 4096], and the reference's timed default width (bf16
+    # The fp32 [4096, 4096] benchmark case, and the reference's timed default width (bf16
     # rows of the Llama-3 vocabulary, src/evograd/ops/level1/softmax/__init__.py:31-37)
     benchmark=(_w2(((4096, 4096),), ("float32",), label="baseline")
                + _w2(((4096, 128256),), ("bfloat16",), label="vocab")),
@@ -350,7 +350,7 @@ CAUSAL_ATTENTION = declare_op(
 # ----------------------------------------------- grouped-query causal attention
 # The attention of src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:
 # 101-107 as the layer runs it: n_kv_heads < n_heads, k and v repeated over each
-# query group. Benchmark: the BASELINE attention batch and sequence with
+# query group. Benchmark: the MHA benchmark's batch and sequence with
 # Llama-3-8B's 32 query and 8 kv heads (src/evograd/opdecl/models.py:250-262).
 CAUSAL_ATTENTION_GQA = declare_op(
     name="causal_attention_gqa",

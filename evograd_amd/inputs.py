@@ -14,8 +14,8 @@ from .opdecl import Active, OpDecl, Workload, bind_shape
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16,
           "float64": torch.float64}
 
-# Llama-3's rotary base (src/evograd/opdecl/models.py:259-261); the BASELINE RoPE
-# configuration overrides it with theta=10000 through the workload's ``extra``.
+# Llama-3's rotary base (src/evograd/opdecl/models.py:259-261); the benchmark RoPE
+# configuration (label "baseline") overrides it with theta=10000 through the workload's ``extra``.
 LLAMA3_ROPE_THETA = 500000.0
 
 
@@ -109,7 +109,7 @@ def rope_tables(tokens: int, head_dim: int, theta: float, dtype, device):
 def make_rope_inputs(op, workload, device="cuda"):
     """rope/__init__.py:30-62: seed T*100003 + heads*1009 + head_dim; x = 0.5 N(0,1);
     tables at Llama-3's theta cast to x's dtype; dy = 0.5 N(0,1). A workload's
-    ``extra`` may set theta, table_dtype and x_scale (the BASELINE case uses
+    ``extra`` may set theta, table_dtype and x_scale (the benchmark case uses
     theta 10000, fp32 tables and unit-variance x)."""
     d = workload.dims
     B, H, T, D = d["B"], d["n_heads"], d["T"], d["head_dim"]
@@ -127,7 +127,7 @@ def make_rope_inputs(op, workload, device="cuda"):
 
 
 def make_attention_inputs(op, workload, device="cuda"):
-    """Generic seed (inputs.py:40-49); q, k, v, do ~ N(0,1) as the BASELINE
+    """Generic seed (inputs.py:40-49); q, k, v, do ~ N(0,1) as the benchmark
     attention configuration specifies."""
     d = workload.dims
     shape = (d["B"], d["H"], d["S"], d["D"])

@@ -4,7 +4,7 @@ The declaration's cases run the reference's gate (oracle: fp32 logits, autograd)
 Beyond it: the chunked result equals the single-chunk one and an fp64 evaluation
 to within the roundings the pair performs (the unit gradient to the input dtype,
 dx and dweight each rounded at the end of the forward and again after the dloss
-scaling), the saved state holds nothing of size rows x vocab, and the BASELINE
+scaling), the saved state holds nothing of size rows x vocab, and the benchmark
 Llama-3-8B size passes the gate.
 """
 

@@ -4,7 +4,7 @@ Every case runs the reference's gate (restated in oracle/verify.py): identical
 seeded inputs, the oracle's forward and gradients, then shape, dtype and
 allclose on the output and every gradient at this build's tolerances
 (fp32 1e-5/1e-5, fp16 1e-2/1e-2, bf16 2e-2/2e-2; see evograd_amd/decls.py).
-The BASELINE-size cases run the same gate at full size plus size-independent
+The benchmark-size cases run the same gate at full size plus size-independent
 properties (bitwise determinism of the two-stage reductions, in-place backward,
 joint q/k RoPE == two single launches).
 """

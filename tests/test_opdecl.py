@@ -94,7 +94,7 @@ def test_baseline_workloads_present():
     labels = {name: [w for w in decls.get_op(name).benchmark if w.label == "baseline"]
               for name in BASELINE_OPS}
     assert all(labels.values()), labels
-    # the operators beyond BASELINE.json carry the reference's own timed workload
+    # the operators beyond the six above carry the reference's own timed workload
     farn = decls.FUSED_ADD_RMS_NORM.benchmark[0]
     assert farn.dims == {"rows": 16384, "cols": 4096} and farn.dtype == "bfloat16"
     assert decls.RMSNORM.benchmark[0].dims == {"rows": 16384, "hidden": 4096}
