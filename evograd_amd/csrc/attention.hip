@@ -53,6 +53,7 @@
 #include "eg_common.hpp"
 
 #include <initializer_list>
+#include <type_traits>
 
 namespace eg {
 namespace {
@@ -80,7 +81,7 @@ template <> struct MM<f16_t> {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: refresh the max past 2^8 growth
-constexpr int kFwdPrefetch = 6;            // forward S operand reads in flight
+constexpr int kFwdPrefetch = 4;            // forward S operand reads in flight
 
 // Eight fp32 values (registers off..off+7 of a result tile) rounded and packed
 // as one MFMA operand.
@@ -257,6 +258,24 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
   for (int kk = 0; kk < KSTEPS; ++kk)
     qf[kk] = *reinterpret_cast<const v8*>(q + base + (int64_t)qrc * D + kk * 16 + 8 * hh);
 
+  // Element offsets of this lane's operand reads inside a tile, computed once: the
+  // S reads (row l32, chunk 2kk + hh; the second 32-row half adds 32 * D) and the
+  // transposed V reads (rows 4hh + m/4 and +8 of each 16-row step, column block t;
+  // step ms adds 16 * D). With the tile loop unrolled over the two buffers, each
+  // read is one of these registers plus an immediate.
+  int offS[KSTEPS], offV[DT][2];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) offS[kk] = toff<D>(l32, 2 * kk + hh);
+  {
+    const int mq = lane & 15, gs = (lane >> 4) & 1, r0 = 4 * hh + (mq >> 2);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int col = 32 * t + 16 * gs + 4 * (mq & 3);
+      offV[t][0] = toff<D>(r0, col >> 3) + (col & 7);
+      offV[t][1] = toff<D>(r0 + 8, col >> 3) + (col & 7);
+    }
+  }
+
   f32x16 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
@@ -272,16 +291,16 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
   ld.init();
   ld.load(kp, 0, S, Ks[0]);
   ld.load(vp, 0, S, Vs[0]);
-  for (int j = 0; j < ntiles; ++j) {
+  auto tile = [&](auto bufc, int j) {
+    constexpr int buf = decltype(bufc)::value;
     wait_loads();
     __syncthreads();
-    const int buf = j & 1;
     if (j + 1 < ntiles) {
       ld.load(kp, (j + 1) * BN, S, Ks[buf ^ 1]);
       ld.load(vp, (j + 1) * BN, S, Vs[buf ^ 1]);
     }
     const int k0 = j * BN;
-    if (k0 > wave_first_row + 31) continue;  // every key of the tile is above this wave's rows
+    if (k0 > wave_first_row + 31) return;  // every key of the tile is above this wave's rows
     const uint16_t* Kb = Ks[buf];
     const uint16_t* Vb = Vs[buf];
     f32x16 s[2] = {f32x16{}, f32x16{}};
@@ -293,12 +312,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
       v8 ring[PF];
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < PF; ++i) ring[i] = rd_rows<v8, D>(Kb, 32 * (i & 1) + l32, i >> 1, hh);
+      for (int i = 0; i < PF; ++i)
+        ring[i] = *reinterpret_cast<const v8*>(Kb + offS[i >> 1] + 32 * D * (i & 1));
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
         s[i & 1] = MM<T>::mma(ring[i % PF], qf[i >> 1], s[i & 1]);
         if (i + PF < NM)
-          ring[i % PF] = rd_rows<v8, D>(Kb, 32 * ((i + PF) & 1) + l32, (i + PF) >> 1, hh);
+          ring[i % PF] =
+              *reinterpret_cast<const v8*>(Kb + offS[(i + PF) >> 1] + 32 * D * ((i + PF) & 1));
       }
       __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);  // the first PF LDS reads
 #pragma unroll
@@ -352,9 +373,21 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     for (int ms = 0; ms < BN / 16; ++ms) {
       const v8 pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
 #pragma unroll
-      for (int t = 0; t < DT; ++t)
-        acc[t] = MM<T>::mma(rd_tr<v8, D>(Vb, 16 * ms, 32 * t, lane), pb, acc[t]);
+      for (int t = 0; t < DT; ++t) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (EG_LDS i16x4*)(Vb + offV[t][0] + 16 * D * ms));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (EG_LDS i16x4*)(Vb + offV[t][1] + 16 * D * ms));
+        v8 va;
+        __builtin_memcpy(&va, &lo, 8);
+        __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
+        acc[t] = MM<T>::mma(va, pb, acc[t]);
+      }
     }
+  };
+  for (int j = 0; j < ntiles; j += 2) {
+    tile(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < ntiles) tile(std::integral_constant<int, 1>{}, j + 1);
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
