@@ -631,6 +631,21 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
   const uint16_t* kp = k + kvbase;
   const uint16_t* vp = v + kvbase;
 
+  // Element offsets of this lane's operand reads inside a tile, computed once (as in
+  // the forward): rows for S and dP (the K and V tiles share the layout), transposed
+  // rows of K for dQ; the tile loop is unrolled over the two buffers.
+  int offS[KSTEPS], offV[DT][2];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) offS[kk] = toff<D>(l32, 2 * kk + hh);
+  {
+    const int mq = lane & 15, gs = (lane >> 4) & 1, r0 = 4 * hh + (mq >> 2);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int col = 32 * t + 16 * gs + 4 * (mq & 3);
+      offV[t][0] = toff<D>(r0, col >> 3) + (col & 7);
+      offV[t][1] = toff<D>(r0 + 8, col >> 3) + (col & 7);
+    }
+  }
   zero_lds<NW * 64>(Ks, sizeof(Ks));
   zero_lds<NW * 64>(Vs, sizeof(Vs));
   __syncthreads();
@@ -638,16 +653,16 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
   ld.init();
   ld.load(kp, 0, S, Ks[0]);
   ld.load(vp, 0, S, Vs[0]);
-  for (int j = 0; j < ntiles; ++j) {
+  auto tile = [&](auto bufc, int j) {
+    constexpr int buf = decltype(bufc)::value;
     wait_loads();
     __syncthreads();
-    const int buf = j & 1;
     if (j + 1 < ntiles) {
       ld.load(kp, (j + 1) * BN, S, Ks[buf ^ 1]);
       ld.load(vp, (j + 1) * BN, S, Vs[buf ^ 1]);
     }
     const int k0 = j * BN;
-    if (k0 > wave_first_row + 31) continue;
+    if (k0 > wave_first_row + 31) return;
     const uint16_t* Kb = Ks[buf];
     const uint16_t* Vb = Vs[buf];
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
@@ -655,8 +670,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2) {
-        s[T2] = MM<T>::mma(rd_rows<v8, D>(Kb, 32 * T2 + l32, kk, hh), qf[kk], s[T2]);
-        dp[T2] = MM<T>::mma(rd_rows<v8, D>(Vb, 32 * T2 + l32, kk, hh), df[kk], dp[T2]);
+        s[T2] = MM<T>::mma(*reinterpret_cast<const v8*>(Kb + offS[kk] + 32 * D * T2), qf[kk],
+                           s[T2]);
+        dp[T2] = MM<T>::mma(*reinterpret_cast<const v8*>(Vb + offS[kk] + 32 * D * T2), df[kk],
+                            dp[T2]);
       }
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
@@ -682,9 +699,21 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     for (int ms = 0; ms < BN / 16; ++ms) {
       const v8 sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
 #pragma unroll
-      for (int t = 0; t < DT; ++t)
-        acc[t] = MM<T>::mma(rd_tr<v8, D>(Kb, 16 * ms, 32 * t, lane), sb, acc[t]);
+      for (int t = 0; t < DT; ++t) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (EG_LDS i16x4*)(Kb + offV[t][0] + 16 * D * ms));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (EG_LDS i16x4*)(Kb + offV[t][1] + 16 * D * ms));
+        v8 ka;
+        __builtin_memcpy(&ka, &lo, 8);
+        __builtin_memcpy(reinterpret_cast<char*>(&ka) + 8, &hi, 8);
+        acc[t] = MM<T>::mma(ka, sb, acc[t]);
+      }
     }
+  };
+  for (int j = 0; j < ntiles; j += 2) {
+    tile(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < ntiles) tile(std::integral_constant<int, 1>{}, j + 1);
   }
 
   if (qrow < S) {
