@@ -82,6 +82,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: refresh the max past 2^8 growth
 constexpr int kFwdPrefetch = 4;            // forward S operand reads in flight
+constexpr int kDqPrefetch = 2;             // dQ S / dP operand reads in flight
 
 // Eight fp32 values (registers off..off+7 of a result tile) rounded and packed
 // as one MFMA operand.
@@ -666,15 +667,34 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     const uint16_t* Kb = Ks[buf];
     const uint16_t* Vb = Vs[buf];
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+    // S^T = K Q^T and dP^T = V dO^T interleaved, each operand read kDqPrefetch MFMAs
+    // ahead (read i: kk = i / 4, T2 = (i / 2) % 2, K for even i and V for odd i);
+    // the scheduling groups keep that order.
+    {
+      constexpr int NR = 4 * KSTEPS, PF = kDqPrefetch;
+      auto rd = [&](int i) {
+        const uint16_t* tb = (i & 1) ? Vb : Kb;
+        return *reinterpret_cast<const v8*>(tb + offS[i >> 2] + 32 * D * ((i >> 1) & 1));
+      };
+      v8 ring[PF];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
+      for (int i = 0; i < PF; ++i) ring[i] = rd(i);
 #pragma unroll
-      for (int T2 = 0; T2 < 2; ++T2) {
-        s[T2] = MM<T>::mma(*reinterpret_cast<const v8*>(Kb + offS[kk] + 32 * D * T2), qf[kk],
-                           s[T2]);
-        dp[T2] = MM<T>::mma(*reinterpret_cast<const v8*>(Vb + offS[kk] + 32 * D * T2), df[kk],
-                            dp[T2]);
+      for (int i = 0; i < NR; ++i) {
+        const int kk = i >> 2, T2 = (i >> 1) & 1;
+        if (i & 1) dp[T2] = MM<T>::mma(ring[i % PF], df[kk], dp[T2]);
+        else s[T2] = MM<T>::mma(ring[i % PF], qf[kk], s[T2]);
+        if (i + PF < NR) ring[i % PF] = rd(i + PF);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);  // the first PF LDS reads
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        if (i + PF < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
