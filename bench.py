@@ -236,7 +236,12 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
         fwd = lambda: mod.rope_qk_forward_with_saved(q, k, cos, sin)  # noqa: E731
         bwd_call = lambda saved: mod.rope_qk_backward_from_saved((inputs["dy"], dk), saved)  # noqa: E731
         values = {"q": q, "k": k, "cos": cos, "sin": sin}
-        autograd_fn = None
+        q_leaf, k_leaf = q.detach().requires_grad_(True), k.detach().requires_grad_(True)
+
+        def autograd_fn():
+            q_leaf.grad = k_leaf.grad = None
+            qo, ko = mod.RopeQK.apply(q_leaf, k_leaf, cos, sin)
+            torch.autograd.backward((qo, ko), (inputs["dy"], dk))
     else:
         f, b = lookup_pair(op, mod)
         args = [inputs.get(a.name, getattr(a, "default", None)) for a in op.args]
@@ -328,47 +333,55 @@ def cpu_baseline(name: str) -> dict:
     import torch
 
     from evograd_amd import decls
-    from evograd_amd.opdecl import Workload
-    from oracle.oracle import resolve_runtime_forward
+    from evograd_amd.inputs import make_case_inputs
+    from evograd_amd.opdecl import shape_tokens
+    from oracle.oracle import check_runtime_forward, resolve_runtime_forward
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     name, label = split_name(name)
     op = decls.get_op(name)
     w = bench_workload(op, label)
-    d = dict(w.dims)
+    d = w.dims
+    # The sample: leading slices of the benchmark's own GPU-seeded tensors.
     if name == "fused_linear_cross_entropy":
-        full_rows = d["rows"]
-        d["rows"] = 64
-        scale = full_rows / d["rows"]
-        sample = f"{d['rows']} of {full_rows} rows"
+        cut = {"rows": 64}
+        scale = d["rows"] / 64
+        sample = f"first 64 of {d['rows']} rows"
     elif name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm",
                   "cross_entropy"):
-        full_rows = d["rows"]
-        d["rows"] = max(1, full_rows // 8)
-        scale = full_rows / d["rows"]
-        sample = f"{d['rows']} of {full_rows} rows"
+        cut = {"rows": max(1, d["rows"] // 8)}
+        scale = d["rows"] / cut["rows"]
+        sample = f"first {cut['rows']} of {d['rows']} rows"
     elif name == "rope":
         full = d["B"] * (d["n_heads"] + int(w.extra["k_heads"]))
-        d["B"], d["n_heads"] = 1, 8
+        cut = {"B": 1, "n_heads": 8}
         scale = full / 8
-        sample = f"8 of {full} (batch, head) rows of q and k"
+        sample = f"8 of {full} (batch, head) rows of q and k (batch 0, query heads 0-7)"
     elif name == "causal_attention_gqa":
-        # one kv head and its group of query heads
+        # kv head 0 of batch 0 and its group of query heads
         full = d["B"] * d["KVH"]
-        d["H"] //= d["KVH"]
-        d["B"], d["KVH"] = 1, 1
+        cut = {"B": 1, "KVH": 1, "H": d["H"] // d["KVH"]}
         scale = float(full)
-        sample = f"1 of {full} (batch, kv head) groups of {d['H']} query heads"
+        sample = f"1 of {full} (batch, kv head) groups of {cut['H']} query heads"
     else:
         full = d["B"] * d["H"]
-        d["B"], d["H"] = 1, 1
+        cut = {"B": 1, "H": 1}
         scale = float(full)
         sample = f"1 of {full} (batch, head) pairs"
-    sw = Workload(dims=d, dtype=w.dtype, label=w.label, extra=w.extra)
-    from evograd_amd.inputs import make_case_inputs
-
-    inputs = make_case_inputs(op, sw, "cpu")
+    checked = check_runtime_forward(op, "cpu")
+    shapes = {a.name: a.shape for a in op.args if getattr(a, "shape", None)}
+    shapes[op.upstream_grad_name] = op.output.shape
+    inputs = {}
+    for key, value in make_case_inputs(op, w, "cuda").items():
+        tokens = shape_tokens(shapes.get(key))
+        if torch.is_tensor(value):
+            if tokens:
+                value = value[tuple(slice(0, cut[t]) if t in cut else slice(None)
+                                    for t in tokens)]
+            value = value.detach().to("cpu").contiguous()
+        inputs[key] = value
+    torch.cuda.empty_cache()
     fwd = resolve_runtime_forward(op)
     args = []
     leaves = []
@@ -394,8 +407,12 @@ def cpu_baseline(name: str) -> dict:
         step()
         samples.append((time.perf_counter_ns() - t0) / 1e3)
     us = statistics.median(samples) * scale
+    verified = (f"runtime forward held to {op.forward} on {checked} correctness workloads"
+                if checked else "the declared forward itself")
     return {"value": us, "unit": "us", "cores": cores, "kind": "port",
-            "sample": f"{sample}, {len(samples)} reps, median scaled x{scale:g}",
+            "sample": (f"{sample} of the benchmark's GPU-seeded inputs copied to the host, "
+                       f"{len(samples)} reps, median scaled x{scale:g} to the full workload"),
+            "timed_forward": f"{op.runtime_forward or op.forward} ({verified})",
             "what": f"eager torch autograd on CPU of {op.runtime_forward or op.forward}"}
 
 

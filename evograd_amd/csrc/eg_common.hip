@@ -67,20 +67,6 @@ int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what) {
   return check_launch(what);
 }
 
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 }  // namespace eg
 
 extern "C" int eg_abi_version(void) { return 1; }

@@ -226,8 +226,6 @@ bool timed_launch(hipEvent_t* start, hipEvent_t* stop);
 // safe inside a captured graph). Returns 0 or an error code.
 int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
 
-// Number of compute units of the current device (cached per device ordinal).
-int device_cus();
 
 }  // namespace eg
 

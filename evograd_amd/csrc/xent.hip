@@ -227,7 +227,10 @@ __global__ __launch_bounds__(256) void scale_copy_kernel(const TS* __restrict__ 
                                                          TO* __restrict__ dst, int64_t npack,
                                                          const TM* __restrict__ mul,
                                                          const float* __restrict__ div) {
-  const float f = (mul ? to_f32(mul[0]) : 1.f) / (div ? div[0] : 1.f);
+  // A zero divisor (no row counted toward a mean loss) scales by 0: the unit
+  // gradients are all zero then, and torch's gradient of such a loss is zero too.
+  const float d = div ? div[0] : 1.f;
+  const float f = d != 0.f ? (mul ? to_f32(mul[0]) : 1.f) / d : 0.f;
   const int64_t p0 = (int64_t)blockIdx.x * (256 * kScaleUnroll) + threadIdx.x;
   float v[kScaleUnroll][VEC];
 #pragma unroll

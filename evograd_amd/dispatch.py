@@ -1,21 +1,22 @@
-"""Shape dispatch between two autograd-pair programs (the reference's wire format).
+"""Two autograd-pair programs behind one pair, chosen by the call's shapes.
 
-Restates the dispatcher that src/evograd/dispatch.py:98-180 emits, so that a
-small-shape and a large-shape HIP program can ship behind one pair:
+Wire format (the reference's emitted dispatcher, src/evograd/dispatch.py:98-180,
+which a saved dispatcher module and its callers agree on):
 
-* the route is computed from the arguments' shapes: every declared tensor
-  argument binds its shape tokens to dims (integer tokens must match, a token
-  bound twice must agree), the declaration's ``regime_feature`` maps those dims
-  to a float, and the route is 0 (small program) below the threshold, 1 (large)
-  at or above it (dispatch.py:138-159);
-* the forward returns ``(output, (route, *saved))``: the saved state is prefixed
-  by a plain integer route tag, which carries no tensor bytes (dispatch.py:162-167);
-* the backward pops the tag and calls the same program's backward with the rest
-  of the saved state and any further arguments (dispatch.py:170-173).
+* the declaration's ``regime_feature`` maps the dims bound by the tensor
+  arguments' shapes to a float; below the threshold the call goes to program 0
+  (small shapes), at or above it to program 1;
+* the forward returns ``(y, (route, *saved))``: a plain ``int`` tag first, so the
+  tag adds no tensor bytes to the saved state;
+* the backward takes the tag off and hands the rest to the same program.
 
-``ShapeDispatch`` builds such a pair in-process from two loaded modules;
-``emit_dispatcher`` writes the same logic as a standalone module that loads the
-two programs from files, as the reference's ``_emit_dispatcher`` does.
+Design: the argument binding is :class:`evograd_amd.bind.CallPlan`'s (so a call
+binds the same way it would through ``bind``); each program's pair is resolved
+once, when the dispatcher is built; the shape-token unification sets each dim
+by its first binding and compares every later one against it.
+``emit_dispatcher`` writes a module file that rebuilds the same object from the
+two program files, so the pair can be handed to any tool that loads a candidate
+from a path.
 """
 
 from __future__ import annotations
@@ -24,132 +25,115 @@ import importlib.util
 from pathlib import Path
 from types import SimpleNamespace
 
-from .opdecl import OpDecl
+from .bind import CallPlan, lookup_pair
+from .opdecl import OpDecl, shape_tokens
 
-
-def _lookup(module, generic: str, prefixed: str):
-    value = getattr(module, generic, None)
-    return value if value is not None else getattr(module, prefixed)
+PACKAGE_ROOT = Path(__file__).resolve().parents[1]
 
 
 def shape_dims(op: OpDecl, args: tuple, kwargs: dict) -> dict:
-    """Dims bound by the declared tensor arguments' shapes (dispatch.py:139-157)."""
+    """The symbolic dims that the call's tensor arguments fix, e.g. {"rows": 3}."""
+    given = CallPlan.of(op).arrange(args, kwargs, fill_defaults=False)
     dims: dict = {}
-    for index, declared in enumerate(op.args):
-        shape = getattr(declared, "shape", None)
-        if shape is None:
+    for declared in op.args:
+        tokens = shape_tokens(getattr(declared, "shape", None))
+        if tokens is None:
             continue
-        if index < len(args):
-            value = args[index]
-        elif declared.name in kwargs:
-            value = kwargs[declared.name]
-        else:
-            raise TypeError(f"missing required argument {declared.name!r}")
-        tokens = [part.strip() for part in shape[1:-1].split(",") if part.strip()]
-        if len(tokens) != value.dim():
-            raise ValueError(f"{declared.name} rank mismatch: {tuple(value.shape)} vs {shape}")
-        for token, actual in zip(tokens, value.shape):
-            if token.isdigit():
-                if int(token) != int(actual):
-                    raise ValueError(f"{declared.name} fixed dimension {token} != {actual}")
-            elif token in dims and dims[token] != int(actual):
-                raise ValueError(f"inconsistent dimension {token}: {dims[token]} != {actual}")
-            else:
-                dims[token] = int(actual)
+        if declared.name not in given:
+            raise TypeError(f"{op.name}: shape dispatch needs tensor argument {declared.name!r}")
+        sizes = tuple(int(s) for s in given[declared.name].shape)
+        if len(sizes) != len(tokens):
+            raise ValueError(f"{op.name}: {declared.name} is {len(sizes)}-d {sizes}, "
+                             f"declared {declared.shape}")
+        for token, size in zip(tokens, sizes):
+            expected = int(token) if token.isdigit() else dims.setdefault(token, size)
+            if expected != size:
+                raise ValueError(f"{op.name}: {declared.name} has {token} = {size}, "
+                                 f"the call already fixed it at {expected}")
     return dims
 
 
 def route_for(op: OpDecl, threshold: float, args: tuple, kwargs: dict) -> int:
-    """0 for the small-shape program, 1 for the large one (dispatch.py:158-159)."""
+    """0 (small-shape program) when the regime feature is below ``threshold``, else 1."""
     if op.regime_feature is None:
-        raise ValueError(f"{op.name}: declaration has no regime_feature to dispatch on")
+        raise ValueError(f"{op.name}: the declaration defines no regime_feature")
     feature = float(op.regime_feature(SimpleNamespace(dims=shape_dims(op, args, kwargs))))
-    return 0 if feature < threshold else 1
+    return int(feature >= threshold)
 
 
 class ShapeDispatch:
-    """An autograd pair that routes each call to ``small`` or ``large``.
-
-    The object exposes ``forward_with_saved`` / ``backward_from_saved`` and the
-    prefixed ``<op>_forward_with_saved`` / ``<op>_backward_from_saved``, so
-    ``lookup_pair`` finds it like any candidate module. ``threshold`` defaults to
-    the declaration's ``regime_split``.
-    """
+    """A pair (generic and ``<op>_`` names) that routes each call to ``small`` or
+    ``large``; ``threshold`` defaults to the declaration's ``regime_split``."""
 
     def __init__(self, op: OpDecl, small, large, threshold: float | None = None):
+        threshold = op.regime_split if threshold is None else threshold
         if threshold is None:
-            threshold = op.regime_split
-        if threshold is None:
-            raise ValueError(f"{op.name}: no threshold and no regime_split")
+            raise ValueError(f"{op.name}: give a threshold (the declaration has no "
+                             "regime_split)")
         self.op = op
         self.threshold = float(threshold)
         self.programs = (small, large)
+        self._pairs = tuple(lookup_pair(op, program) for program in self.programs)
         setattr(self, op.forward_fn_name, self.forward_with_saved)
         setattr(self, op.backward_fn_name, self.backward_from_saved)
 
     def forward_with_saved(self, *args, **kwargs):
         route = route_for(self.op, self.threshold, args, kwargs)
-        forward = _lookup(self.programs[route], "forward_with_saved", self.op.forward_fn_name)
-        output, saved = forward(*args, **kwargs)
-        saved = tuple(saved) if isinstance(saved, (tuple, list)) else (saved,)
-        return output, (route, *saved)
+        y, saved = self._pairs[route][0](*args, **kwargs)
+        rest = tuple(saved) if isinstance(saved, (tuple, list)) else (saved,)
+        return y, (route,) + rest
 
-    def backward_from_saved(self, dout, saved_tensors, *args, **kwargs):
-        route, *saved = tuple(saved_tensors)
-        backward = _lookup(self.programs[int(route)], "backward_from_saved",
-                           self.op.backward_fn_name)
-        return backward(dout, tuple(saved), *args, **kwargs)
+    def backward_from_saved(self, dy, saved, *args, **kwargs):
+        route, rest = int(saved[0]), tuple(saved[1:])
+        return self._pairs[route][1](dy, rest, *args, **kwargs)
 
 
-_TEMPLATE = '''"""Shape dispatcher for {name}, written by evograd_amd.dispatch.emit_dispatcher.
-
-Routes at regime_feature < {threshold!r} to the small-shape program, else to the
-large one. Saved state is prefixed by a plain integer route tag, which
-contributes no tensor-memory bytes.
-"""
-import importlib.util as _ilu
-
-from evograd_amd.decls import get_op as _get_op
-from evograd_amd.dispatch import ShapeDispatch as _ShapeDispatch
-
-_SMALL_PATH = {small!r}
-_LARGE_PATH = {large!r}
-
-
-def _load(label, path):
-    spec = _ilu.spec_from_file_location("evograd_amd_dispatch_" + label, path)
-    module = _ilu.module_from_spec(spec)
+def load_module(path, prefix: str = "evograd_candidate_"):
+    """Execute a module file as a top-level module named ``prefix + stem`` (how
+    evograd's verify and bench commands load a candidate)."""
+    path = Path(path)
+    spec = importlib.util.spec_from_file_location(prefix + path.stem, str(path))
+    if spec is None or spec.loader is None:
+        raise ImportError(f"cannot load a module from {path}")
+    module = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(module)
     return module
 
 
-_PAIR = _ShapeDispatch(_get_op({name!r}), _load("small", _SMALL_PATH), _load("large", _LARGE_PATH),
-                       {threshold!r})
-{forward_fn} = _PAIR.forward_with_saved
-{backward_fn} = _PAIR.backward_from_saved
+_MODULE_SOURCE = '''"""{name}: shape-dispatched autograd pair (written by evograd_amd.dispatch).
+
+Calls whose regime feature is below {threshold!r} run {small_name}, the others
+{large_name}; the saved state starts with the route as a plain int.
+"""
+import sys as _sys
+
+if {root!r} not in _sys.path:
+    _sys.path.insert(0, {root!r})
+
+from evograd_amd.decls import get_op as _get_op
+from evograd_amd.dispatch import ShapeDispatch as _ShapeDispatch, load_module as _load_module
+
+_DISPATCH = _ShapeDispatch(
+    _get_op({name!r}),
+    _load_module({small!r}, "evograd_dispatch_small_"),
+    _load_module({large!r}, "evograd_dispatch_large_"),
+    {threshold!r},
+)
+{forward_fn} = _DISPATCH.forward_with_saved
+{backward_fn} = _DISPATCH.backward_from_saved
 '''
 
 
 def emit_dispatcher(op: OpDecl, small_path, large_path, threshold: float | None,
                     output) -> Path:
-    """Write a standalone dispatcher module (the reference's _emit_dispatcher)."""
-    if threshold is None:
-        threshold = op.regime_split
+    """Write a loadable module file holding a :class:`ShapeDispatch` over two program
+    files (absolute paths are recorded, so the file works from any directory)."""
+    threshold = op.regime_split if threshold is None else threshold
+    small, large = (Path(p).resolve() for p in (small_path, large_path))
     output = Path(output)
     output.parent.mkdir(parents=True, exist_ok=True)
-    output.write_text(
-        _TEMPLATE.format(name=op.name, threshold=float(threshold),
-                         small=str(Path(small_path).resolve()),
-                         large=str(Path(large_path).resolve()),
-                         forward_fn=op.forward_fn_name, backward_fn=op.backward_fn_name),
-        encoding="utf-8",
-    )
+    output.write_text(_MODULE_SOURCE.format(
+        name=op.name, threshold=float(threshold), root=str(PACKAGE_ROOT),
+        small=str(small), large=str(large), small_name=small.name, large_name=large.name,
+        forward_fn=op.forward_fn_name, backward_fn=op.backward_fn_name), encoding="utf-8")
     return output
-
-
-def load_module(path):
-    """Import a module from a file path (for emitted dispatchers)."""
-    spec = importlib.util.spec_from_file_location(Path(path).stem, str(path))
-    module = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(module)
-    return module

@@ -14,6 +14,7 @@ current stream, and medians are reported.
 from __future__ import annotations
 
 import statistics
+from dataclasses import dataclass
 from typing import Any, Callable
 
 import torch
@@ -59,6 +60,40 @@ def saved_state_report(saved, values: dict) -> dict:
         "new_storage_bytes": sum(unique.values()) - sum(retained.values()),
         "saved_tensors": describe_saved(saved),
     }
+
+
+@dataclass(frozen=True)
+class InputRecord:
+    """What a candidate must leave unchanged in one input tensor: its identity
+    (shape, strides, dtype, storage offset) always, its contents unless the
+    declaration lets the backward overwrite it (``contents`` is None then)."""
+
+    name: str
+    identity: tuple
+    contents: torch.Tensor | None
+
+
+def _identity(t: torch.Tensor) -> tuple:
+    return (tuple(t.shape), tuple(t.stride()), t.dtype, t.storage_offset())
+
+
+def record_inputs(values: dict, may_overwrite: tuple = ()) -> tuple:
+    """Record every tensor of a case (the rule of src/evograd/bench/fair.py:212-261)."""
+    return tuple(InputRecord(name, _identity(v),
+                             None if name in may_overwrite else v.detach().clone())
+                 for name, v in values.items() if torch.is_tensor(v))
+
+
+def check_inputs(values: dict, records: tuple, who: str) -> None:
+    """Raise RuntimeError naming the first input whose identity or contents changed."""
+    for rec in records:
+        now = values[rec.name]
+        if _identity(now) != rec.identity:
+            raise RuntimeError(f"{who}: input {rec.name!r} changed from "
+                               f"{rec.identity} to {_identity(now)} (shape, strides, "
+                               "dtype, storage offset)")
+        if rec.contents is not None and not torch.equal(now, rec.contents):
+            raise RuntimeError(f"{who}: input {rec.name!r} was written to")
 
 
 class CacheFlusher:

@@ -52,6 +52,16 @@ class Inactive:
         return self.shape is not None
 
 
+def shape_tokens(shape) -> tuple | None:
+    """``"[rows, cols]"`` -> ``("rows", "cols")``; None when no shape is declared."""
+    if not isinstance(shape, str):
+        return None
+    text = shape.strip()
+    if not (text.startswith("[") and text.endswith("]")):
+        return None
+    return tuple(t.strip() for t in text[1:-1].split(",") if t.strip())
+
+
 def bind_shape(shape: str, dims: dict[str, int]) -> tuple[int, ...]:
     """Resolve ``"[rows, cols]"`` against concrete dims (activity.py:84-100)."""
     text = shape.strip()

@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _lib
+from evograd_amd import _lib
 
 
 def as_contiguous(name: str, t: torch.Tensor) -> torch.Tensor:

@@ -8,10 +8,20 @@ plus fp32 mean and rstd [rows]. bias is not needed by the backward.
 
 from __future__ import annotations
 
+if not __package__:
+    # Loaded from this file's path as a top-level candidate module (evograd's verify
+    # and bench commands load a program that way): put the package root on sys.path.
+    import pathlib as _pathlib
+    import sys as _sys
+
+    _ROOT = str(_pathlib.Path(__file__).resolve().parents[2])
+    if _ROOT not in _sys.path:
+        _sys.path.insert(0, _ROOT)
+
 import torch
 
-from .. import _lib
-from ._util import as_contiguous, check_same, tag, workspace
+from evograd_amd import _lib
+from evograd_amd.pairs._util import as_contiguous, check_same, tag, workspace
 
 
 def layernorm_forward_with_saved(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,

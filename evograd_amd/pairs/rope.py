@@ -12,10 +12,20 @@ per token for both).
 
 from __future__ import annotations
 
+if not __package__:
+    # Loaded from this file's path as a top-level candidate module (evograd's verify
+    # and bench commands load a program that way): put the package root on sys.path.
+    import pathlib as _pathlib
+    import sys as _sys
+
+    _ROOT = str(_pathlib.Path(__file__).resolve().parents[2])
+    if _ROOT not in _sys.path:
+        _sys.path.insert(0, _ROOT)
+
 import torch
 
-from .. import _lib
-from ._util import as_contiguous, tag
+from evograd_amd import _lib
+from evograd_amd.pairs._util import as_contiguous, tag
 
 
 def _tables(x, cos, sin):
@@ -75,6 +85,22 @@ def rope_qk_forward_with_saved(q: torch.Tensor, k: torch.Tensor, cos: torch.Tens
     qo, ko = torch.empty_like(q), torch.empty_like(k)
     _launch(q, k, qo, ko, cos, sin, inverse=False)
     return (qo, ko), (cos, sin)
+
+
+class RopeQK(torch.autograd.Function):
+    """The joint q/k pair as an autograd node: ``RopeQK.apply(q, k, cos, sin)`` ->
+    ``(q', k')``; the tables get no gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, cos, sin):
+        (qo, ko), saved = rope_qk_forward_with_saved(q, k, cos, sin)
+        ctx.save_for_backward(*saved)
+        return qo, ko
+
+    @staticmethod
+    def backward(ctx, dq_out, dk_out):
+        dq, dk = rope_qk_backward_from_saved((dq_out, dk_out), ctx.saved_tensors)
+        return dq, dk, None, None
 
 
 def rope_qk_backward_from_saved(grads, saved):

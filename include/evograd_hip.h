@@ -252,7 +252,7 @@ int eg_flce_chunk(const float* logits, const int64_t* target, float* lse, float*
 
 /* dst[i] = src[i] * mul[0] / div[0] for n elements, with conversion from src_dtype
  * to dst_dtype; mul (of mul_dtype) and div (fp32) are device scalars and either
- * may be NULL (factor 1). Applies dloss / n_valid to the fused linear cross
+ * may be NULL (factor 1); a zero *div gives factor 0. Applies dloss / n_valid to the fused linear cross
  * entropy's saved gradients (the chain rule of
  * src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:116-123). */
 int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,

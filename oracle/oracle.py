@@ -33,6 +33,36 @@ def resolve_runtime_forward(op: OpDecl):
     return resolve_callable(op.runtime_forward or op.forward)
 
 
+_RUNTIME_CHECKED: set = set()
+
+
+def check_runtime_forward(op: OpDecl, device: str = "cpu") -> int:
+    """Hold the forward timed as the eager baseline (``runtime_forward``) to the
+    declared ``forward`` on every correctness workload before anything times it
+    (the reference's verify_runtime_forward, src/evograd/opdecl/baselines.py:82-121):
+    same shape, same dtype, allclose at the declaration's tolerance. Returns the
+    number of workloads checked (0 when the op declares no separate runtime
+    forward, so the timed function is the declared one); raises RuntimeError on a
+    disagreement."""
+    if not op.runtime_forward:
+        return 0
+    from evograd_amd.inputs import make_case_inputs
+
+    definition, runtime = resolve_forward(op), resolve_runtime_forward(op)
+    with torch.no_grad():
+        for w in op.correctness:
+            inputs = make_case_inputs(op, w, device)
+            args = [inputs.get(a.name, getattr(a, "default", None)) for a in op.args]
+            want, got = definition(*args), runtime(*args)
+            atol, rtol = op.tolerance_for(w, op.output.name)
+            if (got.shape != want.shape or got.dtype != want.dtype
+                    or not torch.allclose(got.float(), want.float(), atol=atol, rtol=rtol)):
+                raise RuntimeError(f"{op.name}: runtime forward {op.runtime_forward} differs "
+                                   f"from {op.forward} at {w.dims}/{w.dtype}")
+    _RUNTIME_CHECKED.add(op.name)
+    return len(op.correctness)
+
+
 def _promote(value, dtype):
     if torch.is_tensor(value) and value.is_floating_point():
         return value.to(dtype)

@@ -99,3 +99,26 @@ def test_saved_state_accounting():
     assert rep["retained_input_bytes"] == 8 * 16 * 4 + 16 * 4
     assert rep["new_storage_bytes"] == 8 * 4
     assert rep["logical_saved_bytes"] == saved_bytes(saved)
+
+
+def test_input_guard_names_a_mutated_or_reshaped_input():
+    from evograd_amd.harness import check_inputs, record_inputs
+
+    values = {"x": torch.randn(4, 8), "weight": torch.randn(8), "eps": 1e-5}
+    records = record_inputs(values, may_overwrite=("weight",))
+    check_inputs(values, records, "pair")
+    values["weight"].mul_(2)  # declared overwritable: contents exempt
+    check_inputs(values, records, "pair")
+    values["x"][1, 2] += 1
+    with pytest.raises(RuntimeError, match="'x' was written to"):
+        check_inputs(values, records, "pair")
+    values = {"x": torch.randn(4, 8)}
+    records = record_inputs(values)
+    values["x"] = values["x"].t()
+    with pytest.raises(RuntimeError, match="'x' changed"):
+        check_inputs(values, records, "pair")
+    values = {"weight": torch.randn(8)}
+    records = record_inputs(values, may_overwrite=("weight",))
+    values["weight"] = torch.randn(9)[1:]  # same shape, other storage offset
+    with pytest.raises(RuntimeError, match="'weight' changed"):
+        check_inputs(values, records, "pair")

@@ -43,11 +43,11 @@ def test_route_follows_regime_feature_and_split():
     assert route_for(op, op.regime_split, (torch.zeros(4096, 8), w), {}) == 1
     assert route_for(op, 10.0, (torch.zeros(9, 8),), {"weight": w}) == 0
     assert shape_dims(op, (torch.zeros(3, 8), w), {}) == {"rows": 3, "hidden": 8}
-    with pytest.raises(ValueError, match="rank mismatch"):
+    with pytest.raises(ValueError, match="is 3-d"):
         route_for(op, 10.0, (torch.zeros(3, 8, 1), w), {})
-    with pytest.raises(ValueError, match="inconsistent dimension"):
+    with pytest.raises(ValueError, match="already fixed it at 8"):
         route_for(op, 10.0, (torch.zeros(3, 8), torch.ones(7)), {})
-    with pytest.raises(TypeError, match="missing required argument"):
+    with pytest.raises(TypeError, match="needs tensor argument 'weight'"):
         route_for(op, 10.0, (torch.zeros(3, 8),), {})
 
 

@@ -87,13 +87,13 @@ def test_attention_gqa_matches_mha_on_repeated_kv():
     w = Workload(dims=dict(B=2, H=8, KVH=2, S=300, D=128), dtype="bfloat16")
     _note("gqa vs mha", w.dims)
     inp = make_case_inputs(GQA, w, "cuda")
-    mod = pair_module("causal_attention")
+    mha, gqa = pair_module("causal_attention"), pair_module("causal_attention_gqa")
     kr, vr = (inp[n].repeat_interleave(4, dim=1).contiguous() for n in ("k", "v"))
-    og, sg = mod.causal_attention_forward_with_saved(inp["q"], inp["k"], inp["v"])
-    om, sm = mod.causal_attention_forward_with_saved(inp["q"], kr, vr)
+    og, sg = gqa.causal_attention_gqa_forward_with_saved(inp["q"], inp["k"], inp["v"])
+    om, sm = mha.causal_attention_forward_with_saved(inp["q"], kr, vr)
     assert torch.equal(og, om) and torch.equal(sg[-1], sm[-1])
-    dqg, dkg, dvg = mod.causal_attention_backward_from_saved(inp["do"], sg)
-    dqm, dkm, dvm = mod.causal_attention_backward_from_saved(inp["do"], sm)
+    dqg, dkg, dvg = gqa.causal_attention_gqa_backward_from_saved(inp["do"], sg)
+    dqm, dkm, dvm = mha.causal_attention_backward_from_saved(inp["do"], sm)
     assert torch.equal(dqg, dqm)
     for a, b in ((dkg, dkm), (dvg, dvm)):
         ref = b.float().view(2, 2, 4, 300, 128).sum(2)

@@ -108,3 +108,27 @@ def test_flce_llama_size_gate():
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     assert rep.ok, "\n".join(rep.failures())
+
+
+@pytest.mark.parametrize("rows", [0, 24])
+def test_flce_with_no_counted_row_has_zero_gradients(rows):
+    """Every target ignored (or no rows at all): torch's loss is NaN (a mean over no
+    rows) and its gradients are zero; the dloss / n scaling must not turn the zero
+    unit gradients into NaN."""
+    mod = pair_module("fused_linear_cross_entropy")
+    _note("no counted row", rows)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(rows, 64, device="cuda", dtype=torch.bfloat16, generator=g)
+    wt = torch.randn(512, 64, device="cuda", dtype=torch.bfloat16, generator=g)
+    target = torch.full((rows,), -100, device="cuda", dtype=torch.int64)
+    loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(x, wt, target)
+    dx, dw = mod.fused_linear_cross_entropy_backward_from_saved(
+        torch.ones((), device="cuda", dtype=torch.float32), saved)
+    torch.cuda.synchronize()
+    xr, wr = x.float().cpu().requires_grad_(True), wt.float().cpu().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(xr @ wr.t(), target.cpu(), ignore_index=-100)
+    rgx, rgw = torch.autograd.grad(ref, (xr, wr))
+    assert torch.isnan(loss).item() and torch.isnan(ref).item()
+    assert dx.shape == x.shape and dw.shape == wt.shape
+    assert torch.equal(dx.float().cpu(), rgx) and torch.equal(dw.float().cpu(), rgw)
+    assert not torch.isnan(dw).any().item() and int(torch.count_nonzero(dw)) == 0

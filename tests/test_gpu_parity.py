@@ -138,6 +138,12 @@ def test_rope_joint_qk_partial_head_groups():
     _, gk = oracle(decls.ROPE, {"x": k, "cos": cos, "sin": sin, "dy": k})
     assert torch.allclose(dq.float(), gq["dx"].float(), atol=2e-2, rtol=2e-2)
     assert torch.allclose(dk.float(), gk["dx"].float(), atol=2e-2, rtol=2e-2)
+    # the same pair as an autograd node (the benchmark's autograd-bound step)
+    ql, kl = q.detach().requires_grad_(True), k.detach().requires_grad_(True)
+    qa, ka = mod.RopeQK.apply(ql, kl, cos, sin)
+    assert torch.equal(qa, qo) and torch.equal(ka, ko)
+    torch.autograd.backward((qa, ka), (q, k))
+    assert torch.equal(ql.grad, dq) and torch.equal(kl.grad, dk)
 
 
 def test_fused_add_rms_norm_backward_deterministic_and_grads_not_aliased():

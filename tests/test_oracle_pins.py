@@ -531,3 +531,63 @@ def test_flce_inputs_follow_recipe():
     assert torch.equal(a["target"], torch.randint(0, 512, (8,)))
     assert float(a["dloss"]) == 1.0
     assert op.memory_input_names() == ("x", "weight")
+
+
+# ------------------------------------------------------------- runtime forwards
+# The eager spellings the CPU baseline times. Each is pinned by closed forms of its
+# own and by agreement with the (pinned) declared forward on every correctness
+# workload; a planted mistake in one of them is caught by that agreement check.
+
+def test_runtime_forwards_closed_forms():
+    x = torch.full((3, 8), 2.0, dtype=torch.float64)
+    w = torch.linspace(0.5, 1.5, 8, dtype=torch.float64)
+    # constant row c: rms = |c|, so y = sign(c) * w / sqrt(1 + eps / c^2)
+    eps = 0.25
+    y = fr.rmsnorm_runtime_ref(x, w, eps)
+    assert torch.allclose(y, (w / math.sqrt(1 + eps / 4.0)).expand(3, 8), atol=1e-12)
+    # fused add: x' + r = 2 everywhere gives the constant-row case again
+    xp = torch.randn(3, 8, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    assert torch.allclose(fr.fused_add_rms_norm_runtime_ref(xp, x - xp, w, eps), y, atol=1e-12)
+    # layer norm: zero mean and unit biased variance before the affine map
+    g = torch.Generator().manual_seed(3)
+    xr = torch.randn(5, 16, generator=g, dtype=torch.float64) * 3 + 1
+    ln = fr.layernorm_runtime_ref(xr, torch.ones(16, dtype=torch.float64),
+                                  torch.zeros(16, dtype=torch.float64), 0.0)
+    assert torch.allclose(ln.mean(-1), torch.zeros(5, dtype=torch.float64), atol=1e-12)
+    assert torch.allclose(ln.var(-1, unbiased=False), torch.ones(5, dtype=torch.float64),
+                          atol=1e-10)
+    # attention: S = 1 gives v; the first query attends only to the first key
+    q, k, v = (torch.randn(1, 2, 5, 8, generator=g, dtype=torch.float64) for _ in range(3))
+    assert torch.allclose(fr.causal_attention_runtime_ref(q[:, :, :1], k[:, :, :1], v[:, :, :1]),
+                          v[:, :, :1], atol=1e-12)
+    o = fr.causal_attention_runtime_ref(q, k, v)
+    assert torch.allclose(o[:, :, 0], v[:, :, 0], atol=1e-12)
+    # grouped: kv head 0 serves query heads 0 and 1
+    og = fr.causal_attention_gqa_runtime_ref(q, k[:, :1], v[:, :1])
+    assert torch.allclose(og, fr.causal_attention_runtime_ref(q, k[:, :1].expand_as(q),
+                                                              v[:, :1].expand_as(q)), atol=1e-12)
+
+
+def test_runtime_forwards_agree_with_declared_forwards():
+    from oracle.oracle import check_runtime_forward
+
+    checked = {name: check_runtime_forward(op) for name, op in decls.OPS.items()}
+    for name in ("rmsnorm", "layernorm", "fused_add_rms_norm", "causal_attention",
+                 "causal_attention_gqa"):
+        assert checked[name] == len(decls.get_op(name).correctness) > 0, name
+    assert checked["softmax"] == 0  # no separate runtime forward: the declared one is timed
+
+
+def test_runtime_forward_check_catches_a_planted_mistake(monkeypatch):
+    from dataclasses import replace
+
+    from oracle.oracle import check_runtime_forward
+
+    def no_eps(x, weight, eps=1e-5):  # eps dropped
+        return fr.rmsnorm_runtime_ref(x, weight, 0.0) * (1 + 1e-2)
+
+    monkeypatch.setitem(fr.FORWARDS, "no_eps", no_eps)
+    monkeypatch.setattr(fr, "no_eps", no_eps, raising=False)
+    op = replace(decls.RMSNORM, runtime_forward="oracle.forward_refs:no_eps")
+    with pytest.raises(RuntimeError, match="differs"):
+        check_runtime_forward(op)
