@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_rmsnorm_fwd": (_i32, [_p, _p, _p, _p, _i64, _i64, _f32, _i32, _p]),
     "eg_rmsnorm_workspace_bytes": (_size, [_i64, _i64]),
     "eg_rmsnorm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
+    "eg_rmsnorm_bwd_noalloc": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_fused_add_rmsnorm_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _f32, _i32, _p]),
     "eg_fused_add_rmsnorm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_layernorm_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _i32, _p]),

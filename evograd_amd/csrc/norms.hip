@@ -39,6 +39,7 @@
 #include "eg_common.hpp"
 
 #include <initializer_list>
+#include <mutex>
 
 namespace eg {
 namespace {
@@ -1020,4 +1021,71 @@ extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weigh
     return launch_colsum<T>(pw, pb, (T*)dweight, (T*)dbias, 2, G, h, st,
                             "eg_layernorm_bwd(colsum)");
   });
+}
+
+// ------------------------------------------------- allocation-free backward
+// eg_rmsnorm_bwd_noalloc runs eg_rmsnorm_bwd's kernels with the partial rows in
+// `scratch`, a device-resident array of the library (one copy per GPU, held
+// until the process ends), for callers that cannot allocate. Every workgroup of
+// the ring writes its whole partial row before the column sum reads it, so the
+// array needs no clearing between calls. Calls that overlap on one GPU share the
+// array and race.
+static __device__ __align__(256) unsigned char scratch[EG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// The device address of `scratch` on the current device. The array's name is a
+// host-side stand-in; its device address comes from hipGetSymbolAddress, called
+// once per device with that device current.
+int scratch_address(const char* name, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no usable current device (%d)", name, dev);
+    return 1;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                hipGetErrorString(e));
+      return 1;
+    }
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int eg_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* weight,
+                                      const float* rstd, void* dx, void* dweight, int64_t rows,
+                                      int64_t hidden, int dtype, void* stream) {
+  static const char* name = "eg_rmsnorm_bwd_noalloc";
+  // rms_bwd_impl clears the error slot (and starts the kernel-timing hook's call)
+  if (check_norm_dims(name, rows, hidden)) return 1;
+  const size_t need = norm_workspace_bytes(rows, hidden, false);
+  if (need > (size_t)EG_NOALLOC_SCRATCH_BYTES) {
+    set_error("%s: rows=%lld hidden=%lld need %zu bytes of partial rows, more than the "
+              "%d-byte scratch; use eg_rmsnorm_bwd with a workspace", name, (long long)rows,
+              (long long)hidden, need, EG_NOALLOC_SCRATCH_BYTES);
+    return 1;
+  }
+  const hipStream_t st = as_stream(stream);
+  if (st) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || hipGetStreamDeviceId(st) != cur) {
+      set_error("%s: the stream belongs to device %d, not the current device %d", name,
+                hipGetStreamDeviceId(st), cur);
+      return 1;
+    }
+  }
+  void* part = nullptr;
+  if (rows > 0 && scratch_address(name, &part)) return 1;
+  return rms_bwd_impl<false>(name, dy, x, nullptr, weight, rstd, dx, dweight, part, rows, hidden,
+                             dtype, stream);
 }

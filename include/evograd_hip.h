@@ -88,6 +88,21 @@ int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const floa
                    void* dx, void* dweight, void* workspace, int64_t rows, int64_t hidden,
                    int dtype, void* stream);
 
+/* Size of the device-resident scratch array behind eg_rmsnorm_bwd_noalloc (16 MiB
+ * per GPU: the [G, hidden] fp32 partial rows for hidden up to 8192). */
+#define EG_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+
+/* No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * eg_rmsnorm_bwd without the workspace argument: the partial rows live in a
+ * library-owned device array of EG_NOALLOC_SCRATCH_BYTES per GPU, so the call
+ * allocates nothing. Sizes whose partial rows exceed it (eg_rmsnorm_workspace_bytes
+ * > EG_NOALLOC_SCRATCH_BYTES) are refused with an error. `stream` must belong to
+ * the current device. Calls that overlap on one GPU share the array and race. */
+int eg_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* weight,
+                           const float* rstd, void* dx, void* dweight, int64_t rows,
+                           int64_t hidden, int dtype, void* stream);
+
 /* ----------------------------------------------------- fused_add_rms_norm
  * Replaces fused_add_rms_norm_forward_ref
  * (src/evograd/ops/level2/fused_add_rms_norm/forward_ref.py:6-16):

@@ -67,6 +67,10 @@ def test_host_side_validation_errors_without_gpu():
     with pytest.raises(RuntimeError, match="out of range"):
         _lib.call("eg_cross_entropy_bwd", 16, 16, 16, 16, 16, 16, (1 << 24) + 1, 8, -100,
                   _lib.EG_BF16, None)
+    # the allocation-free backward refuses sizes whose partial rows exceed its scratch
+    with pytest.raises(RuntimeError, match="more than the 16777216-byte scratch"):
+        _lib.call("eg_rmsnorm_bwd_noalloc", 16, 16, 16, 16, 16, 16, 16384, 16384,
+                  _lib.EG_BF16, None)
     # empty inputs are a no-op, not an error
     _lib.call("eg_softmax_fwd", None, None, 0, 0, _lib.EG_F32, None)
     _lib.call("eg_cross_entropy_bwd", None, None, None, None, None, None, 0, 8, -100,
