@@ -44,7 +44,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
 ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
-           "fused_add_rms_norm", "causal_attention_gqa", "cross_entropy",
+           "fused_add_rms_norm", "causal_attention_gqa", "llama3_attention", "cross_entropy",
            "fused_linear_cross_entropy", "softmax@vocab")
 
 
@@ -114,7 +114,7 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
         xb = B * (H + extra_k_heads) * T * D * es
         tables = 2 * T * D * 4
         return {"unit": "bytes", "fwd": 2 * xb + tables, "bwd": 2 * xb + tables}
-    if name in ("causal_attention", "causal_attention_gqa"):
+    if name in ("causal_attention", "causal_attention_gqa", "llama3_attention"):
         B, H, S, D = d["B"], d["H"], d["S"], d["D"]  # FLOPs count query heads
         dense = 2.0 * S * S * D * B * H  # one S x S x D product
         return {"unit": "flops", "fwd": 2 * dense / 2, "bwd": 5 * dense / 2}
@@ -133,7 +133,11 @@ KERNELS = {
     "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
     "causal_attention_gqa": {"fwd": ["attn_fwd_kernel"],
                              "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
-    "cross_entropy": {"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
+    # k rotated into the workspace, then the forward rotating q as it loads it;
+    # the backward rotates q and k again before the two attention kernels
+    "llama3_attention": {"fwd": ["rope_kernel", "attn_fwd_kernel"],
+                         "bwd": ["rope_kernel", "attn_dq_kernel", "attn_dkdv_kernel"]},
+    "cross_entropy":{"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
                       "bwd": ["xent_bwd_flat_kernel"]},
     # first chunk's launches of the forward; the backward's dx scaling
     "fused_linear_cross_entropy": {"fwd": ["xent_lse_kernel", "xent_bwd_flat_kernel"],
@@ -148,6 +152,7 @@ DOMINANT = {
     "softmax": ("bwd", 0), "rmsnorm": ("bwd", 0), "layernorm": ("bwd", 0),
     "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
     "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
+    "llama3_attention": ("bwd", 2),
     "cross_entropy": ("bwd", 0),
     "fused_linear_cross_entropy": ("fwd", 1),
     "softmax@vocab": ("bwd", 0),
@@ -171,7 +176,7 @@ def dominant_work(name: str, w, work: dict) -> float:
         return work["bwd"] - d["cols"] * es
     if name == "layernorm":  # the column sum writes dweight and dbias
         return work["bwd"] - 2 * d["hidden"] * es
-    if name in ("causal_attention", "causal_attention_gqa"):
+    if name in ("causal_attention", "causal_attention_gqa", "llama3_attention"):
         # dK/dV kernel: S, dP, dV, dK of the five products
         return work["bwd"] * 4 / 5
     phase = DOMINANT[name][0]
@@ -358,7 +363,7 @@ def cpu_baseline(name: str) -> dict:
         cut = {"B": 1, "n_heads": 8}
         scale = full / 8
         sample = f"8 of {full} (batch, head) rows of q and k (batch 0, query heads 0-7)"
-    elif name == "causal_attention_gqa":
+    elif name in ("causal_attention_gqa", "llama3_attention"):
         # kv head 0 of batch 0 and its group of query heads
         full = d["B"] * d["KVH"]
         cut = {"B": 1, "KVH": 1, "H": d["H"] // d["KVH"]}

@@ -6,8 +6,8 @@ Layout:
 * ``_lib``      ctypes binding of that library (no CPU fallback)
 * ``opdecl``    the torch-free declaration contract (Active, Inactive, Workload, OpDecl)
 * ``decls``     declarations of softmax, rmsnorm, layernorm, swiglu, rope, causal_attention,
-                fused_add_rms_norm, causal_attention_gqa, cross_entropy,
-                fused_linear_cross_entropy
+                fused_add_rms_norm, causal_attention_gqa, llama3_attention (RoPE on q, k
+                then grouped causal attention), cross_entropy, fused_linear_cross_entropy
 * ``pairs``     one module per operator with the reference's
                 ``<op>_forward_with_saved`` / ``<op>_backward_from_saved`` functions
 * ``bind``      ``bind(op, module)`` -> a ``torch.autograd.Function``-backed callable
@@ -25,6 +25,7 @@ PAIR_MODULES = {
     "causal_attention": "evograd_amd.pairs.attention",
     "fused_add_rms_norm": "evograd_amd.pairs.fused_add_rms_norm",
     "causal_attention_gqa": "evograd_amd.pairs.attention_gqa",
+    "llama3_attention": "evograd_amd.pairs.llama3_attention",
     "cross_entropy": "evograd_amd.pairs.cross_entropy",
     "fused_linear_cross_entropy": "evograd_amd.pairs.fused_linear_cross_entropy",
 }

@@ -58,6 +58,9 @@ SIGNATURES: dict[str, tuple] = {
     "eg_attn_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "eg_attn_gqa_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "eg_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
+    "eg_llama3_attn_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
+    "eg_llama3_attn_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
+    "eg_llama3_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "eg_cross_entropy_workspace_bytes": (_size, [_i64]),
     "eg_cross_entropy_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p]),
     "eg_cross_entropy_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p]),

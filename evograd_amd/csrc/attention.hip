@@ -130,6 +130,80 @@ __device__ __forceinline__ void store_rows(uint16_t* __restrict__ row, const f32
   }
 }
 
+// RoPE on a query row held as MFMA operands (the decoder layer's q rotation,
+// src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:42-51, fused into the
+// forward's Q load): f[kk] holds columns 16kk + 8hh .. +7, so f[kk] and
+// f[kk + KSTEPS/2] are the two halves of the same 8 rotation pairs.
+//   y1 = x1 cos1 - x2 sin1,  y2 = x2 cos2 + x1 sin2   (fp32, rounded once)
+template <typename T, int D>
+__device__ __forceinline__ void rotate_row(typename MM<T>::v8* f, const float* __restrict__ cr,
+                                           const float* __restrict__ sr, int hh) {
+  constexpr int H2 = D / 32;  // KSTEPS / 2
+#pragma unroll
+  for (int kk = 0; kk < H2; ++kk) {
+    const int col = 16 * kk + 8 * hh;
+    uint4 u1, u2;
+    __builtin_memcpy(&u1, &f[kk], 16);
+    __builtin_memcpy(&u2, &f[kk + H2], 16);
+    const uint32_t w1[4] = {u1.x, u1.y, u1.z, u1.w}, w2[4] = {u2.x, u2.y, u2.z, u2.w};
+    float c1[8], s1[8], c2[8], s2[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float4 a = *reinterpret_cast<const float4*>(cr + col + 4 * h);
+      const float4 b = *reinterpret_cast<const float4*>(sr + col + 4 * h);
+      const float4 c = *reinterpret_cast<const float4*>(cr + col + D / 2 + 4 * h);
+      const float4 d = *reinterpret_cast<const float4*>(sr + col + D / 2 + 4 * h);
+      c1[4 * h] = a.x; c1[4 * h + 1] = a.y; c1[4 * h + 2] = a.z; c1[4 * h + 3] = a.w;
+      s1[4 * h] = b.x; s1[4 * h + 1] = b.y; s1[4 * h + 2] = b.z; s1[4 * h + 3] = b.w;
+      c2[4 * h] = c.x; c2[4 * h + 1] = c.y; c2[4 * h + 2] = c.z; c2[4 * h + 3] = c.w;
+      s2[4 * h] = d.x; s2[4 * h + 1] = d.y; s2[4 * h + 2] = d.z; s2[4 * h + 3] = d.w;
+    }
+    uint32_t o1[4], o2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x1l = half_lo<T>(w1[e]), x1h = half_hi<T>(w1[e]);
+      const float x2l = half_lo<T>(w2[e]), x2h = half_hi<T>(w2[e]);
+      const int i = 2 * e;
+      o1[e] = MM<T>::pack2(x1l * c1[i] - x2l * s1[i], x1h * c1[i + 1] - x2h * s1[i + 1]);
+      o2[e] = MM<T>::pack2(x2l * c2[i] + x1l * s2[i], x2h * c2[i + 1] + x1h * s2[i + 1]);
+    }
+    u1 = make_uint4(o1[0], o1[1], o1[2], o1[3]);
+    u2 = make_uint4(o2[0], o2[1], o2[2], o2[3]);
+    __builtin_memcpy(&f[kk], &u1, 16);
+    __builtin_memcpy(&f[kk + H2], &u2, 16);
+  }
+}
+
+// The transpose of RoPE applied to a gradient held as transposed result tiles
+// (lane = one row of the output, register r of tile t = column 32t + 8(r/4) +
+// 4hh + r%4; tiles t and t + DT/2 hold the two halves): with a the first-half and
+// b the second-half entries,
+//   a' = a cos1 + b sin2,  b' = b cos2 - a sin1
+// the gradient of the rotation above (cr, sr: this row of the tables).
+template <int D>
+__device__ __forceinline__ void unrotate_rows(f32x16* acc, const float* __restrict__ cr,
+                                              const float* __restrict__ sr, int hh) {
+  constexpr int H2 = D / 64;  // DT / 2
+#pragma unroll
+  for (int t = 0; t < H2; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * t + 8 * g + 4 * hh;
+      const float4 c1 = *reinterpret_cast<const float4*>(cr + d);
+      const float4 s1 = *reinterpret_cast<const float4*>(sr + d);
+      const float4 c2 = *reinterpret_cast<const float4*>(cr + d + D / 2);
+      const float4 s2 = *reinterpret_cast<const float4*>(sr + d + D / 2);
+      const float cv1[4] = {c1.x, c1.y, c1.z, c1.w}, sv1[4] = {s1.x, s1.y, s1.z, s1.w};
+      const float cv2[4] = {c2.x, c2.y, c2.z, c2.w}, sv2[4] = {s2.x, s2.y, s2.z, s2.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = acc[t][4 * g + i], b = acc[t + H2][4 * g + i];
+        acc[t][4 * g + i] = a * cv1[i] + b * sv2[i];
+        acc[t + H2][4 * g + i] = b * cv2[i] - a * sv1[i];
+      }
+    }
+}
+
 template <int D>
 __device__ __forceinline__ int swz(int row) {
   return (((row & 3) << 2) | ((row >> 2) & 3)) & (D / 8 - 1);
@@ -229,11 +303,12 @@ __device__ __forceinline__ int query_head(int v, int BHkv, int group) {
 }
 
 // ------------------------------------------------------------------ forward
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, bool ROPE>
 __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int S,
-    float scale_log2, int nqb, int BH, int group) {
+    float scale_log2, int nqb, int BH, int group, const float* __restrict__ rope_cos,
+    const float* __restrict__ rope_sin) {
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
@@ -292,6 +367,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
   ld.init();
   ld.load(kp, 0, S, Ks[0]);
   ld.load(vp, 0, S, Vs[0]);
+  // The rotation waits for q and the tables, so it comes after the first tile's
+  // loads are issued: those are in flight meanwhile.
+  if constexpr (ROPE)
+    rotate_row<T, D>(qf, rope_cos + (int64_t)qrc * D, rope_sin + (int64_t)qrc * D, hh);
   auto tile = [&](auto bufc, int j) {
     constexpr int buf = decltype(bufc)::value;
     wait_loads();
@@ -402,12 +481,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
 }
 
 // ------------------------------------------------------------ dK, dV
-template <typename T, int D, int NW, int BQ>
+template <typename T, int D, int NW, int BQ, bool ROPE>
 __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
-    uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int BHkv, int group) {
+    uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int BHkv, int group,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
   using v8 = typename MM<T>::v8;
   constexpr int BK = 32 * NW;
   constexpr int KSTEPS = D / 16, DT = D / 32, MT = BQ / 32;
@@ -563,22 +643,29 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   if (key < S) {
     uint16_t* dkp = dk + base + (int64_t)key * D;
     uint16_t* dvp = dv + base + (int64_t)key * D;
+    float fk = scale;
+    if constexpr (ROPE) {  // dk of the pre-rotation keys: the rotation's transpose
+#pragma unroll
+      for (int t = 0; t < DT; ++t) dka[t] *= scale;
+      unrotate_rows<D>(dka, rope_cos + (int64_t)key * D, rope_sin + (int64_t)key * D, hh);
+      fk = 1.0f;
+    }
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      store_rows<T>(dkp, dka[t], t, hh, scale);
+      store_rows<T>(dkp, dka[t], t, hh, fk);
       store_rows<T>(dvp, dva[t], t, hh, 1.0f);
     }
   }
 }
 
 // ------------------------------------------------------------------- dQ
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, bool ROPE>
 __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const uint16_t* __restrict__ o, const float* __restrict__ lse, float* __restrict__ delta,
     uint16_t* __restrict__ dq, int S, float scale, float scale_log2, int nqb, int BH,
-    int group) {
+    int group, const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
@@ -738,8 +825,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
 
   if (qrow < S) {
     uint16_t* op = dq + base + (int64_t)qrow * D;
+    float fq = scale;
+    if constexpr (ROPE) {  // dq of the pre-rotation queries: the rotation's transpose
 #pragma unroll
-    for (int t = 0; t < DT; ++t) store_rows<T>(op, acc[t], t, hh, scale);
+      for (int t = 0; t < DT; ++t) acc[t] *= scale;
+      unrotate_rows<D>(acc, rope_cos + (int64_t)qrow * D, rope_sin + (int64_t)qrow * D, hh);
+      fq = 1.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) store_rows<T>(op, acc[t], t, hh, fq);
   }
 }
 
@@ -774,58 +868,70 @@ inline unsigned grid_for(int64_t BH, int nblocks) {
   return (unsigned)(((BH + 7) / 8) * 8 * nblocks);
 }
 
-template <typename T, int D>
+// With ROPE, q is rotated in registers by the fp32 tables rc/rs [S, D] as it is
+// loaded (k must already be rotated).
+template <typename T, int D, bool ROPE = false>
 int attn_fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
-                    int64_t S, int group, float scale, hipStream_t st) {
+                    int64_t S, int group, float scale, hipStream_t st,
+                    const float* rc = nullptr, const float* rs = nullptr) {
   constexpr int NW = kFwdWaves;
   const int nqb = (int)((S + 32 * NW - 1) / (32 * NW));
-  EG_LAUNCH((attn_fwd_kernel<T, D, NW>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
+  EG_LAUNCH((attn_fwd_kernel<T, D, NW, ROPE>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
             (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, (int)S,
-            scale * kLog2e, nqb, (int)BH, group);
+            scale * kLog2e, nqb, (int)BH, group, rc, rs);
   return check_launch("eg_attn_fwd");
 }
 
 // BH counts query heads (x batch); the key/value tensors hold BH / group heads.
-template <typename T, int D>
+// With ROPE, q and k are the rotated tensors and dq, dk are written for the
+// pre-rotation ones (the rotation's transpose applied to the results in registers).
+template <typename T, int D, bool ROPE = false>
 int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* v, const void* o,
                     const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t BH,
-                    int64_t S, int group, float scale, hipStream_t st) {
+                    int64_t S, int group, float scale, hipStream_t st,
+                    const float* rc = nullptr, const float* rs = nullptr) {
   // dQ first: it also computes delta = rowsum(do * o) for its rows, which the
   // dK/dV kernel reads.
   constexpr int NQ = kDqWaves;
   const int nqb = (int)((S + 32 * NQ - 1) / (32 * NQ));
-  EG_LAUNCH((attn_dq_kernel<T, D, NQ>), dim3(grid_for(BH, nqb)), dim3(NQ * 64), 0, st,
+  EG_LAUNCH((attn_dq_kernel<T, D, NQ, ROPE>), dim3(grid_for(BH, nqb)), dim3(NQ * 64), 0, st,
             (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
             (const uint16_t*)o, lse, delta, (uint16_t*)dq, (int)S, scale, scale * kLog2e, nqb,
-            (int)BH, group);
+            (int)BH, group, rc, rs);
   if (int rc = check_launch("eg_attn_bwd(dq)")) return rc;
   constexpr int NK = dkdv_waves<D>();
   const int nkb = (int)((S + 32 * NK - 1) / (32 * NK));
   const int64_t BHkv = BH / group;
-  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows>), dim3(grid_for(BHkv, nkb)), dim3(NK * 64), 0,
-            st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
-            lse, delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale, scale * kLog2e, (int)BHkv,
-            group);
+  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows, ROPE>), dim3(grid_for(BHkv, nkb)),
+            dim3(NK * 64), 0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+            (const uint16_t*)dout, lse, delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale,
+            scale * kLog2e, (int)BHkv, group, rc, rs);
   return check_launch("eg_attn_bwd(dkdv)");
 }
 
 // Explicit instantiations: hip-clang leaves some implicitly instantiated kernel
 // templates without a host launch stub (undefined symbol at load time); naming
 // every kernel here makes the stubs certain.
-#define EG_ATTN_INSTANTIATE(T, D)                                                            \
-  template __global__ void attn_fwd_kernel<T, D, kFwdWaves>(                                 \
+#define EG_ATTN_INSTANTIATE(T, D, R)                                                         \
+  template __global__ void attn_fwd_kernel<T, D, kFwdWaves, R>(                              \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, float, int,   \
-      int, int);                                                                             \
-  template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows>(               \
+      int, int, const float*, const float*);                                                 \
+  template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows, R>(            \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
-      const float*, uint16_t*, uint16_t*, int, float, float, int, int);                        \
-  template __global__ void attn_dq_kernel<T, D, kDqWaves>(                                   \
+      const float*, uint16_t*, uint16_t*, int, float, float, int, int, const float*,           \
+      const float*);                                                                         \
+  template __global__ void attn_dq_kernel<T, D, kDqWaves, R>(                                \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,     \
-      const float*, float*, uint16_t*, int, float, float, int, int, int);
-EG_ATTN_INSTANTIATE(bf16_t, 128)
-EG_ATTN_INSTANTIATE(bf16_t, 64)
-EG_ATTN_INSTANTIATE(f16_t, 128)
-EG_ATTN_INSTANTIATE(f16_t, 64)
+      const float*, float*, uint16_t*, int, float, float, int, int, int, const float*,         \
+      const float*);
+EG_ATTN_INSTANTIATE(bf16_t, 128, false)
+EG_ATTN_INSTANTIATE(bf16_t, 64, false)
+EG_ATTN_INSTANTIATE(f16_t, 128, false)
+EG_ATTN_INSTANTIATE(f16_t, 64, false)
+EG_ATTN_INSTANTIATE(bf16_t, 128, true)
+EG_ATTN_INSTANTIATE(bf16_t, 64, true)
+EG_ATTN_INSTANTIATE(f16_t, 128, true)
+EG_ATTN_INSTANTIATE(f16_t, 64, true)
 #undef EG_ATTN_INSTANTIATE
 
 bool attn_aligned(std::initializer_list<const void*> ptrs) {
@@ -905,4 +1011,98 @@ extern "C" int eg_attn_bwd(const void* dout, const void* q, const void* k, const
                            int64_t head_dim, float scale, int dtype, void* stream) {
   return eg_attn_gqa_bwd(dout, q, k, v, o, lse, dq, dk, dv, workspace, batch, heads, heads, seq,
                          head_dim, scale, dtype, stream);
+}
+
+// ----------------------------------------- RoPE(q, k) -> grouped causal attention
+// The attention half of the Llama-3 decoder layer
+// (src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:93-107): q and k
+// rotated by fp32 tables cos/sin [S, D], then causal GQA attention. The forward
+// rotates k into the workspace (one small pass over the kv heads) and q in the
+// attention kernel's registers as it loads them; the backward rotates q and k into
+// the workspace again (the saved state holds the pre-rotation inputs only) and
+// applies the rotation's transpose to dq and dk in the kernels' registers before
+// the stores. Backward workspace: q_r [B, H, S, D], k_r [B, Hkv, S, D] (dtype),
+// delta [B, H, S] fp32, in that order; the forward's holds only its k_r.
+static size_t llama3_ws_qr(int64_t B, int64_t H, int64_t S, int64_t D) { return (size_t)(B * H * S * D) * 2; }
+static size_t llama3_ws_kr(int64_t B, int64_t Hkv, int64_t S, int64_t D) { return (size_t)(B * Hkv * S * D) * 2; }
+
+extern "C" size_t eg_llama3_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                                 int64_t seq, int64_t head_dim) {
+  if (batch <= 0 || heads <= 0 || kv_heads <= 0 || seq <= 0 || head_dim <= 0) return 0;
+  return llama3_ws_qr(batch, heads, seq, head_dim) + llama3_ws_kr(batch, kv_heads, seq, head_dim) +
+         (size_t)(batch * heads * seq) * sizeof(float);
+}
+
+template <typename F>
+static int llama3_dispatch(int dtype, int64_t head_dim, F&& f) {
+  if (dtype == EG_BF16)
+    return head_dim == 128 ? f(bf16_t{}, std::integral_constant<int, 128>{})
+                           : f(bf16_t{}, std::integral_constant<int, 64>{});
+  return head_dim == 128 ? f(f16_t{}, std::integral_constant<int, 128>{})
+                         : f(f16_t{}, std::integral_constant<int, 64>{});
+}
+
+extern "C" int eg_llama3_attn_fwd(const void* q, const void* k, const void* v, const float* cos,
+                                  const float* sin, void* o, float* lse, void* workspace,
+                                  int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                                  int64_t head_dim, float scale, int dtype, void* stream) {
+  static const char* name = "eg_llama3_attn_fwd";
+  clear_error();
+  if (check_attn(name, batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
+  if (batch == 0 || heads == 0 || seq == 0) return 0;
+  if (!q || !k || !v || !cos || !sin || !o || !lse || !workspace) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  if (!attn_aligned({q, k, v, o, cos, sin, workspace})) {
+    set_error("%s: tensors, tables and workspace must be 16-byte aligned", name);
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  void* k_r = workspace;
+  if (int rc = rope_apply(nullptr, k, nullptr, k_r, cos, sin, batch, 0, kv_heads, seq, head_dim,
+                          dtype, EG_F32, false, st))
+    return rc;
+  const int64_t BH = batch * heads;
+  const int group = (int)(heads / kv_heads);
+  return llama3_dispatch(dtype, head_dim, [&](auto tc, auto dc) {
+    using T = decltype(tc);
+    return attn_fwd_launch<T, decltype(dc)::value, true>(q, k_r, v, o, lse, BH, seq, group, scale,
+                                                         st, cos, sin);
+  });
+}
+
+extern "C" int eg_llama3_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                                  const void* o, const float* lse, const float* cos,
+                                  const float* sin, void* dq, void* dk, void* dv, void* workspace,
+                                  int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                                  int64_t head_dim, float scale, int dtype, void* stream) {
+  static const char* name = "eg_llama3_attn_bwd";
+  clear_error();
+  if (check_attn(name, batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
+  if (batch == 0 || heads == 0 || seq == 0) return 0;
+  if (!dout || !q || !k || !v || !o || !lse || !cos || !sin || !dq || !dk || !dv || !workspace) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  if (!attn_aligned({dout, q, k, v, o, cos, sin, dq, dk, dv, workspace})) {
+    set_error("%s: tensors, tables and workspace must be 16-byte aligned", name);
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  char* ws = (char*)workspace;
+  void* q_r = ws;
+  void* k_r = ws + llama3_ws_qr(batch, heads, seq, head_dim);
+  float* delta = (float*)((char*)k_r + llama3_ws_kr(batch, kv_heads, seq, head_dim));
+  if (int rc = rope_apply(q, k, q_r, k_r, cos, sin, batch, heads, kv_heads, seq, head_dim, dtype,
+                          EG_F32, false, st))
+    return rc;
+  const int64_t BH = batch * heads;
+  const int group = (int)(heads / kv_heads);
+  return llama3_dispatch(dtype, head_dim, [&](auto tc, auto dc) {
+    using T = decltype(tc);
+    return attn_bwd_launch<T, decltype(dc)::value, true>(dout, q_r, k_r, v, o, lse, dq, dk, dv,
+                                                         delta, BH, seq, group, scale, st, cos,
+                                                         sin);
+  });
 }

@@ -226,6 +226,13 @@ bool timed_launch(hipEvent_t* start, hipEvent_t* stop);
 // safe inside a captured graph). Returns 0 or an error code.
 int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
 
+// The RoPE launch behind eg_rope (rope.hip), for entry points that rotate as one
+// step of a longer launch sequence: arguments as eg_rope's, already validated.
+int rope_apply(const void* q, const void* k, void* q_out, void* k_out, const void* cos,
+               const void* sin, int64_t batch, int64_t heads_q, int64_t heads_k,
+               int64_t tokens, int64_t head_dim, int dtype, int table_dtype, bool inverse,
+               hipStream_t st);
+
 
 }  // namespace eg
 

@@ -133,6 +133,22 @@ int rope_dispatch_vec(const void* q, const void* k, void* qo, void* ko, const vo
 }
 
 }  // namespace
+
+int rope_apply(const void* q, const void* k, void* q_out, void* k_out, const void* cos,
+               const void* sin, int64_t batch, int64_t heads_q, int64_t heads_k,
+               int64_t tokens, int64_t head_dim, int dtype, int table_dtype, bool inverse,
+               hipStream_t st) {
+  const float sgn = inverse ? -1.0f : 1.0f;
+  return EG_DISPATCH_FLOAT(dtype, "eg_rope", [&] {
+    using T = scalar_t;
+    if (table_dtype == EG_F32)
+      return rope_dispatch_vec<T, float>(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k,
+                                         tokens, head_dim, sgn, st);
+    return rope_dispatch_vec<T, T>(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k, tokens,
+                                   head_dim, sgn, st);
+  });
+}
+
 }  // namespace eg
 
 using namespace eg;
@@ -160,14 +176,6 @@ extern "C" int eg_rope(const void* q, const void* k, void* q_out, void* k_out, c
     set_error("eg_rope: table dtype must be fp32 or the tensor dtype");
     return 1;
   }
-  const float sgn = inverse ? -1.0f : 1.0f;
-  hipStream_t st = as_stream(stream);
-  return EG_DISPATCH_FLOAT(dtype, "eg_rope", [&] {
-    using T = scalar_t;
-    if (table_dtype == EG_F32)
-      return rope_dispatch_vec<T, float>(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k,
-                                         tokens, head_dim, sgn, st);
-    return rope_dispatch_vec<T, T>(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k, tokens,
-                                   head_dim, sgn, st);
-  });
+  return rope_apply(q, k, q_out, k_out, cos, sin, batch, heads_q, heads_k, tokens, head_dim,
+                    dtype, table_dtype, inverse != 0, as_stream(stream));
 }

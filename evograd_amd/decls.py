@@ -393,6 +393,59 @@ CAUSAL_ATTENTION_GQA = declare_op(
     regime_split=LLAMA_REGIME_SPLIT,
 )
 
+# ------------------------------ RoPE(q, k) -> grouped causal attention (one pair)
+# The attention half of the Llama-3 decoder layer,
+# src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:93-107, as one
+# autograd pair. Block-level saved-state choice (the layer's own note,
+# llama3_decoder_layer/__init__.py:190-199, invites it): the pair saves the
+# pre-rotation q and k (inputs, no new storage), v, o and lse, plus the tables,
+# and rotates q and k again in the backward; saving the rotated q and k instead
+# would add B*(H + KVH)*S*D elements of new storage to skip one rotation pass.
+LLAMA3_ATTENTION = declare_op(
+    name="llama3_attention",
+    forward="oracle.forward_refs:llama3_attention_forward_ref",
+    runtime_forward="oracle.forward_refs:llama3_attention_runtime_ref",
+    dims=("B", "H", "KVH", "S", "D"),
+    args=(
+        Active("q", "[B, H, S, D]", note="queries before the rotation"),
+        Active("k", "[B, KVH, S, D]", note="keys before the rotation"),
+        Active("v", "[B, KVH, S, D]"),
+        Inactive("cos", "[S, D]", note="rotary cosine table, duplicated halves"),
+        Inactive("sin", "[S, D]", note="rotary sine table, same layout as cos"),
+    ),
+    output=Active("o", "[B, H, S, D]"),
+    forward_semantics=(
+        "q and k rotated (half-rotated RoPE in fp32, cast back to the input dtype), k "
+        "and v repeated over each group of H/KVH query heads, then o = softmax(q_r "
+        "k_r^T / sqrt(D) + causal mask) v."
+    ),
+    backward_semantics=(
+        "Return dq, dk, dv for the pre-rotation q and k (the rotation's transpose "
+        "applied to the attention gradients); dk and dv summed over each query group."
+    ),
+    reference_dtype="float32",
+    correctness=tuple(
+        Workload(dims=dict(B=b, H=h, KVH=kv, S=s, D=d), dtype=dt)
+        for b, h, kv, s, d in (
+            (1, 4, 1, 64, 128),
+            (2, 8, 2, 129, 128),
+            (1, 4, 2, 200, 64),
+            (1, 2, 2, 100, 128),
+            (1, 32, 8, 512, 128),
+        )
+        for dt in ("bfloat16", "float16")
+    ),
+    benchmark=(
+        Workload(dims=dict(B=4, H=32, KVH=8, S=4096, D=128), dtype="bfloat16",
+                 label="llama3_8b"),
+    ),
+    tolerances=TOLERANCES,
+    make_inputs="evograd_amd.inputs:make_llama3_attention_inputs",
+    memory_inputs=("q", "k", "v"),
+    regime_feature=_seq_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
+)
+
 # ------------------------------------------------------------ cross_entropy
 # src/evograd/ops/level1/cross_entropy/__init__.py:76-111. The gradient's entries
 # have magnitude about dloss / (rows * cols), so a flat atol would pass anything:
@@ -511,7 +564,7 @@ FUSED_LINEAR_CROSS_ENTROPY = declare_op(
 OPS: dict[str, OpDecl] = {
     op.name: op
     for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM,
-               CAUSAL_ATTENTION_GQA, CROSS_ENTROPY, FUSED_LINEAR_CROSS_ENTROPY)
+               CAUSAL_ATTENTION_GQA, LLAMA3_ATTENTION, CROSS_ENTROPY, FUSED_LINEAR_CROSS_ENTROPY)
 }
 
 

@@ -155,6 +155,26 @@ def make_attention_gqa_inputs(op, workload, device="cuda"):
     return {"q": q, "k": k, "v": v, "do": do}
 
 
+def make_llama3_attention_inputs(op, workload, device="cuda"):
+    """Generic seed (inputs.py:40-49); q [B, H, S, D], k, v [B, KVH, S, D], do
+    [B, H, S, D] ~ N(0,1) drawn in that order; cos/sin [S, D] fp32 tables at
+    Llama-3's theta (``extra`` may set theta and table_dtype), the decoder layer's
+    tables (src/evograd/ops/level3/llama3_decoder_layer/__init__.py:106-123)."""
+    d = workload.dims
+    qs = (d["B"], d["H"], d["S"], d["D"])
+    ks = (d["B"], d["KVH"], d["S"], d["D"])
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(case_seed(workload))
+    q = torch.randn(qs, device=device, dtype=dt)
+    k = torch.randn(ks, device=device, dtype=dt)
+    v = torch.randn(ks, device=device, dtype=dt)
+    do = torch.randn(qs, device=device, dtype=dt)
+    theta = float(workload.extra.get("theta", LLAMA3_ROPE_THETA))
+    tdt = resolve_dtype(workload.extra.get("table_dtype", "float32"))
+    cos, sin = rope_tables(d["S"], d["D"], theta, tdt, device)
+    return {"q": q, "k": k, "v": v, "cos": cos, "sin": sin, "do": do}
+
+
 def make_cross_entropy_inputs(op, workload, device="cuda"):
     """cross_entropy/__init__.py:48-56: seed rows*100003+cols; logits ~ N(0,1), target
     uniform in [0, cols) (int64), dloss = U[0,1) + 0.5 (0-dim, logits dtype), drawn in
@@ -200,6 +220,7 @@ RECIPES = {
     "make_rope_inputs": make_rope_inputs,
     "make_attention_inputs": make_attention_inputs,
     "make_attention_gqa_inputs": make_attention_gqa_inputs,
+    "make_llama3_attention_inputs": make_llama3_attention_inputs,
     "make_cross_entropy_inputs": make_cross_entropy_inputs,
     "make_flce_inputs": make_flce_inputs,
 }

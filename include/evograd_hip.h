@@ -216,6 +216,31 @@ int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* 
                     void* workspace, int64_t batch, int64_t heads, int64_t kv_heads,
                     int64_t seq, int64_t head_dim, float scale, int dtype, void* stream);
 
+/* ------------------------------------- RoPE(q, k) -> grouped causal attention
+ * Replaces the attention half of the Llama-3 decoder layer,
+ * src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:93-107:
+ *   q_r = rope(q), k_r = rope(k)   (rotate-half, fp32 tables, rounded to dtype)
+ *   o = causal attention of q_r against k_r, v repeated over each query group
+ * q, o, dout, dq [batch, heads, seq, head_dim]; k, v, dk, dv [batch, kv_heads,
+ * seq, head_dim]; cos, sin fp32 [seq, head_dim] (duplicated halves); lse fp32
+ * [batch, heads, seq] of the rotated scores. The backward takes the pre-rotation
+ * q, k and rotates them again: the saved state holds no rotated copy. dq and dk
+ * are the gradients of the pre-rotation q and k.
+ * Workspace: the backward's holds q_r, k_r (dtype), then delta fp32 [batch, heads,
+ * seq] (eg_llama3_attn_workspace_bytes); the forward's needs only batch * kv_heads
+ * * seq * head_dim elements of dtype (its rotated keys). */
+size_t eg_llama3_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                      int64_t seq, int64_t head_dim);
+int eg_llama3_attn_fwd(const void* q, const void* k, const void* v, const float* cos,
+                       const float* sin, void* o, float* lse, void* workspace, int64_t batch,
+                       int64_t heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
+                       float scale, int dtype, void* stream);
+int eg_llama3_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                       const void* o, const float* lse, const float* cos, const float* sin,
+                       void* dq, void* dk, void* dv, void* workspace, int64_t batch,
+                       int64_t heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
+                       float scale, int dtype, void* stream);
+
 /* ---------------------------------------------------------- cross entropy
  * Replaces cross_entropy_forward_ref
  * (src/evograd/ops/level1/cross_entropy/forward_ref.py:6-12):

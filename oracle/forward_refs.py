@@ -133,6 +133,22 @@ def causal_attention_gqa_runtime_ref(q, k, v):
     return F.scaled_dot_product_attention(q, k, v, is_causal=True)
 
 
+def llama3_attention_forward_ref(q, k, v, cos, sin):
+    """The attention half of src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:
+    93-107: q and k rotated by _apply_rope (:42-51, the half-rotated RoPE in fp32 cast
+    back to the input dtype, as rope_forward_ref), then each kv head repeated over its
+    query group and causal attention."""
+    return causal_attention_gqa_forward_ref(rope_forward_ref(q, cos, sin),
+                                            rope_forward_ref(k, cos, sin), v)
+
+
+def llama3_attention_runtime_ref(q, k, v, cos, sin):
+    """The layer's eager spelling of the same half: _apply_rope, repeat_interleave and
+    F.scaled_dot_product_attention(is_causal=True) (forward_ref.py:93-107)."""
+    return causal_attention_gqa_runtime_ref(rope_forward_ref(q, cos, sin),
+                                            rope_forward_ref(k, cos, sin), v)
+
+
 def causal_attention_lse_ref(q, k):
     """logsumexp over keys of the scaled, causally masked scores, fp32 [B, H, S]:
     the statistic the attention forward saves."""
@@ -172,6 +188,8 @@ FORWARDS = {
     "causal_attention_runtime_ref": causal_attention_runtime_ref,
     "causal_attention_gqa_forward_ref": causal_attention_gqa_forward_ref,
     "causal_attention_gqa_runtime_ref": causal_attention_gqa_runtime_ref,
+    "llama3_attention_forward_ref": llama3_attention_forward_ref,
+    "llama3_attention_runtime_ref": llama3_attention_runtime_ref,
     "cross_entropy_forward_ref": cross_entropy_forward_ref,
     "fused_linear_cross_entropy_forward_ref": fused_linear_cross_entropy_forward_ref,
 }

@@ -172,6 +172,13 @@ def main():
     save("fused_linear_cross_entropy", {"x": xf, "weight": wf, "target": tf}, ["x", "weight"],
          np.array(1.0), flce)
 
+    # RoPE on q and k (exact fp64 rotation), then grouped causal attention
+    cos, sin = rope_tables(5, 64, 10000.0)
+    la = {"q": draw(rng, (1, 4, 5, 64)), "k": draw(rng, (1, 2, 5, 64)),
+          "v": draw(rng, (1, 2, 5, 64)), "cos": cos, "sin": sin}
+    save("llama3_attention", la, ["q", "k", "v"], draw(rng, (1, 4, 5, 64)),
+         lambda q, k, v, cos, sin: causal_attention(rope(q, cos, sin), rope(k, cos, sin), v))
+
 
 if __name__ == "__main__":
     main()

@@ -9,7 +9,9 @@ from evograd_amd import decls
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "fused_add_rms_norm",
-       "causal_attention", "causal_attention_gqa", "cross_entropy", "fused_linear_cross_entropy")
+       "causal_attention", "causal_attention_gqa", "llama3_attention", "cross_entropy",
+       "fused_linear_cross_entropy")
+TABLE_ARGS = {"rope": ("cos", "sin"), "llama3_attention": ("cos", "sin")}
 
 
 def load(op_name: str) -> dict:
@@ -20,7 +22,7 @@ def load(op_name: str) -> dict:
 def case_inputs(op_name: str, dtype: torch.dtype, device: str) -> tuple:
     """(inputs keyed by declared names + upstream grad, expected output, expected
     gradients keyed by gradient name); float inputs in ``dtype``, integer ones as
-    int64, tables of RoPE kept fp32."""
+    int64, rotary tables kept fp32."""
     op = decls.get_op(op_name)
     g = load(op_name)
     inputs = {}
@@ -31,7 +33,7 @@ def case_inputs(op_name: str, dtype: torch.dtype, device: str) -> tuple:
             if a.dtype.kind in "iu":
                 inputs[arg.name] = torch.from_numpy(a).to(device)
             else:
-                dt = torch.float32 if op_name == "rope" and arg.name in ("cos", "sin") else dtype
+                dt = torch.float32 if arg.name in TABLE_ARGS.get(op_name, ()) else dtype
                 inputs[arg.name] = torch.from_numpy(a).to(device=device, dtype=dt)
         elif f"scalar_{arg.name}" in g:
             inputs[arg.name] = float(g[f"scalar_{arg.name}"])

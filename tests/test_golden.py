@@ -8,7 +8,7 @@ import torch
 
 from evograd_amd import decls
 from oracle.oracle import oracle
-from tests.golden_cases import OPS, assert_close, case_inputs
+from tests.golden_cases import OPS, TABLE_ARGS, assert_close, case_inputs
 
 torch.set_grad_enabled(True)
 
@@ -27,8 +27,7 @@ def test_golden_fixtures_are_bf16_exact_and_cover_edge_cases():
     for name in OPS:
         inputs, _, _ = case_inputs(name, torch.float64, "cpu")
         for k, v in inputs.items():
-            if torch.is_tensor(v) and v.is_floating_point() and not (
-                    name == "rope" and k in ("cos", "sin")):
+            if torch.is_tensor(v) and v.is_floating_point() and k not in TABLE_ARGS.get(name, ()):
                 assert torch.equal(v, v.bfloat16().double()), (name, k)
     # an ignored row in both losses
     assert -100 in case_inputs("cross_entropy", torch.float64, "cpu")[0]["target"].tolist()

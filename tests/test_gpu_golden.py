@@ -13,7 +13,7 @@ from tests.golden_cases import OPS, assert_close, case_inputs
 
 pytestmark = pytest.mark.gpu
 
-MFMA_ONLY = ("causal_attention", "causal_attention_gqa")
+MFMA_ONLY = ("causal_attention", "causal_attention_gqa", "llama3_attention")
 # (output/gradient rtol, atol as a fraction of the largest expected magnitude)
 BOUNDS = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 1e-2)}
 

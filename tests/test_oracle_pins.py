@@ -591,3 +591,78 @@ def test_runtime_forward_check_catches_a_planted_mistake(monkeypatch):
     op = replace(decls.RMSNORM, runtime_forward="oracle.forward_refs:no_eps")
     with pytest.raises(RuntimeError, match="differs"):
         check_runtime_forward(op)
+
+
+# ------------------------------------ RoPE(q, k) -> grouped attention (one pair)
+def _rope_brute(x, cos, sin):
+    """Pure-Python loops: pair (d, d + D/2) rotated by the table entries of its
+    position, first half x1 c - x2 s, second half x2 c + x1 s."""
+    B, H, S, D = x.shape
+    half = D // 2
+    y = torch.zeros_like(x)
+    for b in range(B):
+        for h in range(H):
+            for t in range(S):
+                for d in range(half):
+                    x1, x2 = float(x[b, h, t, d]), float(x[b, h, t, d + half])
+                    y[b, h, t, d] = x1 * float(cos[t, d]) - x2 * float(sin[t, d])
+                    y[b, h, t, d + half] = x2 * float(cos[t, d + half]) + x1 * float(sin[t, d + half])
+    return y
+
+
+def test_llama3_attention_forward_brute_force_and_reductions():
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(1, 4, 5, 8, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(1, 2, 5, 8, generator=g, dtype=torch.float64) for _ in range(2))
+    from evograd_amd.inputs import rope_tables
+
+    cos, sin = rope_tables(5, 8, 10000.0, torch.float64, "cpu")
+    out = fr.llama3_attention_forward_ref(q, k, v, cos, sin)
+    qr, kr = _rope_brute(q, cos, sin), _rope_brute(k, cos, sin)
+    for h in range(4):  # query head h attends with kv head h // 2
+        ref = _attn_brute(qr[:, h:h + 1], kr[:, h // 2:h // 2 + 1], v[:, h // 2:h // 2 + 1])[0]
+        # the rotation is evaluated in fp32 (x.float()), as the reference's is
+        assert torch.allclose(out[:, h:h + 1], ref, atol=1e-6)
+    # zero angles (cos 1, sin 0): plain grouped attention
+    ones, zeros = torch.ones(5, 8, dtype=torch.float64), torch.zeros(5, 8, dtype=torch.float64)
+    assert torch.allclose(fr.llama3_attention_forward_ref(q, k, v, ones, zeros),
+                          fr.causal_attention_gqa_forward_ref(q, k, v))
+    # the eager spelling (F.sdpa, in the inputs' fp64) agrees with the fp32 scores
+    assert torch.allclose(fr.llama3_attention_runtime_ref(q, k, v, cos, sin), out, atol=1e-5)
+
+
+def test_llama3_attention_depends_on_relative_positions_only():
+    """q_m . k_n after the rotation depends on m - n only: tables of positions shifted
+    by a constant give the same output (a rotation convention that is not a proper
+    rotation of each pair, or that rotates q and k differently, breaks this)."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, 2, 6, 8, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(1, 1, 6, 8, generator=g, dtype=torch.float64) for _ in range(2))
+    pos = torch.arange(6 + 37, dtype=torch.float64)[:, None]
+    inv = 100.0 ** (-torch.arange(0, 8, 2, dtype=torch.float64) / 8)
+    ang = torch.cat((pos * inv, pos * inv), dim=-1)
+    cos, sin = ang.cos(), ang.sin()
+    base = fr.llama3_attention_forward_ref(q, k, v, cos[:6], sin[:6])
+    shifted = fr.llama3_attention_forward_ref(q, k, v, cos[37:], sin[37:])
+    # equal up to the fp32 evaluation inside the restated forwards
+    assert torch.allclose(base, shifted, atol=1e-5)
+    assert not torch.allclose(base, fr.causal_attention_gqa_forward_ref(q, k, v), atol=1e-3)
+
+
+def test_llama3_attention_gradient_fd_and_chain_rule():
+    op = decls.LLAMA3_ATTENTION
+    w = Workload(dims=dict(B=1, H=4, KVH=2, S=6, D=8), dtype="float32", extra={"theta": 100.0})
+    inputs = _f64(make_case_inputs(op, w, "cpu"))
+    _fd_check(op, inputs)
+    # dq, dk are the rotation's transpose applied to the grouped attention's
+    # gradients of the rotated q, k; dv is that gradient unchanged
+    _, g = oracle(op, inputs, use_reference_dtype=False)
+    cos, sin = inputs["cos"], inputs["sin"]
+    rot = {"q": fr.rope_forward_ref(inputs["q"], cos, sin),
+           "k": fr.rope_forward_ref(inputs["k"], cos, sin), "v": inputs["v"], "do": inputs["do"]}
+    _, ga = oracle(decls.CAUSAL_ATTENTION_GQA, rot, use_reference_dtype=False)
+    for name, src in (("dq", "q"), ("dk", "k")):
+        _, gr = oracle(decls.ROPE, {"x": rot[src], "cos": cos, "sin": sin, "dy": ga[name]},
+                       use_reference_dtype=False)
+        assert torch.allclose(g[name], gr["dx"])
+    assert torch.allclose(g["dv"], ga["dv"])
