@@ -139,9 +139,16 @@ KERNELS = {
                          "bwd": ["rope_kernel", "attn_dq_kernel", "attn_dkdv_kernel"]},
     "cross_entropy":{"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
                       "bwd": ["xent_bwd_flat_kernel"]},
-    # first chunk's launches of the forward; the backward's dx scaling
-    "fused_linear_cross_entropy": {"fwd": ["xent_lse_kernel", "xent_bwd_flat_kernel"],
-                                   "bwd": ["scale_copy_kernel"]},
+    # eg_flce_fwd at 8192 rows of 128256 (two 4096-row chunks; the vocabulary needs no
+    # column padding): per chunk the logits product, the row logsumexp, the unit
+    # gradient and the dx product; then the dweight product over all rows and the
+    # mean. The backward's two dloss / n scalings.
+    "fused_linear_cross_entropy": {
+        "fwd": ["gemm_kernel(logits 0)", "xent_lse_kernel(0)", "xent_bwd_flat_kernel(0)",
+                "gemm_kernel(dx 0)", "gemm_kernel(logits 1)", "xent_lse_kernel(1)",
+                "xent_bwd_flat_kernel(1)", "gemm_kernel(dx 1)", "gemm_kernel(dweight)",
+                "xent_mean_kernel"],
+        "bwd": ["scale_copy_kernel(dx)", "scale_copy_kernel(dweight)"]},
     # bf16 rows of 128256: the forward's x and the backward's y held in registers
     # as raw packs, one kernel each
     "softmax@vocab": {"fwd": ["softmax_fwd_raw"], "bwd": ["softmax_bwd_raw"]},
@@ -154,7 +161,7 @@ DOMINANT = {
     "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
     "llama3_attention": ("bwd", 2),
     "cross_entropy": ("bwd", 0),
-    "fused_linear_cross_entropy": ("fwd", 1),
+    "fused_linear_cross_entropy": ("fwd", 8),
     "softmax@vocab": ("bwd", 0),
 }
 
@@ -164,12 +171,8 @@ def dominant_work(name: str, w, work: dict) -> float:
     d = w.dims
     es = {"float32": 4, "float16": 2, "bfloat16": 2}[w.dtype]
     if name == "fused_linear_cross_entropy":
-        # the unit-gradient kernel of one chunk: reads the chunk's fp32 logits,
-        # writes dlogits in the input dtype (the GEMMs are the library's)
-        from evograd_amd.pairs.fused_linear_cross_entropy import chunk_rows
-
-        rc = chunk_rows(d["rows"], d["vocab"])
-        return rc * d["vocab"] * (4 + es) + rc * 12
+        # the dweight product: dlogits.T @ x over every row
+        return 2.0 * d["rows"] * d["hidden"] * d["vocab"]
     if name == "rmsnorm":  # the column sum writes dweight
         return work["bwd"] - d["hidden"] * es
     if name == "fused_add_rms_norm":
@@ -301,7 +304,7 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     kname = KERNELS[name][phase][idx]
     k_us = kt[f"{phase}:{kname}"]
     k_work = dominant_work(base, w, work)
-    k_unit = "bytes" if base == "fused_linear_cross_entropy" else work["unit"]
+    k_unit = work["unit"]
     if k_unit == "bytes":
         k_rate = k_work / (k_us * 1e-6) / 1e9
         out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "bytes": k_work,

@@ -65,8 +65,10 @@ SIGNATURES: dict[str, tuple] = {
     "eg_cross_entropy_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p]),
     "eg_cross_entropy_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p]),
     "eg_cross_entropy_mean": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _p]),
-    "eg_flce_chunk": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p]),
+    "eg_flce_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i32]),
+    "eg_flce_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p]),
     "eg_scale_copy": (_i32, [_p, _i32, _p, _i32, _i64, _p, _i32, _p, _p]),
+    "eg_gemm": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p]),
 }
 
 _lib = None

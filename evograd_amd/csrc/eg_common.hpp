@@ -226,6 +226,14 @@ bool timed_launch(hipEvent_t* start, hipEvent_t* stop);
 // safe inside a captured graph). Returns 0 or an error code.
 int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
 
+// The MFMA product behind eg_gemm (gemm.hip): c[m][n] = sum_k a(m, k) b(k, n) with
+// fp32 accumulation. a_kc: a is [a_rows][lda] holding rows m, else rows k; b_kc:
+// b is [b_rows][ldb] holding rows n, else rows k; rows at or past a_rows / b_rows
+// read as zero. bf16/fp16 operands need k % 64 == 0 for a k-contiguous operand.
+int gemm_launch(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
+                int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name);
+
 // The RoPE launch behind eg_rope (rope.hip), for entry points that rotate as one
 // step of a longer launch sequence: arguments as eg_rope's, already validated.
 int rope_apply(const void* q, const void* k, void* q_out, void* k_out, const void* cos,

@@ -1,0 +1,476 @@
+// Dense products of the fused linear cross entropy on gfx950 MFMA.
+//
+// fused_linear_cross_entropy (src/evograd/ops/level2/fused_linear_cross_entropy/
+// forward_ref.py:23-35, gradients declared at fused_linear_cross_entropy/
+// __init__.py:91-152) needs three rows x hidden x vocab products:
+//   logits = x W^T     A = x [M][K],        B = W [N][K]      (both K-contiguous)
+//   dx     = dl W      A = dl [M][K],       B = W [K][N]      (B N-contiguous)
+//   dW     = dl^T x    A = dl^T: dl [K][M], B = x [K][N]      (both K-major)
+// One kernel template covers them: C[M][N] = sum_k A[m][k] B[k][n], fp32
+// accumulation, with each operand either K-contiguous (rows of the operand's
+// matrix run along k) or K-major (rows run along m or n).
+//
+// Block tile 256 x 256 x 64 for 4 waves (2 x 2, each wave 128 x 128: sixteen
+// 32 x 32 accumulator tiles, 256 fp32 registers per lane, held in AGPRs at one
+// wave per SIMD). Per 64-deep k step a workgroup stages a 256 x 64 slice of each
+// operand in LDS (32 KB each, double-buffered: 128 KB), filled by direct
+// buffer->LDS loads (16 bytes per lane, no VGPR staging) issued one step ahead.
+// Operands reach the MFMA v_mfma_f32_32x32x16_{bf16,f16} (lane l: row/column
+// l%32, k = 8(l/32) .. +7) as
+//   K-contiguous slice [256][64]: one ds_read_b128 per operand, 16-byte chunks
+//     XOR-swizzled by (row >> 1) & 7 so the 16 rows a read serves at a time fall
+//     in 16 distinct bank groups;
+//   K-major slice [64][256]: two ds_read_b64_tr_b16 per operand (lane gets 4
+//     consecutive k of one column each), chunks XOR-swizzled by 4 (k & 3) so the
+//     4 rows of one transposed read fall in 4 distinct 64-byte quarters.
+// Per k step a wave issues 64 MFMAs against 32 (K-contiguous) or 64 (K-major)
+// LDS reads.
+//
+// Bounds: rows of an operand past its end are outside the buffer resource's range
+// and read as zero, so M, N and a K-major operand's K may be ragged. A K-contiguous
+// operand must have K % 64 == 0 (its rows are padded by the caller) and every row
+// stride must be a multiple of 8 elements, with 16-byte aligned bases (checked by
+// the host). Workgroups walk the output tiles m-fastest within contiguous ranges
+// per XCD, so the workgroups in flight on one XCD share B panels in its L2.
+#include "eg_common.hpp"
+
+#include <type_traits>
+
+namespace eg {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+#define EG_LDS __attribute__((address_space(3)))
+
+template <typename T> struct GM;
+template <> struct GM<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct GM<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kBM = 256, kBN = 256, kBK = 64, kThreads = 256;
+constexpr int kSliceElems = 256 * 64;  // one operand slice: 32 KB of 16-bit values
+
+__device__ __forceinline__ int gwave() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+__device__ __forceinline__ int swz_kc(int row) { return (row >> 1) & 7; }   // 8 chunks/row
+__device__ __forceinline__ int swz_km(int krow) { return (krow & 3) << 2; }  // 32 chunks/row
+
+// Buffer resource over [base, base + bytes); reads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* base, int64_t bytes) {
+  const int64_t cap = 0x7fffffff;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0,
+                                           (int)(bytes < cap ? (bytes > 0 ? bytes : 0) : cap),
+                                           0x00020000);
+}
+
+// Loads one 256 x 64 operand slice into LDS. K-contiguous (KC): the slice is rows
+// r0 .. r0+255 of a [rows][ld] matrix, columns k0 .. k0+63. K-major: rows
+// k0 .. k0+63 of a [K][ld] matrix, columns c0 .. c0+255.
+template <bool KC>
+struct SliceLoader {
+  int voff[8];
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int w = gwave(), lane = threadIdx.x & 63;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int p = (it * 4 + w) * 64 + lane;  // LDS chunk (16 bytes) this lane fills
+      if (KC) {
+        const int r = p >> 3, c = (p & 7) ^ swz_kc(r);
+        voff[it] = (int)(((int64_t)r * ld + c * 8) * 2);
+      } else {
+        const int k = p >> 5, c = (p & 31) ^ swz_km(k);
+        voff[it] = (int)(((int64_t)k * ld + c * 8) * 2);
+      }
+    }
+  }
+  // `base` = first element of the slice; `bytes` = bytes from there to the end of
+  // the matrix.
+  __device__ __forceinline__ void load(const uint16_t* base, int64_t bytes,
+                                       uint16_t* lds) const {
+    const __amdgpu_buffer_rsrc_t rs = rsrc(base, bytes);
+    const int w = gwave();
+#pragma unroll
+    for (int it = 0; it < 8; ++it)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (EG_LDS void*)(lds + (it * 4 + w) * 512), 16,
+                                               voff[it], 0, 0, 0);
+  }
+};
+
+// Operands of the 32 x 32 x 16 MFMA from a slice: for block i (32 rows, or
+// columns, starting at w0 + 32 i) and substep s (k = 16 s .. +15), lane l takes row
+// w0 + 32 i + l%32, k 8(l/32) .. +7. The per-lane element offsets are computed once,
+// so each read is a register plus an immediate:
+//   K-contiguous: the swizzle depends on the lane and s only (32 i leaves
+//     (row >> 1) & 7 unchanged): off[s], block i adds 32 rows = 2048 elements;
+//   K-major: ds_read_b64_tr_b16 (within each 16-lane group, lane j addresses row
+//     base + j/4, columns 4(j%4) .. +3 of a 16-column group and receives column j of
+//     rows base .. base+3); two reads (rows +0..3, +4..7) give k in natural order.
+//     The swizzle depends on the lane only (k & 3 is the same for every s and for
+//     the +4 read): off[i], substep s adds 16 rows = 4096 elements.
+template <bool KC>
+struct OperandReader {
+  int off[4];
+  __device__ __forceinline__ void init(int w0, int lane) {
+    const int l32 = lane & 31, hh = lane >> 5;
+    if constexpr (KC) {
+      const int row = w0 + l32;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) off[s] = row * 64 + (((2 * s + hh) ^ swz_kc(row)) << 3);
+    } else {
+      const int m = lane & 15, gs = (lane >> 4) & 1;
+      const int k0 = 8 * hh + (m >> 2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = w0 + 32 * i + 16 * gs + 4 * (m & 3);
+        off[i] = k0 * 256 + (((col >> 3) ^ swz_km(k0)) << 3) + (col & 7);
+      }
+    }
+  }
+  template <typename V>
+  __device__ __forceinline__ V read(const uint16_t* lds, int i, int s) const {
+    if constexpr (KC) {
+      return *reinterpret_cast<const V*>(lds + off[s] + i * 2048);
+    } else {
+      const uint16_t* p = lds + off[i] + s * 4096;
+      const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EG_LDS i16x4*)p);
+      const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EG_LDS i16x4*)(p + 1024));
+      V r;
+      __builtin_memcpy(&r, &a, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&r) + 8, &b, 8);
+      return r;
+    }
+  }
+};
+
+template <typename TC> __device__ __forceinline__ void put(TC* p, float v);
+template <> __device__ __forceinline__ void put<float>(float* p, float v) { *p = v; }
+template <> __device__ __forceinline__ void put<bf16_t>(bf16_t* p, float v) { *p = from_f32<bf16_t>(v); }
+template <> __device__ __forceinline__ void put<f16_t>(f16_t* p, float v) { *p = from_f32<f16_t>(v); }
+
+// Output tile of workgroup i: XCD i % 8 takes a contiguous range of the tile
+// order. The order walks groups of kGroupM m-tiles: within a group, m fastest,
+// then n. The 32 workgroups in flight on one XCD then cover about 4 x 8 tiles
+// and share 4 A and 8 B slices per k step in that XCD's L2 (measured against
+// m-fastest over all m tiles, 16 x 2 in flight: logits 4.38 -> 3.96 ms at
+// 4096 x 128256 x 4096).
+constexpr int kGroupM = 4;
+__device__ __forceinline__ void tile_of(int tiles_m, int tiles, int& tm, int& tn) {
+  const int i = blockIdx.x;
+  const int per = (tiles + 7) / 8;
+  const int t = (i % 8) * per + i / 8;
+  if (t >= tiles) {
+    tn = -1;
+    return;
+  }
+  const int tiles_n = tiles / tiles_m;
+  const int g = t / (kGroupM * tiles_n);
+  const int gm = min(kGroupM, tiles_m - g * kGroupM);
+  const int r = t - g * kGroupM * tiles_n;
+  tm = g * kGroupM + r % gm;
+  tn = r / gm;
+}
+
+template <typename T, bool AKC, bool BKC, typename TC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                 TC* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+                 int64_t a_rows, int64_t b_rows, int tiles_m, int tiles) {
+  using v8 = typename GM<T>::v8;
+  // Two separate buffers per operand, selected at compile time in the unrolled k
+  // loop: the LDS reads of one buffer provably do not alias the loads in flight
+  // into the other, so they need not wait for them.
+  __shared__ __align__(16) uint16_t As0[kSliceElems], As1[kSliceElems];
+  __shared__ __align__(16) uint16_t Bs0[kSliceElems], Bs1[kSliceElems];
+  int tm, tn;
+  tile_of(tiles_m, tiles, tm, tn);
+  if (tn < 0) return;
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int lane = threadIdx.x & 63, w = gwave();
+  const int wm = (w >> 1) * 128, wn = (w & 1) * 128;
+
+  SliceLoader<AKC> la;
+  SliceLoader<BKC> lb;
+  la.init(lda);
+  lb.init(ldb);
+  // slice k of each operand: its first element and the bytes to the matrix end
+  const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
+  auto a_at = [&](int k0, int64_t& left) {
+    const int64_t off = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
+    left = (a_end - off) * 2;
+    return A + off;
+  };
+  auto b_at = [&](int k0, int64_t& left) {
+    const int64_t off = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
+    left = (b_end - off) * 2;
+    return B + off;
+  };
+  const int nk = (K + kBK - 1) / kBK;
+  // The k loop runs an even number of steps (two per iteration, one per buffer); the
+  // step past K, when nk is odd, loads through an empty range and adds zeros.
+  const int nk2 = nk + (nk & 1);
+  auto load = [&](int kt, uint16_t* as, uint16_t* bs) {
+    int64_t left;
+    const uint16_t* pa = a_at(kt * kBK, left);
+    la.load(pa, kt < nk ? left : 0, as);
+    const uint16_t* pb = b_at(kt * kBK, left);
+    lb.load(pb, kt < nk ? left : 0, bs);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  // One k step on the slices in (as, bs): the operands of substep s + 1 are read
+  // while the 16 MFMAs of substep s run.
+  OperandReader<AKC> ra;
+  OperandReader<BKC> rb;
+  ra.init(wm, lane);
+  rb.init(wn, lane);
+  // LDS read instructions per substep (a K-major operand takes two per block).
+  constexpr int NR = 4 * (AKC ? 1 : 2) + 4 * (BKC ? 1 : 2);
+  auto compute = [&](const uint16_t* as, const uint16_t* bs) {
+    v8 a[2][4], b[2][4];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[0][i] = ra.template read<v8>(as, i, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[0][j] = rb.template read<v8>(bs, j, 0);
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < kBK / 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[cur ^ 1][i] = ra.template read<v8>(as, i, s + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[cur ^ 1][j] = rb.template read<v8>(bs, j, s + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = GM<T>::mma(a[cur][i], b[cur][j], acc[i][j]);
+    }
+    // Schedule: the reads of substep 0, then each substep's 16 MFMAs with the NR
+    // reads of the next substep spread evenly among them.
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        // NR <= 16: at most one read after each MFMA
+        if (s + 1 < kBK / 16 && ((q + 1) * NR) / 16 != (q * NR) / 16)
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  load(0, As0, Bs0);
+  auto step = [&](auto bufc, int kt) {
+    constexpr bool odd = decltype(bufc)::value;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kt + 1 < nk2) load(kt + 1, odd ? As0 : As1, odd ? Bs0 : Bs1);
+    compute(odd ? As1 : As0, odd ? Bs1 : Bs0);
+  };
+  for (int kt = 0; kt < nk2; kt += 2) {
+    step(std::false_type{}, kt);
+    step(std::true_type{}, kt + 1);
+  }
+
+  // C tile (i, j): lane l holds column l%32, register r holds row 8(r/4) + 4(l/32) + r%4.
+  const int hh = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = n0 + wn + 32 * j + l32;
+    if (col >= N) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+        if (row < M) put<TC>(C + (int64_t)row * ldc + col, acc[i][j][r]);
+      }
+  }
+}
+
+// fp32 operands (no fp32 MFMA path is worth its registers here): a plain tiled
+// product, 64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread, 16-deep
+// k slices staged in LDS with every element bounds-checked. Used for fp32 inputs
+// of the fused linear cross entropy.
+template <bool AKC, bool BKC>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A,
+                                                       const float* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N, int K,
+                                                       int64_t lda, int64_t ldb, int64_t ldc,
+                                                       int64_t a_rows, int64_t b_rows) {
+  __shared__ float As[16][65], Bs[16][65];
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int e = threadIdx.x; e < 16 * 64; e += 256) {
+      const int kk = e / 64, mm = e % 64;
+      const int64_t k = k0 + kk, m = m0 + mm, n = n0 + mm;
+      float av = 0.f, bv = 0.f;
+      if (k < K && m < M) {
+        const int64_t r = AKC ? m : k;
+        if (r < a_rows) av = AKC ? A[m * lda + k] : A[k * lda + m];
+      }
+      if (k < K && n < N) {
+        const int64_t r = BKC ? n : k;
+        if (r < b_rows) bv = BKC ? B[n * ldb + k] : B[k * ldb + n];
+      }
+      As[kk][mm] = av;
+      Bs[kk][mm] = bv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += As[kk][ty * 4 + i] * Bs[kk][tx * 4 + j];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+      if (m < M && n < N) C[(int64_t)m * ldc + n] = acc[i][j];
+    }
+}
+
+}  // namespace
+
+// C[M][N] = A B in fp32 accumulation; see the file comment for the layouts.
+// a_kc: A is [a_rows][lda] holding rows m (else rows k); b_kc: B is [b_rows][ldb]
+// holding rows n (else rows k). Rows at or past a_rows / b_rows read as zero.
+int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
+                int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name) {
+  if (M <= 0 || N <= 0) return 0;
+  if (K <= 0) {
+    set_error("%s: K must be positive", name);
+    return 1;
+  }
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || a_rows < 0 || b_rows < 0) {
+    set_error("%s: size out of range", name);
+    return 1;
+  }
+  if (a_rows > (a_kc ? M : K) || b_rows > (b_kc ? N : K)) {
+    set_error("%s: an operand holds more rows than the product reads", name);
+    return 1;
+  }
+  if (dtype == EG_F32) {
+    if (c_dtype != EG_F32) {
+      set_error("%s: fp32 operands give an fp32 output", name);
+      return 1;
+    }
+    if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N) {
+      set_error("%s: a leading dimension is smaller than its row", name);
+      return 1;
+    }
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+    if (grid.y > 65535) {
+      set_error("%s: M too large for the fp32 path", name);
+      return 1;
+    }
+    auto go32 = [&](auto akc, auto bkc) {
+      EG_LAUNCH((gemm_f32_kernel<decltype(akc)::value, decltype(bkc)::value>), grid, dim3(256),
+                0, st, (const float*)A, (const float*)B, (float*)C, (int)M, (int)N, (int)K, lda,
+                ldb, ldc, a_rows, b_rows);
+      return check_launch(name);
+    };
+    using TT = std::true_type;
+    using FF = std::false_type;
+    if (a_kc && b_kc) return go32(TT{}, TT{});
+    if (a_kc) return go32(TT{}, FF{});
+    if (b_kc) return go32(FF{}, TT{});
+    return go32(FF{}, FF{});
+  }
+  if (dtype != EG_BF16 && dtype != EG_F16) {
+    set_error("%s: operands must be fp32, bf16 or fp16", name);
+    return 1;
+  }
+  if (c_dtype != EG_F32 && c_dtype != dtype) {
+    set_error("%s: output must be fp32 or the operand dtype", name);
+    return 1;
+  }
+  if (((a_kc || b_kc) && K % kBK) || lda % 8 || ldb % 8 || !aligned16(A) || !aligned16(B)) {
+    set_error("%s: K-contiguous operands need K %% 64 == 0; strides must be multiples of 8 "
+              "elements and bases 16-byte aligned", name);
+    return 1;
+  }
+  if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N) {
+    set_error("%s: a leading dimension is smaller than its row", name);
+    return 1;
+  }
+  // Per-lane byte offsets inside one slice are 32-bit: up to 255 rows (K-contiguous)
+  // or 63 rows (K-major) of the stride.
+  if ((a_kc ? 256 : 64) * lda * 2 >= ((int64_t)1 << 31) ||
+      (b_kc ? 256 : 64) * ldb * 2 >= ((int64_t)1 << 31)) {
+    set_error("%s: row stride too large", name);
+    return 1;
+  }
+  const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  const int64_t tiles = tiles_m * tiles_n;
+  if (tiles > 0x7fffffff / 2) {
+    set_error("%s: too many tiles", name);
+    return 1;
+  }
+  const unsigned grid = (unsigned)(((tiles + 7) / 8) * 8);
+  auto go = [&](auto tag, auto ctag, auto akc, auto bkc) {
+    using T = decltype(tag);
+    using TC = decltype(ctag);
+    EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>), dim3(grid),
+              dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
+              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles);
+    return check_launch(name);
+  };
+  auto layouts = [&](auto tag, auto ctag) {
+    using TT = std::true_type;
+    using FF = std::false_type;
+    if (a_kc && b_kc) return go(tag, ctag, TT{}, TT{});
+    if (a_kc) return go(tag, ctag, TT{}, FF{});
+    if (b_kc) return go(tag, ctag, FF{}, TT{});
+    return go(tag, ctag, FF{}, FF{});
+  };
+  if (dtype == EG_BF16)
+    return c_dtype == EG_F32 ? layouts(bf16_t{}, float{}) : layouts(bf16_t{}, bf16_t{});
+  return c_dtype == EG_F32 ? layouts(f16_t{}, float{}) : layouts(f16_t{}, f16_t{});
+}
+
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" int eg_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                       int64_t lda, int64_t ldb, int64_t ldc, int a_k_contiguous,
+                       int b_k_contiguous, int dtype, int c_dtype, void* stream) {
+  clear_error();
+  if (m < 0 || n < 0 || k < 0) {
+    set_error("eg_gemm: negative size");
+    return 1;
+  }
+  if (m > 0 && n > 0 && (!a || !b || !c)) {
+    set_error("eg_gemm: null pointer");
+    return 1;
+  }
+  const bool akc = a_k_contiguous != 0, bkc = b_k_contiguous != 0;
+  return gemm_launch(a, b, c, m, n, k, lda, ldb, ldc, akc, bkc, akc ? m : k, bkc ? n : k, dtype,
+                     c_dtype, as_stream(stream), "eg_gemm");
+}

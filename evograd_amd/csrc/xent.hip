@@ -26,8 +26,9 @@
 //   scale_copy_kernel dst = src * mul / div with a dtype conversion (the fused
 //                     linear cross entropy's dweight conversion and its dloss / n
 //                     scaling).
-// The fused linear cross entropy (eg_flce_chunk) runs xent_lse_kernel and the
-// backward kernels on a chunk's fp32 logits, the backward with unit scale.
+// The fused linear cross entropy (eg_flce_fwd) runs xent_lse_kernel and the
+// backward kernels on each chunk's fp32 logits, the backward with unit scale and
+// a padded output row stride.
 // No atomics: every sum has a fixed order, so results are bitwise repeatable.
 //
 // A target outside [0, cols) that is not ignore_index makes that row's loss and
@@ -159,7 +160,7 @@ template <typename TI, typename TO, typename TD, int VEC, bool NT>
 __global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
     const TD* __restrict__ dloss, const TI* __restrict__ x, const int64_t* __restrict__ target,
     const float* __restrict__ lse, const float* __restrict__ n_valid, TO* __restrict__ dx,
-    int64_t rows, int cols, int64_t ignore_index) {
+    int64_t rows, int cols, int64_t ldd, int64_t ignore_index) {
   const int64_t ppr = cols / VEC;  // packs per row
   const int64_t npack = rows * ppr;
   const int64_t first = (int64_t)blockIdx.x * kFlatPer;
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(kFlatBlock) void xent_bwd_flat_kernel(
       const int c = (int)((hi ? p - bound : p - row0 * ppr) * VEC);
       float o[VEC];
       grad_pack<VEC>(hi ? r1 : r0, c, v[u], o);
-      store_vec<TO, VEC, NT>(dx + p * VEC, o);
+      store_vec<TO, VEC, NT>(dx + (row0 + (hi ? 1 : 0)) * ldd + c, o);
     }
   }
 }
@@ -193,13 +194,13 @@ template <typename TI, typename TO, typename TD, int VEC, bool NT>
 __global__ __launch_bounds__(kBwdBlock) void xent_bwd_rows_kernel(
     const TD* __restrict__ dloss, const TI* __restrict__ x, const int64_t* __restrict__ target,
     const float* __restrict__ lse, const float* __restrict__ n_valid, TO* __restrict__ dx,
-    int cols, int64_t ignore_index) {
+    int cols, int64_t ldd, int64_t ignore_index) {
   constexpr int STEP = kBwdBlock * VEC;
   const int64_t row = blockIdx.x;
   const RowGrad rg = row_grad(dloss, target, lse, n_valid, row, cols, ignore_index);
   const int c0 = (int)blockIdx.y * (STEP * kUnroll) + (int)threadIdx.x * VEC;
   const TI* __restrict__ xr = x + row * cols;
-  TO* __restrict__ dr = dx + row * cols;
+  TO* __restrict__ dr = dx + row * ldd;
   float v[kUnroll][VEC];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -260,19 +261,22 @@ struct LseLaunch {
 };
 
 template <typename TI, typename TO, typename TD, int VEC>
+// dlogits rows are written with row stride ldd (>= cols, a multiple of VEC).
 void launch_bwd(const TD* gp, const TI* xp, const int64_t* target, const float* lse,
                 const float* n_valid, TO* dp, int64_t rows, int cols, int64_t ignore_index,
-                hipStream_t st) {
+                hipStream_t st, int64_t ldd = -1) {
   constexpr bool NT = VEC * sizeof(TI) == 16;
+  if (ldd < 0) ldd = cols;
   const int64_t ppr = cols / VEC;
   if (ppr >= kFlatPer) {
     const int64_t blocks = (rows * ppr + kFlatPer - 1) / kFlatPer;
     EG_LAUNCH((xent_bwd_flat_kernel<TI, TO, TD, VEC, NT>), dim3((unsigned)blocks),
-              dim3(kFlatBlock), 0, st, gp, xp, target, lse, n_valid, dp, rows, cols,
+              dim3(kFlatBlock), 0, st, gp, xp, target, lse, n_valid, dp, rows, cols, ldd,
               ignore_index);
   } else {
     EG_LAUNCH((xent_bwd_rows_kernel<TI, TO, TD, VEC, NT>), dim3((unsigned)rows, 1u),
-              dim3(kBwdBlock), 0, st, gp, xp, target, lse, n_valid, dp, cols, ignore_index);
+              dim3(kBwdBlock), 0, st, gp, xp, target, lse, n_valid, dp, cols, ldd,
+              ignore_index);
   }
 }
 
@@ -371,10 +375,18 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
 }
 
 // ------------------------------------------------ fused linear cross entropy
-// The chunked fused linear cross entropy of
-// src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152 runs, per row
-// chunk, the projection on the library GEMM and these two steps on the chunk's
-// fp32 logits; the mean and the final scaling use the entries below.
+// fused_linear_cross_entropy (src/evograd/ops/level2/fused_linear_cross_entropy/
+// forward_ref.py:23-35; gradients declared at fused_linear_cross_entropy/
+// __init__.py:91-152) in one launch sequence. The gradient is formed in the
+// forward (the backward only receives the scalar dloss): per row chunk,
+//   logits = x_c W^T (fp32, MFMA product, gemm.hip) -> lse and row losses
+//   (xent_lse_kernel) -> unit dlogits = softmax - onehot in the input dtype
+//   (xent_bwd_*_kernel), kept for all rows -> dx_c = dl_c W (MFMA);
+// then dW = dl^T x over all rows at once (MFMA, accumulated in registers over
+// every row, rounded once) and the mean loss. Chunks hold at most 2^29 logits
+// (2 GiB of fp32); the dlogits of all rows are kept so that dW is one product.
+// dlogits rows are padded to a multiple of 64 columns with zeros, the product's
+// k step. No atomics: bitwise repeatable.
 
 namespace eg {
 namespace {
@@ -389,40 +401,147 @@ int dispatch_type(int dtype, const char* what, F&& f) {
   }
 }
 
+// Zeroes columns [c0, c1) of every row of a [rows][ld] 16-bit matrix (the padding
+// of the dlogits rows).
+__global__ __launch_bounds__(256) void zero_cols_kernel(uint16_t* __restrict__ p, int64_t rows,
+                                                        int c0, int c1, int64_t ld) {
+  const int w = c1 - c0;
+  const int64_t n = rows * w;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[(i / w) * ld + c0 + i % w] = 0;
+}
+
+constexpr int64_t kFlceChunkElems = (int64_t)1 << 29;
+
+// Rows per chunk: as many as kFlceChunkElems logits allow, a power of two when
+// that splits the rows.
+int64_t flce_chunk_rows(int64_t rows, int64_t vocab) {
+  int64_t rc = kFlceChunkElems / (vocab > 0 ? vocab : 1);
+  if (rc < 1) rc = 1;
+  if (rc >= rows) return rows > 0 ? rows : 1;
+  int64_t p = 1;
+  while (p * 2 <= rc) p *= 2;
+  return p;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct FlceLayout {
+  int64_t rc, vp;
+  size_t stats, logits, dl, total;
+};
+
+FlceLayout flce_layout(int64_t rows, int64_t vocab, int64_t chunk_rows, int dtype) {
+  FlceLayout l;
+  l.rc = chunk_rows > 0 ? std::min(chunk_rows, rows > 0 ? rows : 1) : flce_chunk_rows(rows, vocab);
+  l.vp = dtype == EG_F32 ? vocab : (vocab + 63) / 64 * 64;
+  const size_t es = dtype == EG_F32 ? 4 : 2;
+  l.stats = align_up((size_t)rows * 2 * sizeof(float));
+  l.logits = align_up((size_t)l.rc * vocab * sizeof(float));
+  l.dl = align_up((size_t)rows * l.vp * es);
+  l.total = l.stats + l.logits + l.dl;
+  return l;
+}
+
 }  // namespace
 }  // namespace eg
 
-extern "C" int eg_flce_chunk(const float* logits, const int64_t* target, float* lse,
-                             float* rowloss, void* dlogits, int64_t rows, int64_t cols,
-                             int64_t ignore_index, int grad_dtype, void* stream) {
+extern "C" size_t eg_flce_workspace_bytes(int64_t rows, int64_t hidden, int64_t vocab,
+                                          int64_t chunk_rows, int dtype) {
+  (void)hidden;
+  if (rows <= 0 || vocab <= 0) return 0;
+  return flce_layout(rows, vocab, chunk_rows, dtype).total;
+}
+
+extern "C" int eg_flce_fwd(const void* x, const void* weight, const int64_t* target, float* loss,
+                           void* dx, void* dweight, float* n_valid, void* workspace,
+                           int64_t rows, int64_t hidden, int64_t vocab, int64_t ignore_index,
+                           int64_t chunk_rows, int dtype, void* stream) {
+  static const char* name = "eg_flce_fwd";
   clear_error();
-  if (check_xent("eg_flce_chunk", rows, cols)) return 1;
-  if (rows == 0) return 0;
-  if (!logits || !target || !lse || !rowloss || !dlogits) {
-    set_error("eg_flce_chunk: null pointer");
+  if (check_xent(name, rows, vocab)) return 1;
+  if (hidden <= 0 || hidden > ((int64_t)1 << 20)) {
+    set_error("%s: hidden=%lld out of range", name, (long long)hidden);
     return 1;
   }
-  if (rows * cols / kFlatPer >= ((int64_t)1 << 32) / kFlatBlock) {
-    set_error("eg_flce_chunk: rows*cols=%lld exceeds the launch grid", (long long)(rows * cols));
+  if (dtype != EG_F32 && dtype != EG_F16 && dtype != EG_BF16) {
+    set_error("%s: unsupported dtype %d", name, dtype);
+    return 1;
+  }
+  if (dtype != EG_F32 && hidden % 64) {
+    set_error("%s: 16-bit inputs need hidden %% 64 == 0 (pad x and weight with zero columns)",
+              name);
+    return 1;
+  }
+  if (!loss || !n_valid || !dweight || (rows > 0 && (!x || !weight || !target || !dx ||
+                                                     !workspace))) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(workspace)) {
+    set_error("%s: x, weight and workspace must be 16-byte aligned", name);
+    return 1;
+  }
+  const FlceLayout L = flce_layout(rows, vocab, chunk_rows, dtype);
+  if (L.rc * vocab / kFlatPer >= ((int64_t)1 << 32) / kFlatBlock) {
+    set_error("%s: vocab=%lld exceeds the launch grid", name, (long long)vocab);
     return 1;
   }
   hipStream_t st = as_stream(stream);
-  return dispatch_type(grad_dtype, "eg_flce_chunk", [&](auto tag) {
-    using TO = decltype(tag);
-    TO* dp = static_cast<TO*>(dlogits);
-    const float* none = nullptr;
-    if (cols % 4 == 0 && aligned16(logits)) {
-      pick_row_block(cols / 4, LseLaunch<float, 4>{logits, target, lse, rowloss, rows,
-                                                   (int)cols, ignore_index, st});
-      launch_bwd<float, TO, float, 4>(none, logits, target, lse, nullptr, dp, rows, (int)cols,
-                                      ignore_index, st);
-    } else {
-      pick_row_block(cols, LseLaunch<float, 1>{logits, target, lse, rowloss, rows, (int)cols,
-                                               ignore_index, st});
-      launch_bwd<float, TO, float, 1>(none, logits, target, lse, nullptr, dp, rows, (int)cols,
-                                      ignore_index, st);
+  const size_t es = dtype == EG_F32 ? 4 : 2;
+  if (rows == 0) {
+    // no rows: dweight is a sum over nothing; the mean loss is 0 / 0
+    if (int rc = zero_fill(dweight, (size_t)vocab * hidden * es, st, name)) return rc;
+    EG_LAUNCH((xent_mean_kernel<float>), dim3(1), dim3(kMeanBlock), 0, st, target, nullptr,
+              loss, n_valid, rows, ignore_index);
+    return check_launch(name);
+  }
+  char* ws = (char*)workspace;
+  float* lse = (float*)ws;
+  float* rowloss = lse + rows;
+  float* logits = (float*)(ws + L.stats);
+  char* dl = ws + L.stats + L.logits;
+  return dispatch_type(dtype, name, [&](auto tag) {
+    using T = decltype(tag);
+    T* dlp = (T*)dl;
+    if (L.vp > vocab) {
+      const int64_t n = rows * (L.vp - vocab);
+      const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+      EG_LAUNCH(zero_cols_kernel, dim3(grid), dim3(256), 0, st, (uint16_t*)dl, rows, (int)vocab,
+                (int)L.vp, L.vp);
     }
-    return check_launch("eg_flce_chunk");
+    for (int64_t r0 = 0; r0 < rows; r0 += L.rc) {
+      const int64_t n = std::min(L.rc, rows - r0);
+      const T* xc = (const T*)x + r0 * hidden;
+      if (int rc = gemm_launch(xc, weight, logits, n, vocab, hidden, hidden, hidden, vocab, true,
+                               true, n, vocab, dtype, EG_F32, st, name))
+        return rc;
+      const float* none = nullptr;
+      if (vocab % 4 == 0) {
+        pick_row_block(vocab / 4, LseLaunch<float, 4>{logits, target + r0, lse + r0,
+                                                      rowloss + r0, n, (int)vocab,
+                                                      ignore_index, st});
+        launch_bwd<float, T, float, 4>(none, logits, target + r0, lse + r0, nullptr,
+                                       dlp + r0 * L.vp, n, (int)vocab, ignore_index, st, L.vp);
+      } else {
+        pick_row_block(vocab, LseLaunch<float, 1>{logits, target + r0, lse + r0, rowloss + r0,
+                                                  n, (int)vocab, ignore_index, st});
+        launch_bwd<float, T, float, 1>(none, logits, target + r0, lse + r0, nullptr,
+                                       dlp + r0 * L.vp, n, (int)vocab, ignore_index, st, L.vp);
+      }
+      if (int rc = check_launch(name)) return rc;
+      if (int rc = gemm_launch(dlp + r0 * L.vp, weight, (T*)dx + r0 * hidden, n, hidden, L.vp,
+                               L.vp, hidden, hidden, true, false, n, vocab, dtype, dtype, st,
+                               name))
+        return rc;
+    }
+    if (int rc = gemm_launch(dlp, x, dweight, vocab, hidden, rows, L.vp, hidden, hidden, false,
+                             false, rows, rows, dtype, dtype, st, name))
+      return rc;
+    EG_LAUNCH((xent_mean_kernel<float>), dim3(1), dim3(kMeanBlock), 0, st, target, rowloss, loss,
+              n_valid, rows, ignore_index);
+    return check_launch(name);
   });
 }
 

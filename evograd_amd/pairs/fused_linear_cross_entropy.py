@@ -5,24 +5,22 @@ Replaces fused_linear_cross_entropy_forward_ref
 hard-label cross entropy of ``x @ weight.T`` against ``target``, ignore_index -100,
 projection and logsumexp accumulated in fp32) under the contract of
 fused_linear_cross_entropy/__init__.py:91-152: the ``[rows, vocab]`` logits are never
-materialised in full. The rows are processed in chunks; per chunk:
-
-1. ``logits = x_c @ weight.T`` on the library GEMM (bf16/fp16 operands, fp32
-   accumulation and fp32 output);
-2. ``eg_flce_chunk`` (HIP): per row logsumexp and loss, and the unit gradient
-   ``softmax - onehot`` in the input dtype;
-3. ``dx_c = dlogits @ weight`` and ``dweight += dlogits.T @ x_c`` on the library
-   GEMM, dweight accumulated in fp32 across chunks.
+materialised in full. One C entry point (``eg_flce_fwd``) runs the whole pass on
+this library's kernels: per row chunk the fp32 logits on the MFMA product
+(``gemm.hip``), their logsumexp, the row losses and the unit gradient
+``softmax - onehot`` in the input dtype, and ``dx_c = dlogits @ weight``; then
+``dweight = dlogits.T @ x`` over all rows in one product and the mean loss.
 
 The gradient is formed in the forward because the backward's only input is the
-scalar ``dloss``: the backward (``eg_scale_copy``, HIP) scales the saved unit
-gradients by ``dloss / n_valid``. The loss is fp32, as the reference's forward
-returns it. Saved state: ``(dx, dweight, n_valid)`` — the gradients in the inputs'
-dtypes and one fp32 count, nothing of size rows x vocab.
+scalar ``dloss``: the backward (``eg_scale_copy``) scales the saved unit gradients
+by ``dloss / n_valid``. The loss is fp32, as the reference's forward returns it.
+Saved state: ``(dx, dweight, n_valid)`` — the gradients in the inputs' dtypes and
+one fp32 count, nothing of size rows x vocab.
 
-Peak scratch is one chunk: ``rows_c x vocab`` fp32 logits plus the same in the input
-dtype for the gradient, with ``rows_c * vocab <= CHUNK_ELEMS``; and the fp32
-dweight accumulator (vocab x hidden).
+Scratch (freed when the forward returns): one chunk of fp32 logits, at most
+``CHUNK_ELEMS`` of them, and the unit gradient of every row in the input dtype.
+16-bit inputs whose hidden size is not a multiple of 64 (the product's k step) are
+copied into zero-padded buffers first.
 """
 
 from __future__ import annotations
@@ -40,19 +38,17 @@ if not __package__:
 import torch
 
 from evograd_amd import _lib
-from evograd_amd.pairs._util import as_contiguous, tag
+from evograd_amd.pairs._util import as_contiguous, tag, workspace
 
 IGNORE_INDEX = -100
-# Logits elements per chunk: 2^29 fp32 values = 2 GiB (4096 rows of Llama-3's
-# 128256-entry vocabulary). Measured at 8192 x 4096 x 128256: 2048-row chunks
-# 25.6 ms, 4096-row chunks 23.6 ms per forward (fewer fp32 dweight read-modify-
-# write passes), single chunk 22.9 ms (but the whole logits).
+# Logits per chunk: 2^29 fp32 values = 2 GiB (4096 rows of Llama-3's 128256-entry
+# vocabulary); the C side uses the same bound when chunk_rows is 0.
 CHUNK_ELEMS = 1 << 29
 
 
 def chunk_rows(rows: int, vocab: int) -> int:
     """Rows per chunk: as many as CHUNK_ELEMS allows, rounded down to a power of
-    two when that splits the rows (GEMM shapes of whole tiles)."""
+    two when that splits the rows."""
     rc = max(1, min(rows, CHUNK_ELEMS // max(vocab, 1)))
     if rc < rows:
         rc = 1 << (rc.bit_length() - 1)
@@ -74,10 +70,10 @@ def _check(x, weight, target):
     tag(x.dtype)
 
 
-def _logits(xc: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-    if xc.dtype == torch.float32:
-        return torch.mm(xc, weight.t())
-    return torch.mm(xc, weight.t(), out_dtype=torch.float32)
+def _pad_cols(t: torch.Tensor, cols: int) -> torch.Tensor:
+    out = torch.zeros((t.shape[0], cols), dtype=t.dtype, device=t.device)
+    out[:, :t.shape[1]] = t
+    return out
 
 
 def fused_linear_cross_entropy_forward_with_saved(x: torch.Tensor, weight: torch.Tensor,
@@ -88,44 +84,24 @@ def fused_linear_cross_entropy_forward_with_saved(x: torch.Tensor, weight: torch
     target = as_contiguous("target", target)
     rows, hidden = x.shape
     vocab = weight.shape[0]
-    dev, dt = x.device, x.dtype
-    stream = _lib.stream_of(x)
-    stats = torch.empty(2 * rows + 1, dtype=torch.float32, device=dev)  # lse | rowloss | n
-    lse, rowloss, n_valid = stats[:rows], stats[rows:2 * rows], stats[2 * rows:]
-    dx = torch.empty_like(x)
-    dw32 = torch.empty((vocab, hidden), dtype=torch.float32, device=dev)
+    dt = x.dtype
+    hp = hidden
+    if dt != torch.float32 and hidden % 64:
+        hp = (hidden + 63) // 64 * 64
+        x, weight = _pad_cols(x, hp), _pad_cols(weight, hp)
+    dx = torch.empty((rows, hp), dtype=dt, device=x.device)
+    dw = torch.empty((vocab, hp), dtype=dt, device=x.device)
+    out = torch.empty(2, dtype=torch.float32, device=x.device)  # loss | n_valid
     rc = chunk_rows(rows, vocab)
-    dl_buf = torch.empty((rc, vocab), dtype=dt, device=dev) if rows else None
-    for r0 in range(0, rows, rc):
-        r1 = min(rows, r0 + rc)
-        n = r1 - r0
-        xc = x[r0:r1]
-        logits = _logits(xc, weight)
-        dl = dl_buf[:n]
-        _lib.call("eg_flce_chunk", logits.data_ptr(), target[r0:].data_ptr(), lse[r0:].data_ptr(),
-                  rowloss[r0:].data_ptr(), dl.data_ptr(), n, vocab, IGNORE_INDEX, tag(dt), stream)
-        del logits
-        torch.mm(dl, weight, out=dx[r0:r1])
-        # the first chunk overwrites the accumulator (beta = 0 never reads it)
-        beta = 0.0 if r0 == 0 else 1.0
-        if dt == torch.float32:
-            torch.addmm(dw32, dl.t(), xc, beta=beta, out=dw32)
-        else:
-            torch.addmm(dw32, dl.t(), xc, beta=beta, out_dtype=torch.float32, out=dw32)
-    if rows == 0:
-        dw32.zero_()
-    loss = torch.empty((), dtype=torch.float32, device=dev)
-    _lib.call("eg_cross_entropy_mean", _lib.ptr(target), rowloss.data_ptr(), _lib.ptr(loss),
-              n_valid.data_ptr(), rows, IGNORE_INDEX, _lib.EG_F32, stream)
-    if dt == torch.float32:
-        dw = dw32
-    else:
-        dw = torch.empty_like(weight)
-        _lib.call("eg_scale_copy", dw32.data_ptr(), _lib.EG_F32, dw.data_ptr(), tag(dt),
-                  dw.numel(), None, _lib.EG_F32, None, stream)
-    del dw32
-    n_saved = n_valid.clone()
-    return loss, (dx, dw, n_saved)
+    ws = workspace(_lib.query("eg_flce_workspace_bytes", rows, hp, vocab, rc, tag(dt)), x.device)
+    _lib.call("eg_flce_fwd", _lib.ptr(x), _lib.ptr(weight), _lib.ptr(target), out.data_ptr(),
+              _lib.ptr(dx), _lib.ptr(dw), out[1:].data_ptr(), _lib.ptr(ws), rows, hp, vocab,
+              IGNORE_INDEX, rc, tag(dt), _lib.stream_of(x))
+    del ws
+    if hp != hidden:
+        dx, dw = dx[:, :hidden].contiguous(), dw[:, :hidden].contiguous()
+    loss = out[0].clone()
+    return loss, (dx, dw, out[1:].clone())
 
 
 def fused_linear_cross_entropy_backward_from_saved(dloss: torch.Tensor, saved):

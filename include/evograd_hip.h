@@ -269,7 +269,7 @@ int eg_cross_entropy_bwd(const void* dloss, const void* logits, const int64_t* t
 
 /* Mean of per-row losses: loss = sum(rowloss[r] over rows with target[r] !=
  * ignore_index) / n_valid, written in loss_dtype; n_valid (one fp32) is the count.
- * Ignored rows must hold rowloss 0 (as eg_flce_chunk writes them). The reduction
+ * Ignored rows must hold rowloss 0 (as eg_cross_entropy_fwd writes them). The reduction
  * of cross_entropy_forward_ref (src/evograd/ops/level1/cross_entropy/forward_ref.py:9-11)
  * over rows whose losses were produced chunk by chunk. */
 int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* loss,
@@ -277,18 +277,27 @@ int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* los
                           void* stream);
 
 /* --------------------------------------------- fused linear cross entropy
- * One row chunk of the fused linear cross entropy
- * (src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152; forward
- * fused_linear_cross_entropy/forward_ref.py:23-35). Given the chunk's fp32 logits
- * [rows, cols] (x_chunk @ weight.T, accumulated in fp32 by the caller's GEMM):
- *   lse[r] = logsumexp(logits[r]); rowloss[r] = lse[r] - logits[r, target[r]]
- *   dlogits = softmax(logits) - onehot(target)   (grad_dtype; unscaled)
- * Rows whose target is ignore_index get rowloss 0 and zero dlogits; a target
- * outside [0, cols) gives NaN. The caller then forms dx = dlogits @ weight and
- * dweight += dlogits.T @ x_chunk and scales both by dloss / n_valid. */
-int eg_flce_chunk(const float* logits, const int64_t* target, float* lse, float* rowloss,
-                  void* dlogits, int64_t rows, int64_t cols, int64_t ignore_index,
-                  int grad_dtype, void* stream);
+ * Replaces fused_linear_cross_entropy_forward_ref
+ * (src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35) and
+ * forms its gradient (declared at fused_linear_cross_entropy/__init__.py:91-152)
+ * in the same pass, every product on this library's MFMA kernels:
+ *   logits = x @ weight.T (fp32, in row chunks of at most 2^29 logits)
+ *   loss = mean over rows with target != ignore_index of lse - logits[target] (fp32)
+ *   dl = softmax(logits) - onehot(target) (dtype; zero on ignored rows)
+ *   dx = dl @ weight, dweight = dl.T @ x   (dtype: the unit gradients)
+ *   n_valid = the number of counted rows (fp32)
+ * x [rows, hidden], weight [vocab, hidden], dx, dweight as their inputs (dtype);
+ * target int64 [rows]; a target outside [0, vocab) that is not ignore_index
+ * gives NaN. 16-bit inputs need hidden % 64 == 0. The backward scales dx and
+ * dweight by dloss / n_valid (eg_scale_copy). chunk_rows <= 0 takes the default
+ * chunking; the workspace (eg_flce_workspace_bytes, same chunk_rows) holds the
+ * fp32 logits of one chunk and the dlogits of every row. */
+size_t eg_flce_workspace_bytes(int64_t rows, int64_t hidden, int64_t vocab, int64_t chunk_rows,
+                               int dtype);
+int eg_flce_fwd(const void* x, const void* weight, const int64_t* target, float* loss, void* dx,
+                void* dweight, float* n_valid, void* workspace, int64_t rows, int64_t hidden,
+                int64_t vocab, int64_t ignore_index, int64_t chunk_rows, int dtype,
+                void* stream);
 
 /* dst[i] = src[i] * mul[0] / div[0] for n elements, with conversion from src_dtype
  * to dst_dtype; mul (of mul_dtype) and div (fp32) are device scalars and either
@@ -297,6 +306,21 @@ int eg_flce_chunk(const float* logits, const int64_t* target, float* lse, float*
  * src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:116-123). */
 int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
                   const void* mul, int mul_dtype, const float* div, void* stream);
+
+/* ------------------------------------------------------------ dense product
+ * The products inside fused_linear_cross_entropy (the logits x @ weight.T of
+ * src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35 and the
+ * dx = dlogits @ weight, dweight = dlogits.T @ x of its gradient), on MFMA:
+ *   c[m][n] = sum_k a(m, k) b(k, n)   (fp32 accumulation; bf16/fp16 operands on
+ *                                      MFMA, fp32 operands on a plain tiled path)
+ * a_k_contiguous: a(m, k) = a[m * lda + k], else a[k * lda + m];
+ * b_k_contiguous: b(k, n) = b[n * ldb + k], else b[k * ldb + n];
+ * c [m][ldc] in c_dtype (EG_F32 or dtype). A k-contiguous operand needs k % 64 == 0
+ * (pad its rows with zeros); strides are multiples of 8 elements and a, b are
+ * 16-byte aligned. */
+int eg_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+            int64_t lda, int64_t ldb, int64_t ldc, int a_k_contiguous, int b_k_contiguous,
+            int dtype, int c_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,106 @@
+"""The MFMA product behind the fused linear cross entropy (eg_gemm) against a torch
+fp32 reference: every operand layout (k-contiguous or k-major A and B), ragged M,
+N and k-major K, padded strides, fp32 / bf16 / fp16 outputs, and the fp32 path.
+Bound: the fp32 result within fp32 accumulation rounding of the exact product of
+the (exactly representable) 16-bit inputs; a 16-bit result within one rounding."""
+
+import sys
+
+import pytest
+import torch
+
+from evograd_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = [(True, True), (True, False), (False, False), (False, True)]
+SHAPES = [(256, 256, 64), (300, 200, 128), (8, 512, 64), (1000, 777, 320), (260, 300, 100),
+          (513, 1031, 192)]
+
+
+def _r8(v):
+    return (v + 7) // 8 * 8
+
+
+def _operands(M, N, K, akc, bkc, dtype, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    A = torch.randn(M, K, device="cuda", generator=g).to(dtype)
+    B = torch.randn(K, N, device="cuda", generator=g).to(dtype)
+    if akc:
+        lda = _r8(K)
+        a = torch.zeros(M, lda, device="cuda", dtype=dtype)
+        a[:, :K] = A
+    else:
+        lda = _r8(M)
+        a = torch.zeros(K, lda, device="cuda", dtype=dtype)
+        a[:, :M] = A.t()
+    if bkc:
+        ldb = _r8(K)
+        b = torch.zeros(N, ldb, device="cuda", dtype=dtype)
+        b[:, :K] = B.t()
+    else:
+        ldb = _r8(N)
+        b = torch.zeros(K, ldb, device="cuda", dtype=dtype)
+        b[:, :N] = B
+    return A, B, a, b, lda, ldb
+
+
+def _run(a, b, M, N, K, lda, ldb, akc, bkc, dtype, cdt):
+    ldc = N + 3 if cdt == torch.float32 else _r8(N)
+    c = torch.full((M, ldc), float("nan"), device="cuda", dtype=cdt)
+    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, lda, ldb, ldc,
+              int(akc), int(bkc), _lib.dtype_tag(dtype), _lib.dtype_tag(cdt),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return c
+
+
+def _cases():
+    for M, N, K in SHAPES:
+        for akc, bkc in LAYOUTS:
+            if (akc or bkc) and K % 64:
+                continue
+            yield pytest.param(M, N, K, akc, bkc, id=f"{M}x{N}x{K}-a{'k' if akc else 'm'}-b{'k' if bkc else 'n'}")
+
+
+@pytest.mark.parametrize("M,N,K,akc,bkc", list(_cases()))
+def test_gemm_bf16_fp32_out(M, N, K, akc, bkc):
+    print(f"\n[gpu-gemm] bf16 {M}x{N}x{K} akc={akc} bkc={bkc}", flush=True)
+    sys.stdout.flush()
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, torch.bfloat16, M + 7 * N + K)
+    c = _run(a, b, M, N, K, lda, ldb, akc, bkc, torch.bfloat16, torch.float32)
+    ref = A.double() @ B.double()
+    err = (c[:, :N].double() - ref).abs().max().item()
+    # fp32 accumulation of K products of magnitude ~1: a few ulps of sqrt(K)
+    assert err <= 4e-6 * K, err
+    assert torch.isnan(c[:, N:]).all()  # columns past N untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("akc,bkc", LAYOUTS)
+def test_gemm_16bit_out_is_one_rounding(dtype, akc, bkc):
+    M, N, K = 384, 320, 256
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, dtype, 11)
+    c = _run(a, b, M, N, K, lda, ldb, akc, bkc, dtype, dtype)
+    ref = (A.double() @ B.double())
+    rel = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    err = (c[:, :N].double() - ref).abs()
+    assert (err <= rel * ref.abs() + 1e-5 * K).all(), err.max().item()
+
+
+def test_gemm_fp32_path_and_zero_rows_past_the_operand():
+    M, N, K = 130, 70, 45
+    A, B, a, b, lda, ldb = _operands(M, N, K, False, False, torch.float32, 5)
+    c = _run(a, b, M, N, K, lda, ldb, False, False, torch.float32, torch.float32)
+    assert torch.allclose(c[:, :N].double(), A.double() @ B.double(), atol=1e-4, rtol=1e-5)
+    A, B, a, b, lda, ldb = _operands(M, N, K, True, True, torch.float32, 6)
+    c = _run(a, b, M, N, K, lda, ldb, True, True, torch.float32, torch.float32)
+    assert torch.allclose(c[:, :N].double(), A.double() @ B.double(), atol=1e-4, rtol=1e-5)
+
+
+def test_gemm_refuses_unsupported_shapes_on_the_host():
+    x = torch.zeros(64, 64, device="cuda", dtype=torch.bfloat16)
+    c = torch.zeros(64, 64, device="cuda")
+    with pytest.raises(RuntimeError, match="K % 64"):
+        _lib.call("eg_gemm", x.data_ptr(), x.data_ptr(), c.data_ptr(), 64, 64, 40, 64, 64, 64,
+                  1, 1, _lib.EG_BF16, _lib.EG_F32, torch.cuda.current_stream().cuda_stream)
