@@ -312,8 +312,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
-  __shared__ __align__(16) uint16_t Ks[2][BN * D];
-  __shared__ __align__(16) uint16_t Vs[2][BN * D];
+  // One __shared__ object per buffer (see the file comment): LDS reads of one
+  // buffer never wait for the loads in flight into the other.
+  __shared__ __align__(16) uint16_t Ks0[BN * D], Ks1[BN * D];
+  __shared__ __align__(16) uint16_t Vs0[BN * D], Vs1[BN * D];
 
   int vh, blk;
   block_coords(BH, vh, blk);
@@ -360,13 +362,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
   const int ntiles = (kv_end + BN - 1) / BN;
   const int wave_first_row = q0 + 32 * w;
 
-  zero_lds<NW * 64>(Ks, sizeof(Ks));
-  zero_lds<NW * 64>(Vs, sizeof(Vs));
+  zero_lds<NW * 64>(Ks0, sizeof(Ks0));
+  zero_lds<NW * 64>(Ks1, sizeof(Ks1));
+  zero_lds<NW * 64>(Vs0, sizeof(Vs0));
+  zero_lds<NW * 64>(Vs1, sizeof(Vs1));
   __syncthreads();
   TileLoader<BN, D, NW> ld;
   ld.init();
-  ld.load(kp, 0, S, Ks[0]);
-  ld.load(vp, 0, S, Vs[0]);
+  ld.load(kp, 0, S, Ks0);
+  ld.load(vp, 0, S, Vs0);
   // The rotation waits for q and the tables, so it comes after the first tile's
   // loads are issued: those are in flight meanwhile.
   if constexpr (ROPE)
@@ -376,13 +380,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     wait_loads();
     __syncthreads();
     if (j + 1 < ntiles) {
-      ld.load(kp, (j + 1) * BN, S, Ks[buf ^ 1]);
-      ld.load(vp, (j + 1) * BN, S, Vs[buf ^ 1]);
+      ld.load(kp, (j + 1) * BN, S, buf ? Ks0 : Ks1);
+      ld.load(vp, (j + 1) * BN, S, buf ? Vs0 : Vs1);
     }
     const int k0 = j * BN;
     if (k0 > wave_first_row + 31) return;  // every key of the tile is above this wave's rows
-    const uint16_t* Kb = Ks[buf];
-    const uint16_t* Vb = Vs[buf];
+    const uint16_t* Kb = buf ? Ks1 : Ks0;
+    const uint16_t* Vb = buf ? Vs1 : Vs0;
     f32x16 s[2] = {f32x16{}, f32x16{}};
     // S^T = K Q^T with the K operand reads kFwdPrefetch MFMAs ahead of their use
     // (MFMA i takes (kk, T2) = (i / 2, i % 2)); the scheduling groups keep that
@@ -490,9 +494,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
   using v8 = typename MM<T>::v8;
   constexpr int BK = 32 * NW;
-  constexpr int KSTEPS = D / 16, DT = D / 32, MT = BQ / 32;
-  __shared__ __align__(16) uint16_t Qs[2][BQ * D];
-  __shared__ __align__(16) uint16_t Ds[2][BQ * D];
+  constexpr int KSTEPS = D / 16, DT = D / 32;
+  static_assert(BQ == 32, "one 32-row Q / dO tile per step");
+  __shared__ __align__(16) uint16_t Qs0[BQ * D], Qs1[BQ * D];  // one object per buffer
+  __shared__ __align__(16) uint16_t Ds0[BQ * D], Ds1[BQ * D];
   // V of the workgroup's keys: the B operand of dP = dO V^T, read from LDS so
   // that its 64 registers per wave stay free for operand staging.
   __shared__ __align__(16) uint16_t Vk[BK * D];
@@ -517,8 +522,25 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
 #pragma unroll
   for (int t = 0; t < DT; ++t) { dka[t] = f32x16{}; dva[t] = f32x16{}; }
 
-  zero_lds<NW * 64>(Qs, sizeof(Qs));
-  zero_lds<NW * 64>(Ds, sizeof(Ds));
+  // Operand read offsets as one register per read family. The fields of toff() are
+  // disjoint bit ranges (row * D, chunk ^ swizzle in bits 3-6, the 4-column
+  // sub-offset in bit 2), and the swizzle depends on the row's low 4 bits only, so
+  //   rows as A operand, row l32 (+32 for this wave's V rows), chunk 2kk + hh:  R0 ^ 16kk
+  //   transposed reads, column block t, rows r0 / r0 + 8 (+16 per ms step):    T0[j] ^ 32t
+  const int R0 = toff<D>(l32, hh);
+  int T0[2];
+  {
+    const int mq = lane & 15, gs = (lane >> 4) & 1, r0 = 4 * hh + (mq >> 2);
+    const int col = 16 * gs + 4 * (mq & 3);
+    T0[0] = toff<D>(r0, col >> 3) + (col & 7);
+    T0[1] = toff<D>(r0 + 8, col >> 3) + (col & 7);
+  }
+  const uint16_t* Vw = Vk + 32 * w * D;  // this wave's 32 keys
+
+  zero_lds<NW * 64>(Qs0, sizeof(Qs0));
+  zero_lds<NW * 64>(Qs1, sizeof(Qs1));
+  zero_lds<NW * 64>(Ds0, sizeof(Ds0));
+  zero_lds<NW * 64>(Ds1, sizeof(Ds1));
   zero_lds<NW * 64>(Vk, sizeof(Vk));
   // The walk: for each query head of the group (in order), the q tiles from the
   // diagonal block to S. dK and dV accumulate over all of them in registers, so
@@ -531,23 +553,26 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   ld.init();
   auto qhead = [&](int step) { return kvh * group + step / ntq; };
   auto qtile = [&](int step) { return i_first + step % ntq; };
-  // lse (as log2) and delta of a tile's rows: wave 0 loads them into registers
-  // when the tile is requested and stores them to LDS after its own compute.
-  float lreg = INFINITY, ereg = 0.f;
+  // lse and delta of a tile's rows: wave 0 loads them when the tile is requested
+  // and converts and stores them to LDS only after the current step's compute, so
+  // that waiting for them does not hold that compute behind the tile loads.
+  float lraw = 0.f, eraw = 0.f;
+  bool lrow = false;
   auto load_stats = [&](int step) {
     if (w == 0 && lane < BQ) {
       const int64_t hb = (int64_t)qhead(step) * S;
       const int row = qtile(step) * BQ + lane;
       const int rc = row < S ? row : S - 1;
-      const float lv = lse[hb + rc], ev = delta[hb + rc];
-      lreg = row < S ? lv * kLog2e : INFINITY;
-      ereg = row < S ? ev : 0.f;
+      lraw = lse[hb + rc];
+      eraw = delta[hb + rc];
+      lrow = row < S;
     }
   };
-  auto load_tiles = [&](int step, int buf) {
-    const int64_t hb = (int64_t)qhead(step) * S * D;
-    ld.load(q + hb, qtile(step) * BQ, S, Qs[buf]);
-    ld.load(dout + hb, qtile(step) * BQ, S, Ds[buf]);
+  auto store_stats = [&](float* ls, float* es) {
+    if (w == 0 && lane < BQ) {
+      ls[lane] = lrow ? lraw * kLog2e : INFINITY;  // rows past S: p = 0
+      es[lane] = lrow ? eraw : 0.f;
+    }
   };
   __syncthreads();
   {
@@ -556,56 +581,86 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     lv.load(v + base, k0, S, Vk);
   }
   if (nsteps > 0) {
-    load_tiles(0, 0);
+    const int64_t hb = (int64_t)qhead(0) * S * D;
+    ld.load(q + hb, qtile(0) * BQ, S, Qs0);
+    ld.load(dout + hb, qtile(0) * BQ, S, Ds0);
     load_stats(0);
-    if (w == 0 && lane < BQ) { Ls[0][lane] = lreg; Es[0][lane] = ereg; }
+    store_stats(Ls[0], Es[0]);
   }
-  for (int step = 0; step < nsteps; ++step) {
+  auto step_fn = [&](auto bufc, int step) {
+    constexpr int buf = decltype(bufc)::value;
     wait_loads();
     __syncthreads();
-    const int buf = step & 1;
     const bool more = step + 1 < nsteps;
     if (more) {
-      load_tiles(step + 1, buf ^ 1);
+      const int64_t hb = (int64_t)qhead(step + 1) * S * D;
+      ld.load(q + hb, qtile(step + 1) * BQ, S, buf ? Qs0 : Qs1);
+      ld.load(dout + hb, qtile(step + 1) * BQ, S, buf ? Ds0 : Ds1);
       load_stats(step + 1);
     }
     const int qi0 = qtile(step) * BQ;
     if (qi0 + BQ - 1 >= wave_first_key) {  // some row of the tile sees some key of this wave
-      const uint16_t* Qb = Qs[buf];
-      const uint16_t* Db = Ds[buf];
-      f32x16 s[MT], dp[MT];
+      const uint16_t* Qb = buf ? Qs1 : Qs0;
+      const uint16_t* Db = buf ? Ds1 : Ds0;
+      // Opaque copies of the offset registers: the XORs are redone in each step
+      // instead of being hoisted out of the loop into 24 live registers.
+      int r0 = R0, t0 = T0[0], t1 = T0[1];
+      asm volatile("" : "+v"(r0), "+v"(t0), "+v"(t1));
+      auto offR = [&](int kk) { return r0 ^ (16 * kk); };
+      auto offT = [&](int t, int j) { return (j ? t1 : t0) ^ (32 * t); };
+      // S = Q K^T and dP = dO V^T, the three operand reads of step kk + 1 issued
+      // before the two MFMAs of step kk (scheduling groups keep that order).
+      f32x16 s = f32x16{}, dp = f32x16{};
+      {
+        v8 qa[2], da[2], vb[2];
+        __builtin_amdgcn_sched_barrier(0);
+        qa[0] = *reinterpret_cast<const v8*>(Qb + offR(0));
+        da[0] = *reinterpret_cast<const v8*>(Db + offR(0));
+        vb[0] = *reinterpret_cast<const v8*>(Vw + offR(0));
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) { s[mt] = f32x16{}; dp[mt] = f32x16{}; }
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          s[mt] = MM<T>::mma(rd_rows<v8, D>(Qb, 32 * mt + l32, kk, hh), kf[kk], s[mt]);
-          dp[mt] = MM<T>::mma(rd_rows<v8, D>(Db, 32 * mt + l32, kk, hh),
-                              rd_rows<v8, D>(Vk, 32 * w + l32, kk, hh), dp[mt]);
-        }
-      // Causal mask: row qi0 + 32mt + 8g + 4hh + i4 sees this lane's key iff
-      // 32mt + 8g + i4 >= key - qi0 - 4hh (never true off the diagonal tiles, where
-      // that bound is <= 0). Rows past S have lse = +inf, so their p is 0 already.
-      const int mask_below = key - qi0 - 4 * hh;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int rr = 32 * mt + 8 * g + 4 * hh;  // first row of this 4-row group
-          const float4 l4 = *reinterpret_cast<const float4*>(&Ls[buf][rr]);
-          const float4 e4 = *reinterpret_cast<const float4*>(&Es[buf][rr]);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-          const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) {
-            const int r = 4 * g + i4;
-            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][r], scale_log2, -lv[i4]));
-            if (32 * mt + 8 * g + i4 < mask_below) p = 0.f;
-            s[mt][r] = p;
-            dp[mt][r] = p * (dp[mt][r] - ev[i4]);
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          if (kk + 1 < KSTEPS) {
+            qa[(kk + 1) & 1] = *reinterpret_cast<const v8*>(Qb + offR(kk + 1));
+            da[(kk + 1) & 1] = *reinterpret_cast<const v8*>(Db + offR(kk + 1));
+            vb[(kk + 1) & 1] = *reinterpret_cast<const v8*>(Vw + offR(kk + 1));
           }
+          s = MM<T>::mma(qa[kk & 1], kf[kk], s);
+          dp = MM<T>::mma(da[kk & 1], vb[kk & 1], dp);
         }
+        __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          if (kk + 1 < KSTEPS) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // P = exp(S * scale - lse); register r holds row 8(r/4) + 4hh + r%4.
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 l4 = *reinterpret_cast<const float4*>(&Ls[buf][8 * g + 4 * hh]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          s[4 * g + i4] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * g + i4], scale_log2, -lv[i4]));
+      }
+      // Causal mask, in the diagonal steps only (a wave-uniform branch): row
+      // qi0 + 8g + 4hh + i4 sees this lane's key iff 8g + i4 >= key - qi0 - 4hh.
+      if (qi0 < wave_first_key + 31) {
+        const int mask_below = key - qi0 - 4 * hh;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (8 * (r >> 2) + (r & 3) < mask_below) s[r] = 0.f;
+      }
+      // dS = P (dP - delta)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 e4 = *reinterpret_cast<const float4*>(&Es[buf][8 * g + 4 * hh]);
+        const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          dp[4 * g + i4] = s[4 * g + i4] * (dp[4 * g + i4] - ev[i4]);
+      }
       // dV^T += dO^T P and dK^T += Q^T dS in the order (ms, t, dV then dK), each
       // MFMA's transposed operand read one MFMA ahead (two ds_read_b64_tr_b16); the
       // scheduling groups keep that order, which the default schedule collapses to
@@ -613,7 +668,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
       constexpr int NM = 2 * DT * (BQ / 16);
       auto rd = [&](int i) {
         const int ms = i / (2 * DT), t = (i / 2) % DT;
-        return rd_tr<v8, D>((i & 1) ? Qb : Db, 16 * ms, 32 * t, lane);
+        const uint16_t* tb = (i & 1) ? Qb : Db;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (EG_LDS i16x4*)(tb + offT(t, 0) + 16 * D * ms));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (EG_LDS i16x4*)(tb + offT(t, 1) + 16 * D * ms));
+        v8 r;
+        __builtin_memcpy(&r, &lo, 8);
+        __builtin_memcpy(reinterpret_cast<char*>(&r) + 8, &hi, 8);
+        return r;
       };
       v8 op[2], pb, sb;
       __builtin_amdgcn_sched_barrier(0);
@@ -623,8 +686,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
         if (i + 1 < NM) op[(i + 1) & 1] = rd(i + 1);
         const int ms = i / (2 * DT), t = (i / 2) % DT;
         if (i % (2 * DT) == 0) {
-          pb = pack8<T>(s[ms >> 1], 8 * (ms & 1));
-          sb = pack8<T>(dp[ms >> 1], 8 * (ms & 1));
+          pb = pack8<T>(s, 8 * ms);
+          sb = pack8<T>(dp, 8 * ms);
         }
         if (i & 1) dka[t] = MM<T>::mma(op[i & 1], sb, dka[t]);
         else dva[t] = MM<T>::mma(op[i & 1], pb, dva[t]);
@@ -637,7 +700,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (more && w == 0 && lane < BQ) { Ls[buf ^ 1][lane] = lreg; Es[buf ^ 1][lane] = ereg; }
+    if (more) store_stats(Ls[buf ^ 1], Es[buf ^ 1]);
+  };
+  // Unrolled over the two buffers, so every LDS address is a register plus an
+  // immediate and the buffers are distinct objects at compile time.
+  for (int step = 0; step < nsteps; step += 2) {
+    step_fn(std::integral_constant<int, 0>{}, step);
+    if (step + 1 < nsteps) step_fn(std::integral_constant<int, 1>{}, step + 1);
   }
 
   if (key < S) {
@@ -669,8 +738,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
   using v8 = typename MM<T>::v8;
   constexpr int BM = 32 * NW, BN = 64;
   constexpr int KSTEPS = D / 16, DT = D / 32;
-  __shared__ __align__(16) uint16_t Ks[2][BN * D];
-  __shared__ __align__(16) uint16_t Vs[2][BN * D];
+  __shared__ __align__(16) uint16_t Ks0[BN * D], Ks1[BN * D];  // one object per buffer
+  __shared__ __align__(16) uint16_t Vs0[BN * D], Vs1[BN * D];
 
   int vh, blk;
   block_coords(BH, vh, blk);
@@ -734,25 +803,27 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
       offV[t][1] = toff<D>(r0 + 8, col >> 3) + (col & 7);
     }
   }
-  zero_lds<NW * 64>(Ks, sizeof(Ks));
-  zero_lds<NW * 64>(Vs, sizeof(Vs));
+  zero_lds<NW * 64>(Ks0, sizeof(Ks0));
+  zero_lds<NW * 64>(Ks1, sizeof(Ks1));
+  zero_lds<NW * 64>(Vs0, sizeof(Vs0));
+  zero_lds<NW * 64>(Vs1, sizeof(Vs1));
   __syncthreads();
   TileLoader<BN, D, NW> ld;
   ld.init();
-  ld.load(kp, 0, S, Ks[0]);
-  ld.load(vp, 0, S, Vs[0]);
+  ld.load(kp, 0, S, Ks0);
+  ld.load(vp, 0, S, Vs0);
   auto tile = [&](auto bufc, int j) {
     constexpr int buf = decltype(bufc)::value;
     wait_loads();
     __syncthreads();
     if (j + 1 < ntiles) {
-      ld.load(kp, (j + 1) * BN, S, Ks[buf ^ 1]);
-      ld.load(vp, (j + 1) * BN, S, Vs[buf ^ 1]);
+      ld.load(kp, (j + 1) * BN, S, buf ? Ks0 : Ks1);
+      ld.load(vp, (j + 1) * BN, S, buf ? Vs0 : Vs1);
     }
     const int k0 = j * BN;
     if (k0 > wave_first_row + 31) return;
-    const uint16_t* Kb = Ks[buf];
-    const uint16_t* Vb = Vs[buf];
+    const uint16_t* Kb = buf ? Ks1 : Ks0;
+    const uint16_t* Vb = buf ? Vs1 : Vs0;
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
     // S^T = K Q^T and dP^T = V dO^T interleaved, each operand read kDqPrefetch MFMAs
     // ahead (read i: kk = i / 4, T2 = (i / 2) % 2, K for even i and V for odd i);
