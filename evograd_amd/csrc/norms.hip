@@ -65,6 +65,18 @@ inline int64_t ring_blocks(int64_t rows, int64_t per512, int block) {
   return rows < g ? (rows > 0 ? rows : 1) : g;
 }
 
+// Backward rings whose row stream is one 512-thread range (rows of 257-512 packs,
+// e.g. 4096 bf16 columns) run two streams per 1024-thread workgroup: the same
+// threads in flight as per512 workgroups of 512, half the partial rows. At
+// [16384, 4096] bf16 (backward call: ring + column sum, interleaved runs):
+// LayerNorm 78.6 -> 74.4 us, RMSNorm 74.3 -> 72.2 us, both with the ring's loads
+// issued unconditionally (with the loads under branches the split LayerNorm ring
+// was slower, 72.5 -> 85 us). The residual-add ring keeps its own configuration.
+inline bool bwd_split(int64_t npack, bool add) { return !add && npack > 256 && npack <= 512; }
+inline int64_t split_blocks(int64_t rows, int64_t per512) {
+  return ring_blocks((rows + 1) / 2, per512 / 2, 512);
+}
+
 // Workgroup width for a row of npack packs: (BLOCK, ITEMS) with BLOCK * ITEMS >= npack.
 template <typename F>
 bool pick_ring(int64_t npack, F&& f) {
@@ -116,12 +128,13 @@ __device__ __forceinline__ void st_vec(T* __restrict__ p, const float (&f)[VEC])
   store_vec<T, VEC, true>(p, f);
 }
 
-// Sums of N values over the workgroup with one barrier per call: per-wave
-// butterflies, then the wave totals added in wave order from one of two
-// alternating LDS slots. Every thread ends with the totals.
-template <int BLOCK, int N>
+// Sums of N values over each of the SPLIT equal thread ranges of the workgroup
+// (one row stream each), with one barrier per call: per-wave butterflies, then
+// the wave totals of the range added in wave order from one of two alternating
+// LDS slots. Every thread ends with its range's totals.
+template <int BLOCK, int N, int SPLIT = 1>
 struct SlotSum {
-  static constexpr int NW = BLOCK / kWave;
+  static constexpr int NW = BLOCK / kWave, NWS = NW / SPLIT;
   float (*slot)[N][NW];  // [2][N][NW] in LDS
   int par;
   __device__ __forceinline__ void operator()(float (&v)[N]) {
@@ -130,15 +143,16 @@ struct SlotSum {
     if constexpr (NW > 1) {
       const int lane = threadIdx.x & (kWave - 1);
       const int wid = threadIdx.x / kWave;
+      const int w0 = wid / NWS * NWS;  // first wave of this thread's range
       if (lane == 0)
 #pragma unroll
         for (int i = 0; i < N; ++i) slot[par][i][wid] = v[i];
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < N; ++i) {
-        float t = slot[par][i][0];
+        float t = slot[par][i][w0];
 #pragma unroll
-        for (int q = 1; q < NW; ++q) t += slot[par][i][q];
+        for (int q = 1; q < NWS; ++q) t += slot[par][i][w0 + q];
         v[i] = t;
       }
       par ^= 1;
@@ -485,53 +499,69 @@ __global__ __launch_bounds__(BLOCK) void layernorm_fwd_row(const T* __restrict__
 // LayerNorm: xhat = (x - mean) * rstd, dx = rstd * (g - mean(g) - xhat * mean(g * xhat))
 // dweight += dy * xhat, dbias += dy (per thread, per owned column).
 // ADD: the normalised row was s = x + r; it is formed again here from the inputs.
-template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN, bool ADD = false>
+// SPLIT: row streams per workgroup. With SPLIT = 2 the two halves of the workgroup
+// walk interleaved rows (stream s of workgroup b takes rows 2b + s, + 2G, ...) and
+// add their column sums in LDS (stream 0's + stream 1's) before the one partial row
+// of the workgroup is written: half the partial rows of SPLIT = 1 at the same
+// number of threads in flight.
+template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN, bool ADD = false,
+          int SPLIT = 1>
 __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ res,
     const T* __restrict__ w,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
     float* __restrict__ partial_w, float* __restrict__ partial_b, int64_t rows, int hidden) {
   static_assert(!(LN && ADD), "the residual add is fused into RMSNorm only");
+  static_assert(SPLIT == 1 || SPLIT == 2, "one or two row streams");
   constexpr int NS = LN ? 2 : 1;
+  constexpr int SB = BLOCK / SPLIT;  // threads per row stream
   __shared__ float slots[2][NS][BLOCK / kWave];
-  SlotSum<BLOCK, NS> bsum{slots, 0};
-  const int64_t G = gridDim.x;
+  SlotSum<BLOCK, NS, SPLIT> bsum{slots, 0};
+  const int sid = SPLIT > 1 ? (int)threadIdx.x / SB : 0;
+  const int tid = (int)threadIdx.x - sid * SB;
+  const int64_t GS = (int64_t)gridDim.x * SPLIT;  // row streams in the grid
+  const int64_t first = (int64_t)blockIdx.x * SPLIT;
   const float inv_h = 1.0f / (float)hidden;
-  int col[ITEMS];
+  // Every load is issued unconditionally: rows past the end read the last row and
+  // dead column packs read pack 0, and their data is never used. With the loads
+  // under branches the compiler's load waits are more conservative at the branch
+  // joins (the two-stream LayerNorm ring measured 85 against 69 us).
+  int col[ITEMS], lcol[ITEMS];
   bool live[ITEMS];
   float wv[ITEMS][VEC], aw[ITEMS][VEC], ab[ITEMS][VEC];
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
-    col[it] = (it * BLOCK + (int)threadIdx.x) * VEC;
+    col[it] = (it * SB + tid) * VEC;
     live[it] = col[it] < hidden;
+    lcol[it] = live[it] ? col[it] : 0;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) { wv[it][i] = 0.f; aw[it][i] = 0.f; ab[it][i] = 0.f; }
     if (live[it]) unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(w + col[it]), wv[it]);
   }
+  const int64_t last = rows - 1;
   Pack<T, VEC> xb[DEPTH][ITEMS], gb[DEPTH][ITEMS], resb[ADD ? DEPTH : 1][ITEMS];
   float rb[DEPTH], mb[DEPTH];
+  auto fill = [&](int k, int64_t row) {
+    const int64_t rc = row < rows ? row : last;
 #pragma unroll
-  for (int k = 0; k < DEPTH; ++k) {
-    const int64_t row = blockIdx.x + k * G;
-    rb[k] = 0.f;
-    mb[k] = 0.f;
-    if (row < rows) {
-#pragma unroll
-      for (int it = 0; it < ITEMS; ++it)
-        if (live[it]) {
-          xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
-          gb[k][it] = ld_raw<T, VEC>(dy + row * hidden + col[it]);
-          if (ADD) resb[ADD ? k : 0][it] = ld_raw<T, VEC>(res + row * hidden + col[it]);
-        }
-      rb[k] = rstd[row];
-      if (LN) mb[k] = mean[row];
+    for (int it = 0; it < ITEMS; ++it) {
+      xb[k][it] = ld_raw<T, VEC>(x + rc * hidden + lcol[it]);
+      gb[k][it] = ld_raw<T, VEC>(dy + rc * hidden + lcol[it]);
+      if (ADD) resb[ADD ? k : 0][it] = ld_raw<T, VEC>(res + rc * hidden + lcol[it]);
     }
-  }
-  for (int64_t base = blockIdx.x; base < rows; base += DEPTH * G) {
+    rb[k] = rstd[rc];
+    mb[k] = LN ? mean[rc] : 0.f;
+  };
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k) fill(k, first + sid + k * GS);
+  for (int64_t base = first; base < rows; base += DEPTH * GS) {
 #pragma unroll
     for (int k = 0; k < DEPTH; ++k) {
-      const int64_t row = base + k * G;
-      if (row >= rows) break;
+      // Stream 0's row decides for the whole workgroup (every thread reaches the
+      // barrier in bsum); stream 1 past the last row takes part with zero sums.
+      if (base + k * GS >= rows) break;
+      const int64_t row = base + k * GS + sid;
+      const bool here = row < rows;
       const float r = rb[k];
       const float mr = LN ? -mb[k] * r : 0.f;  // xhat = x * r + mr
       float xh[ITEMS][VEC], g[ITEMS][VEC];
@@ -541,22 +571,22 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
 #pragma unroll
       for (int it = 0; it < ITEMS; ++it) {
         float xv[VEC], gv[VEC];
+        unpack<T, VEC>(xb[k][it], xv);
+        unpack<T, VEC>(gb[k][it], gv);
+        if (ADD) {
+          float av[VEC];
+          unpack<T, VEC>(resb[ADD ? k : 0][it], av);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) { xv[i] = 0.f; gv[i] = 0.f; }
-        if (live[it]) {
-          unpack<T, VEC>(xb[k][it], xv);
-          unpack<T, VEC>(gb[k][it], gv);
-          if (ADD) {
-            float av[VEC];
-            unpack<T, VEC>(resb[ADD ? k : 0][it], av);
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) xv[i] += av[i];
-          }
+          for (int i = 0; i < VEC; ++i) xv[i] += av[i];
         }
+        // Dead packs (columns past the row, read from pack 0) and a stream's row past
+        // the end (read from the last row) take x = dy = 0, so they add nothing to the
+        // sums; their outputs are not stored.
+        const bool use = here && live[it];
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          // Columns past the row (whole dead packs) hold dy = 0 and a finite xhat,
-          // so they add nothing to the sums; their outputs are not stored.
+          xv[i] = use ? xv[i] : 0.f;
+          gv[i] = use ? gv[i] : 0.f;
           const float h = LN ? __builtin_fmaf(xv[i], r, mr) : xv[i] * r;
           aw[it][i] = __builtin_fmaf(gv[i], h, aw[it][i]);
           if (LN) ab[it][i] += gv[i];
@@ -567,19 +597,9 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
           g[it][i] = gg;
         }
       }
-      const int64_t nrow = row + DEPTH * G;
-      if (nrow < rows) {
-#pragma unroll
-        for (int it = 0; it < ITEMS; ++it)
-          if (live[it]) {
-            xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
-            gb[k][it] = ld_raw<T, VEC>(dy + nrow * hidden + col[it]);
-            if (ADD) resb[ADD ? k : 0][it] = ld_raw<T, VEC>(res + nrow * hidden + col[it]);
-          }
-        rb[k] = rstd[nrow];
-        if (LN) mb[k] = mean[nrow];
-      }
+      fill(k, row + DEPTH * GS);
       bsum(s);
+      if (!here) continue;
       // dx = r * (g - mean(g) - xhat * mean(g * xhat)) = g * r + (xhat * c2 + c1)
       const float c2 = -(s[0] * inv_h) * r;
       const float c1 = LN ? -(s[1] * inv_h) * r : 0.f;
@@ -594,6 +614,29 @@ __global__ __launch_bounds__(BLOCK) void norm_bwd_ring(
         st_vec<T, VEC>(dxr + col[it], o);
       }
     }
+  }
+  if constexpr (SPLIT > 1) {
+    // Stream 1 hands its column sums to stream 0 through LDS; stream 0 adds them
+    // to its own (that order) and writes the workgroup's partial row.
+    __shared__ float comb[NS][SB * ITEMS * VEC];
+    if (sid == 1) {
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          comb[0][(it * SB + tid) * VEC + i] = aw[it][i];
+          if (LN) comb[NS - 1][(it * SB + tid) * VEC + i] = ab[it][i];
+        }
+    }
+    __syncthreads();
+    if (sid == 1) return;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        aw[it][i] += comb[0][(it * SB + tid) * VEC + i];
+        if (LN) ab[it][i] += comb[NS - 1][(it * SB + tid) * VEC + i];
+      }
   }
   float* pw = partial_w + (int64_t)blockIdx.x * hidden;
   float* pb = LN ? partial_b + (int64_t)blockIdx.x * hidden : nullptr;
@@ -762,6 +805,13 @@ struct BwdRing {
     // Two workgroups per CU share its registers: half the forward's ring depth.
     constexpr int D = ADD ? ring_depth<ITEMS>()
                           : (ring_depth<ITEMS>() > 1 ? ring_depth<ITEMS>() / 2 : 1);
+    if constexpr (BLOCK == 512 && ITEMS == 1 && !ADD) {
+      // Two 512-thread row streams per 1024-thread workgroup (see bwd_split).
+      const int64_t G = split_blocks(rows, bwd_per512(LN, ADD));
+      EG_LAUNCH((norm_bwd_ring<T, VEC, 1, 1024, D, LN, ADD, 2>), dim3((unsigned)G), dim3(1024),
+                0, st, dy, x, res, w, mean, rstd, dx, pw, pb, rows, hidden);
+      return true;
+    }
     const int64_t G = ring_blocks(rows, bwd_per512(LN, ADD), BLOCK);
     EG_LAUNCH((norm_bwd_ring<T, VEC, ITEMS, BLOCK, D, LN, ADD>), dim3((unsigned)G), dim3(BLOCK),
               0, st, dy, x, res, w, mean, rstd, dx, pw, pb, rows, hidden);
@@ -794,6 +844,7 @@ bool vec_ok(int hidden, std::initializer_list<const void*> ptrs) {
 // Partial rows of the backward for a given dtype width (must match the launch).
 int64_t bwd_blocks(int64_t rows, int64_t hidden, bool ln, bool add, bool vec, int elem) {
   const int64_t npack = vec ? (hidden + (16 / elem) - 1) / (16 / elem) : hidden;
+  if (bwd_split(npack, add)) return split_blocks(rows, bwd_per512(ln, add));
   return ring_blocks(rows, bwd_per512(ln, add), ring_block_for(npack));
 }
 
