@@ -151,7 +151,7 @@ KERNELS = {
         "bwd": ["scale_copy_kernel(dx)", "scale_copy_kernel(dweight)"]},
     # bf16 rows of 128256: the forward's x and the backward's y held in registers
     # as raw packs, one kernel each
-    "softmax@vocab": {"fwd": ["softmax_fwd_raw"], "bwd": ["softmax_bwd_raw"]},
+    "softmax@vocab": {"fwd": ["softmax_fwd_lds"], "bwd": ["softmax_bwd_lds"]},
 }
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.

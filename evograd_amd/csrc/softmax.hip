@@ -8,8 +8,8 @@
 // One workgroup per row. When the row fits in registers (BLOCK threads x ITEMS
 // packs x VEC elements >= cols) it is read from HBM exactly once with 16-byte
 // loads, reduced with wave butterflies + one LDS exchange, and written once.
-// 16-bit rows up to 131072 columns keep the forward's x, and the backward's y, in
-// registers as raw packs (softmax_fwd_raw / softmax_bwd_raw). Wider rows take a
+// 16-bit rows up to 131072 columns are held on chip split between LDS and registers
+// (softmax_fwd_lds / softmax_bwd_lds), so both passes read HBM once. Wider rows take a
 // two-read path: the row's logsumexp
 // (forward) or sum(dy * y) (backward) in one read, then y = exp(x - lse) or
 // dx = y * (dy - sum) in a second read and the write.
@@ -164,12 +164,16 @@ __global__ __launch_bounds__(BLOCK) void softmax_bwd_loop(const T* __restrict__ 
   }
 }
 
-// ---- 16-bit rows up to 16 packs x 1024 threads (131072 columns, the Llama-3
-// vocabulary): the row stays in registers as raw 16-byte packs (64 VGPRs) and is
-// converted again in each pass, so it is read from HBM once. The empty asm
-// statements keep the compiler from hoisting fp32 copies of the row (128 VGPRs,
-// which would spill at 1024 threads).
+// ---- 16-bit rows of up to 131072 columns (the Llama-3 vocabulary): every input
+// byte is read from HBM once. A row is held on chip as raw 16-byte packs, split
+// between LDS (packs 0..LITEMS-1 of every thread, filled by buffer->LDS loads) and
+// registers, and converted to fp32 again in each pass; the empty asm statements keep
+// the compiler from hoisting fp32 copies of the register packs across the
+// reductions. All loads go through buffer resources bounded by the row's bytes, so
+// none sits under a branch: packs past the row read as zeros (registers) or leave
+// their LDS slot unwritten, and are masked in the reductions.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T>
 __device__ __forceinline__ void unpack8(const u32x4& raw, float (&f)[8]) {
@@ -179,111 +183,166 @@ __device__ __forceinline__ void unpack8(const u32x4& raw, float (&f)[8]) {
   for (int i = 0; i < 8; ++i) f[i] = to_f32(pk.v[i]);
 }
 
-template <typename T, int ITEMS, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void softmax_fwd_raw(const T* __restrict__ x,
-                                                         T* __restrict__ y, int cols) {
-  static_assert(sizeof(T) == 2, "raw rows hold 16-bit elements");
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const T* row, int cols) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), (short)0, cols * (int)sizeof(T),
+                                           0x00020000);
+}
+constexpr int kNtLoad = 2;  // buffer-load cache policy: non-temporal
+
+// Forward: 512-thread workgroups, two per CU (72 KB of LDS and at most 128 VGPRs each),
+// so that one workgroup's stores overlap the other's loads (one 1024-thread
+// workgroup per CU holding the row in registers: 405.6 us against 393.8 us at
+// [4096, 128256] bf16). The LDS packs are read one ahead of their use, each read's
+// address tied to the previous pack, so that the reads are not all hoisted into
+// registers at once.
+template <typename T, int ITEMS, int LITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void softmax_fwd_lds(const T* __restrict__ x, T* __restrict__ y, int cols) {
+  static_assert(sizeof(T) == 2, "16-bit rows");
+  constexpr int RI = ITEMS - LITEMS;
   __shared__ float lds[BLOCK / kWave];
+  __shared__ __align__(16) uint16_t xs[LITEMS * BLOCK * 8];
   const int64_t off = (int64_t)blockIdx.x * cols;
-  u32x4 raw[ITEMS];
-  u32x4 fill;
-  {
-    Pack<T, 8> pk;
+  const int tid = threadIdx.x, w = tid >> 6;
+  const __amdgpu_buffer_rsrc_t rx = row_rsrc(x + off, cols);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) pk.v[i] = from_f32<T>(-INFINITY);
-    __builtin_memcpy(&fill, &pk, 16);
-  }
+  for (int it = 0; it < LITEMS; ++it)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(xs + (it * BLOCK + w * kWave) * 8),
+                                             16, (it * BLOCK + tid) * 16, 0, 0, kNtLoad);
+  u32x4 xr[RI];
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
-    raw[it] = c < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + off + c))
-                       : fill;
-  }
+  for (int it = 0; it < RI; ++it)
+    xr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rx, ((it + LITEMS) * BLOCK + tid) * 16, 0, kNtLoad));
+  // A lane reads only the LDS slots its own loads wrote: no barrier needed.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  auto pass = [&](auto&& fn) {
+#pragma unroll
+    for (int it = LITEMS; it < ITEMS; ++it) fn(it, xr[it - LITEMS]);
+    const char* base = reinterpret_cast<const char*>(xs);
+    u32x4 cur = *reinterpret_cast<const u32x4*>(base + tid * 16);
+#pragma unroll
+    for (int it = 0; it < LITEMS; ++it) {
+      u32x4 nxt = cur;
+      if (it + 1 < LITEMS) {
+        int an = ((it + 1) * BLOCK + tid) * 16;
+        asm volatile("" : "+v"(an) : "v"(cur));
+        nxt = *reinterpret_cast<const u32x4*>(base + an);
+      }
+      fn(it, cur);
+      cur = nxt;
+    }
+  };
   float m = -INFINITY;
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
+  // Packs past the row (zeros from the register loads, unwritten LDS slots) are
+  // masked out of the max and the sum.
+  pass([&](int it, const u32x4& p) {
+    const bool in = (it * BLOCK + tid) * 8 < cols;
     float f[8];
-    unpack8<T>(raw[it], f);
+    unpack8<T>(p, f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, f[i]);
-  }
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, in ? f[i] : -INFINITY);
+  });
   m = block_reduce<BLOCK>(m, MaxOp(), lds);
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(raw[it]));
+  for (int it = 0; it < RI; ++it) asm volatile("" : "+v"(xr[it]));
   const float ml = m * rowwise::kLog2e;
   float s = 0.f;
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
+  pass([&](int it, const u32x4& p) {
+    const bool in = (it * BLOCK + tid) * 8 < cols;
     float f[8];
-    unpack8<T>(raw[it], f);
+    unpack8<T>(p, f);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      s += __builtin_amdgcn_exp2f(__builtin_fmaf(f[i], rowwise::kLog2e, -ml));
-  }
+      s += in ? __builtin_amdgcn_exp2f(__builtin_fmaf(f[i], rowwise::kLog2e, -ml)) : 0.f;
+  });
   s = block_reduce<BLOCK>(s, SumOp(), lds);
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(raw[it]));
+  for (int it = 0; it < RI; ++it) asm volatile("" : "+v"(xr[it]));
   const float ll = ml + log2f(s);  // log2 of the row's normaliser, max included
-#pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+  pass([&](int it, const u32x4& p) {
+    const int c = (it * BLOCK + tid) * 8;
     if (c < cols) {
       float f[8];
-      unpack8<T>(raw[it], f);
+      unpack8<T>(p, f);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         f[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(f[i], rowwise::kLog2e, -ll));
       store_vec<T, 8, true>(y + off + c, f);
     }
-  }
+  });
 }
-constexpr int kRawItems = 16, kRawBlock = 1024;
+constexpr int kFwdRowItems = 32, kFwdRowLds = 9, kFwdRowBlock = 512;
 
-// Backward for the same rows: y stays in registers as raw packs, dy is read twice
-// (the first read temporal, so the rows in flight serve the second from the
-// device cache): sum(dy * y), then dx = y * (dy - sum).
-template <typename T, int ITEMS, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void softmax_bwd_raw(const T* __restrict__ y,
+// Backward: one 1024-thread workgroup per CU. y in registers (64 VGPRs); dy's first
+// LITEMS packs per thread in LDS (144 KB), the rest in registers: y and dy are both
+// read once (against y in registers and dy read twice: 651.3 -> 544.2 us at
+// [4096, 128256] bf16, 1.21x -> 1.0x of the algorithmic bytes).
+template <typename T, int ITEMS, int LITEMS, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void softmax_bwd_lds(const T* __restrict__ y,
                                                          const T* __restrict__ dy,
                                                          T* __restrict__ dx, int cols) {
-  static_assert(sizeof(T) == 2, "raw rows hold 16-bit elements");
+  static_assert(sizeof(T) == 2, "16-bit rows");
+  constexpr int RI = ITEMS - LITEMS;
   __shared__ float lds[BLOCK / kWave];
+  __shared__ __align__(16) uint16_t dys[LITEMS * BLOCK * 8];
   const int64_t off = (int64_t)blockIdx.x * cols;
-  u32x4 raw[ITEMS];
+  const int tid = threadIdx.x, w = tid >> 6;
+  const __amdgpu_buffer_rsrc_t ry = row_rsrc(y + off, cols);
+  const __amdgpu_buffer_rsrc_t rg = row_rsrc(dy + off, cols);
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
-    raw[it] = c < cols ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(y + off + c))
-                       : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int it = 0; it < LITEMS; ++it)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void*)(dys + (it * BLOCK + w * kWave) * 8),
+                                             16, (it * BLOCK + tid) * 16, 0, 0, kNtLoad);
+  u32x4 yr[ITEMS], gr[RI];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+    yr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           ry, (it * BLOCK + tid) * 16, 0, kNtLoad));
+#pragma unroll
+  for (int it = 0; it < RI; ++it)
+    gr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rg, ((it + LITEMS) * BLOCK + tid) * 16, 0, kNtLoad));
+  // LDS slots past the row, which the bounded loads leave unwritten, hold zeros (the
+  // register loads return zeros there), so they add nothing to sum(dy * y).
+#pragma unroll
+  for (int it = 0; it < LITEMS; ++it)
+    if ((it * BLOCK + tid) * 8 >= cols)
+      *reinterpret_cast<u32x4*>(dys + (it * BLOCK + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own LDS slots only: no barrier
+  auto gpack = [&](int it) -> u32x4 {
+    return it < LITEMS ? *reinterpret_cast<const u32x4*>(dys + (it * BLOCK + tid) * 8)
+                       : gr[it - LITEMS];
+  };
   float d = 0.f;
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
-    if (c < cols) {
-      float f[8], g[8];
-      unpack8<T>(raw[it], f);
-      load_vec<T, 8, false>(dy + off + c, g);
+    float f[8], g[8];
+    unpack8<T>(yr[it], f);
+    unpack8<T>(gpack(it), g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d += f[i] * g[i];
-    }
+    for (int i = 0; i < 8; ++i) d += f[i] * g[i];
   }
   d = block_reduce<BLOCK>(d, SumOp(), lds);
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(raw[it]));
+  for (int it = 0; it < ITEMS; ++it) asm volatile("" : "+v"(yr[it]));
+#pragma unroll
+  for (int it = 0; it < RI; ++it) asm volatile("" : "+v"(gr[it]));
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
-    const int c = (it * BLOCK + (int)threadIdx.x) * 8;
+    const int c = (it * BLOCK + tid) * 8;
     if (c < cols) {
       float f[8], g[8];
-      unpack8<T>(raw[it], f);
-      load_vec<T, 8, true>(dy + off + c, g);
+      unpack8<T>(yr[it], f);
+      unpack8<T>(gpack(it), g);
 #pragma unroll
       for (int i = 0; i < 8; ++i) g[i] = f[i] * (g[i] - d);
       store_vec<T, 8, true>(dx + off + c, g);
     }
   }
 }
+constexpr int kBwdRowItems = 16, kBwdRowLds = 9, kBwdRowBlock = 1024;
 
 // Picks (BLOCK, ITEMS) so that BLOCK * ITEMS packs cover the row; returns false
 // when the row is too wide for the register path.
@@ -326,9 +385,9 @@ void softmax_fwd_vec(const T* x, T* y, int64_t rows, int cols, hipStream_t st) {
   const int64_t npack = (cols + VEC - 1) / VEC;
   if (pick_row_config(npack, l)) return;
   if constexpr (sizeof(T) == 2 && VEC == 8) {
-    if (npack <= (int64_t)kRawItems * kRawBlock) {
-      EG_LAUNCH((softmax_fwd_raw<T, kRawItems, kRawBlock>), dim3((unsigned)rows), dim3(kRawBlock),
-                0, st, x, y, cols);
+    if (npack <= (int64_t)kFwdRowItems * kFwdRowBlock) {
+      EG_LAUNCH((softmax_fwd_lds<T, kFwdRowItems, kFwdRowLds, kFwdRowBlock>), dim3((unsigned)rows),
+                dim3(kFwdRowBlock), 0, st, x, y, cols);
       return;
     }
   }
@@ -342,9 +401,9 @@ void softmax_bwd_vec(const T* y, const T* dy, T* dx, int64_t rows, int cols, hip
   const int64_t npack = (cols + VEC - 1) / VEC;
   if (pick_row_config(npack, l)) return;
   if constexpr (sizeof(T) == 2 && VEC == 8) {
-    if (npack <= (int64_t)kRawItems * kRawBlock) {
-      EG_LAUNCH((softmax_bwd_raw<T, kRawItems, kRawBlock>), dim3((unsigned)rows), dim3(kRawBlock),
-                0, st, y, dy, dx, cols);
+    if (npack <= (int64_t)kBwdRowItems * kBwdRowBlock) {
+      EG_LAUNCH((softmax_bwd_lds<T, kBwdRowItems, kBwdRowLds, kBwdRowBlock>), dim3((unsigned)rows),
+                dim3(kBwdRowBlock), 0, st, y, dy, dx, cols);
       return;
     }
   }
