@@ -162,7 +162,10 @@ struct SlotSum {
 
 // --------------------------------------------------------------- forward
 // ADD: the normalised row is s = x + r (fused residual add), formed in fp32.
-template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN, bool ADD = false>
+// SPLIT: row streams per workgroup, as in norm_bwd_ring. Every load is issued
+// unconditionally (rows past the end read the last row, dead packs read pack 0).
+template <typename T, int VEC, int ITEMS, int BLOCK, int DEPTH, bool LN, bool ADD = false,
+          int SPLIT = 1>
 __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
                                                        const T* __restrict__ r,
                                                        const T* __restrict__ w,
@@ -172,17 +175,23 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
                                                        float* __restrict__ rstd_out,
                                                        int64_t rows, int hidden, float eps) {
   static_assert(!(LN && ADD), "the residual add is fused into RMSNorm only");
+  static_assert(SPLIT == 1 || SPLIT == 2, "one or two row streams");
+  constexpr int SB = BLOCK / SPLIT;
   __shared__ float slots[2][1][BLOCK / kWave];
-  SlotSum<BLOCK, 1> bsum{slots, 0};
-  const int64_t G = gridDim.x;
+  SlotSum<BLOCK, 1, SPLIT> bsum{slots, 0};
+  const int sid = SPLIT > 1 ? (int)threadIdx.x / SB : 0;
+  const int tid = (int)threadIdx.x - sid * SB;
+  const int64_t GS = (int64_t)gridDim.x * SPLIT;
+  const int64_t first = (int64_t)blockIdx.x * SPLIT;
   const float inv_h = 1.0f / (float)hidden;
-  int col[ITEMS];
+  int col[ITEMS], lcol[ITEMS];
   bool live[ITEMS];
   float wv[ITEMS][VEC], bv[ITEMS][VEC];
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
-    col[it] = (it * BLOCK + (int)threadIdx.x) * VEC;
+    col[it] = (it * SB + tid) * VEC;
     live[it] = col[it] < hidden;
+    lcol[it] = live[it] ? col[it] : 0;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) { wv[it][i] = 0.f; bv[it][i] = 0.f; }
     if (live[it]) {
@@ -190,45 +199,39 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
       if (LN) unpack<T, VEC>(*reinterpret_cast<const Pack<T, VEC>*>(b + col[it]), bv[it]);
     }
   }
+  const int64_t last = rows - 1;
   Pack<T, VEC> xb[DEPTH][ITEMS], rb[ADD ? DEPTH : 1][ITEMS];
+  auto fill = [&](int k, int64_t row) {
+    const int64_t rc = row < rows ? row : last;
 #pragma unroll
-  for (int k = 0; k < DEPTH; ++k) {
-    const int64_t row = blockIdx.x + k * G;
+    for (int it = 0; it < ITEMS; ++it) {
+      xb[k][it] = ld_raw<T, VEC>(x + rc * hidden + lcol[it]);
+      if (ADD) rb[ADD ? k : 0][it] = ld_raw<T, VEC>(r + rc * hidden + lcol[it]);
+    }
+  };
 #pragma unroll
-    for (int it = 0; it < ITEMS; ++it)
-      if (row < rows && live[it]) {
-        xb[k][it] = ld_raw<T, VEC>(x + row * hidden + col[it]);
-        if (ADD) rb[ADD ? k : 0][it] = ld_raw<T, VEC>(r + row * hidden + col[it]);
-      }
-  }
-  for (int64_t base = blockIdx.x; base < rows; base += DEPTH * G) {
+  for (int k = 0; k < DEPTH; ++k) fill(k, first + sid + k * GS);
+  for (int64_t base = first; base < rows; base += DEPTH * GS) {
 #pragma unroll
     for (int k = 0; k < DEPTH; ++k) {
-      const int64_t row = base + k * G;
-      if (row >= rows) break;
+      if (base + k * GS >= rows) break;  // stream 0's row decides for the workgroup
+      const int64_t row = base + k * GS + sid;
+      const bool here = row < rows;
       float xv[ITEMS][VEC];
 #pragma unroll
       for (int it = 0; it < ITEMS; ++it) {
+        unpack<T, VEC>(xb[k][it], xv[it]);
+        if (ADD) {
+          float rv[VEC];
+          unpack<T, VEC>(rb[ADD ? k : 0][it], rv);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[it][i] = 0.f;
-        if (live[it]) {
-          unpack<T, VEC>(xb[k][it], xv[it]);
-          if (ADD) {
-            float rv[VEC];
-            unpack<T, VEC>(rb[ADD ? k : 0][it], rv);
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) xv[it][i] += rv[i];
-          }
+          for (int i = 0; i < VEC; ++i) xv[it][i] += rv[i];
         }
-      }
-      const int64_t nrow = row + DEPTH * G;
-      if (nrow < rows)
+        // dead packs (read from pack 0) are zero
 #pragma unroll
-        for (int it = 0; it < ITEMS; ++it)
-          if (live[it]) {
-            xb[k][it] = ld_raw<T, VEC>(x + nrow * hidden + col[it]);
-            if (ADD) rb[ADD ? k : 0][it] = ld_raw<T, VEC>(r + nrow * hidden + col[it]);
-          }
+        for (int i = 0; i < VEC; ++i) xv[it][i] = live[it] ? xv[it][i] : 0.f;
+      }
+      fill(k, row + DEPTH * GS);
       float mean = 0.f;
       if (LN) {
         float s[1] = {0.f};
@@ -249,6 +252,7 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
           q[0] += d * d;
         }
       bsum(q);
+      if (!here) continue;
       const float rstd = rsqrtf(q[0] * inv_h + eps);
       T* yr = y + row * hidden;
 #pragma unroll
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(BLOCK) void norm_fwd_ring(const T* __restrict__ x,
                     : (xv[it][i] * rstd) * wv[it][i];
         st_vec<T, VEC>(yr + col[it], o);
       }
-      if (threadIdx.x == 0) {
+      if (tid == 0) {
         rstd_out[row] = rstd;
         if (LN) mean_out[row] = mean;
       }
