@@ -34,9 +34,11 @@
 //
 // Kernels (all deterministic, no atomics):
 //   attn_fwd:   workgroup = 4 waves x 32 query rows; double-buffered 64-key K and
-//               V tiles; online softmax in the log2 domain, the running max
-//               refreshed only when it grows by more than 2^8 (exact: the
-//               reference point cancels in o = sum / l); S^T = K Q^T, O^T += V^T P^T.
+//               V tiles; online softmax in the log2 domain against a running
+//               reference max, refreshed only when a P term could exceed 2^8 (a
+//               lane's sum of P terms bounds each term, so no per-tile max is
+//               formed; exact: the reference point cancels in o = sum / l);
+//               S^T = K Q^T, O^T += V^T P^T.
 //   attn_dq:    (runs first) workgroup = 4 waves x 32 query rows; also computes
 //               delta = rowsum(do * o) for its rows into the workspace;
 //               double-buffered 64-key K, V tiles; S^T = K Q^T, dP^T = V dO^T,
@@ -80,7 +82,7 @@ template <> struct MM<f16_t> {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kRescaleThreshold = 8.0f;  // log2 units: refresh the max past 2^8 growth
+constexpr float kRescaleBound = 256.0f;  // largest P term kept without a max refresh
 constexpr int kFwdPrefetch = 4;            // forward S operand reads in flight
 constexpr int kDqPrefetch = 2;             // dQ S / dP operand reads in flight
 
@@ -387,11 +389,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
     if (k0 > wave_first_row + 31) return;  // every key of the tile is above this wave's rows
     const uint16_t* Kb = buf ? Ks1 : Ks0;
     const uint16_t* Vb = buf ? Vs1 : Vs0;
-    f32x16 s[2] = {f32x16{}, f32x16{}};
+    f32x16 s[2];
     // S^T = K Q^T with the K operand reads kFwdPrefetch MFMAs ahead of their use
     // (MFMA i takes (kk, T2) = (i / 2, i % 2)); the scheduling groups keep that
-    // order, which the default schedule would collapse to one read ahead.
-    {
+    // order, which the default schedule would collapse to one read ahead. Keys past
+    // the diagonal (and past S) are set to -inf (diagonal tiles only).
+    auto scores = [&]() {
+      s[0] = f32x16{};
+      s[1] = f32x16{};
       constexpr int NM = 2 * KSTEPS, PF = kFwdPrefetch;
       v8 ring[PF];
       __builtin_amdgcn_sched_barrier(0);
@@ -412,46 +417,56 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_kernel(
         if (i + PF < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-
-    // Raw scores: keys past the diagonal (and past S) are -inf; max in raw units.
-    float mt = -INFINITY;
-    if (k0 + BN - 1 > wave_first_row) {
+      if (k0 + BN - 1 > wave_first_row) {
+#pragma unroll
+        for (int T2 = 0; T2 < 2; ++T2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
+            if (key > qrow) s[T2][r] = -INFINITY;
+          }
+      }
+    };
+    auto exps = [&](float nm) {
+      float sum = 0.f;
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 32 * T2 + (r >> 2) * 8 + 4 * hh + (r & 3);
-          if (key > qrow) s[T2][r] = -INFINITY;
-          mt = fmaxf(mt, s[T2][r]);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[T2][r], scale_log2, nm));
+          s[T2][r] = p;
+          sum += p;
         }
-    } else {
+      return sum;
+    };
+    scores();
+    // P against the running reference max m (log2 units), in place. A lane's sum of
+    // its 32 terms bounds each of them, so a sum <= 2^8 shows that no score of its
+    // row grew past m + 8. Otherwise (and on the first tile, where m is -inf, or
+    // on overflow) the tile's scores are formed again, the row max is taken, the
+    // running sums are rescaled to it and P is recomputed.
+    float ps = 0.f;
+    bool refresh = j == 0;
+    if (!refresh) {
+      ps = exps(-m);
+      refresh = __builtin_amdgcn_ballot_w64(!(ps <= kRescaleBound)) != 0;
+      if (refresh) scores();
+    }
+    if (refresh) {
+      float mt = -INFINITY;
 #pragma unroll
       for (int T2 = 0; T2 < 2; ++T2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[T2][r]);
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
-    // Refresh the reference max only when some row's max grew past the
-    // threshold (always on the first tile, where m is -inf).
-    if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleThreshold) != 0) {
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * scale_log2;
       const float m_new = fmaxf(m, mt);
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);
       lsum *= alpha;
 #pragma unroll
       for (int t = 0; t < DT; ++t) acc[t] *= alpha;
       m = m_new;
+      ps = exps(m == -INFINITY ? 0.f : -m);
     }
-    const float nm = m == -INFINITY ? 0.f : -m;
-    float ps = 0.f;
-#pragma unroll
-    for (int T2 = 0; T2 < 2; ++T2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[T2][r], scale_log2, nm));
-        s[T2][r] = p;
-        ps += p;
-      }
     lsum += ps;
 #pragma unroll
     for (int ms = 0; ms < BN / 16; ++ms) {
