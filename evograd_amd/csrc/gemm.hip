@@ -15,6 +15,11 @@
 // wave per SIMD). Per 64-deep k step a workgroup stages a 256 x 64 slice of each
 // operand in LDS (32 KB each, double-buffered: 128 KB), filled by direct
 // buffer->LDS loads (16 bytes per lane, no VGPR staging) issued one step ahead.
+// Each wave's 16 loads of the next slice are spread over the first 32 (both
+// operands K-contiguous) or 40 of the step's 64 MFMAs: a load instruction holds
+// the wave's issue for several cycles, and issued as one block before the MFMAs
+// they left the matrix unit idle (measured at the benchmark sizes: logits
+// 44.6 -> 49.0%, dx 44.8 -> 52.8%, dweight 42.2 -> 48.7% of bf16 peak).
 // Operands reach the MFMA v_mfma_f32_32x32x16_{bf16,f16} (lane l: row/column
 // l%32, k = 8(l/32) .. +7) as
 //   K-contiguous slice [256][64]: one ds_read_b128 per operand, 16-byte chunks
@@ -24,7 +29,10 @@
 //     consecutive k of one column each), chunks XOR-swizzled by 4 (k & 3) so the
 //     4 rows of one transposed read fall in 4 distinct 64-byte quarters.
 // Per k step a wave issues 64 MFMAs against 32 (K-contiguous) or 64 (K-major)
-// LDS reads.
+// LDS reads. The MFMA takes the B operand as its first (row) operand, so each
+// accumulator holds a tile of C^T: lane l keeps row l%32 of C and four
+// consecutive columns per register group, stored as one 16-byte (fp32) or 8-byte
+// (16-bit) vector.
 //
 // Bounds: rows of an operand past its end are outside the buffer resource's range
 // and read as zero, so M, N and a K-major operand's K may be ragged. A K-contiguous
@@ -181,11 +189,14 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles, int& tm, int& tn
   tn = r / gm;
 }
 
+// MFMAs of one k step over which a wave's 16 slice loads are spread.
+template <bool AKC, bool BKC> struct LoadSpread { static constexpr int value = AKC && BKC ? 32 : 40; };
+
 template <typename T, bool AKC, bool BKC, typename TC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
-                 int64_t a_rows, int64_t b_rows, int tiles_m, int tiles) {
+                 int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c) {
   using v8 = typename GM<T>::v8;
   // Two separate buffers per operand, selected at compile time in the unrolled k
   // loop: the LDS reads of one buffer provably do not alias the loads in flight
@@ -203,28 +214,18 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   SliceLoader<BKC> lb;
   la.init(lda);
   lb.init(ldb);
-  // slice k of each operand: its first element and the bytes to the matrix end
   const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
-  auto a_at = [&](int k0, int64_t& left) {
-    const int64_t off = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
-    left = (a_end - off) * 2;
-    return A + off;
-  };
-  auto b_at = [&](int k0, int64_t& left) {
-    const int64_t off = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
-    left = (b_end - off) * 2;
-    return B + off;
-  };
   const int nk = (K + kBK - 1) / kBK;
-  // The k loop runs an even number of steps (two per iteration, one per buffer); the
-  // step past K, when nk is odd, loads through an empty range and adds zeros.
+  // The k loop runs an even number of steps (two per iteration, one per buffer). A
+  // slice at or past nk loads through an empty range: the step past K, when nk is
+  // odd, adds zeros, and the load issued in the last step fills nothing.
   const int nk2 = nk + (nk & 1);
   auto load = [&](int kt, uint16_t* as, uint16_t* bs) {
-    int64_t left;
-    const uint16_t* pa = a_at(kt * kBK, left);
-    la.load(pa, kt < nk ? left : 0, as);
-    const uint16_t* pb = b_at(kt * kBK, left);
-    lb.load(pb, kt < nk ? left : 0, bs);
+    const int k0 = kt * kBK;
+    const int64_t oa = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
+    const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
+    la.load(A + oa, kt < nk ? (a_end - oa) * 2 : 0, as);
+    lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
   };
 
   f32x16 acc[4][4];
@@ -234,20 +235,22 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
   // One k step on the slices in (as, bs): the operands of substep s + 1 are read
-  // while the 16 MFMAs of substep s run.
+  // while the 16 MFMAs of substep s run; `issue` emits the next slice's loads.
   OperandReader<AKC> ra;
   OperandReader<BKC> rb;
   ra.init(wm, lane);
   rb.init(wn, lane);
   // LDS read instructions per substep (a K-major operand takes two per block).
   constexpr int NR = 4 * (AKC ? 1 : 2) + 4 * (BKC ? 1 : 2);
-  auto compute = [&](const uint16_t* as, const uint16_t* bs) {
+  constexpr int DS = LoadSpread<AKC, BKC>::value;
+  auto compute = [&](const uint16_t* as, const uint16_t* bs, auto&& issue) {
     v8 a[2][4], b[2][4];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[0][i] = ra.template read<v8>(as, i, 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) b[0][j] = rb.template read<v8>(bs, j, 0);
+    issue();
 #pragma unroll
     for (int s = 0; s < kBK / 16; ++s) {
       const int cur = s & 1;
@@ -260,16 +263,21 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = GM<T>::mma(a[cur][i], b[cur][j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = GM<T>::mma(b[cur][j], a[cur][i], acc[i][j]);
     }
-    // Schedule: the reads of substep 0, then each substep's 16 MFMAs with the NR
-    // reads of the next substep spread evenly among them.
+    // Schedule: the reads of substep 0, then the 64 MFMAs with the 16 slice loads
+    // spread over the first DS of them and the NR reads of each next substep over
+    // the 16 MFMAs of the current one.
     __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
 #pragma unroll
     for (int s = 0; s < kBK / 16; ++s)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        const int qq = s * 16 + q;
+        // DS >= 16: at most one load after each MFMA
+        if (qq < DS && ((qq + 1) * 16) / DS != (qq * 16) / DS)
+          __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
         // NR <= 16: at most one read after each MFMA
         if (s + 1 < kBK / 16 && ((q + 1) * NR) / 16 != (q * NR) / 16)
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -282,26 +290,49 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     constexpr bool odd = decltype(bufc)::value;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (kt + 1 < nk2) load(kt + 1, odd ? As0 : As1, odd ? Bs0 : Bs1);
-    compute(odd ? As1 : As0, odd ? Bs1 : Bs0);
+    compute(odd ? As1 : As0, odd ? Bs1 : Bs0,
+            [&] { load(kt + 1, odd ? As0 : As1, odd ? Bs0 : Bs1); });
   };
   for (int kt = 0; kt < nk2; kt += 2) {
     step(std::false_type{}, kt);
     step(std::true_type{}, kt + 1);
   }
 
-  // C tile (i, j): lane l holds column l%32, register r holds row 8(r/4) + 4(l/32) + r%4.
+  // C tile (i, j): lane l holds row l%32, register r holds column 8(r/4) + 4(l/32) + r%4.
   const int hh = lane >> 5, l32 = lane & 31;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = n0 + wn + 32 * j + l32;
-    if (col >= N) continue;
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + wm + 32 * i + l32;
+    if (row >= M) continue;
+    TC* crow = C + (int64_t)row * ldc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (row < M) put<TC>(C + (int64_t)row * ldc + col, acc[i][j][r]);
+      for (int q = 0; q < 4; ++q) {
+        const int col = n0 + wn + 32 * j + 8 * q + 4 * hh;
+        const float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1];
+        const float v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        if (vec_c && col + 3 < N) {
+          if constexpr (std::is_same<TC, float>::value) {
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<f32x4*>(crow + col) = f32x4{v0, v1, v2, v3};
+          } else {
+            typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+            auto bits = [](TC x) {
+              uint16_t u;
+              __builtin_memcpy(&u, &x, 2);
+              return (unsigned)u;
+            };
+            *reinterpret_cast<u32x2*>(crow + col) =
+                u32x2{bits(from_f32<TC>(v0)) | (bits(from_f32<TC>(v1)) << 16),
+                      bits(from_f32<TC>(v2)) | (bits(from_f32<TC>(v3)) << 16)};
+          }
+        } else {
+          if (col < N) put<TC>(crow + col, v0);
+          if (col + 1 < N) put<TC>(crow + col + 1, v1);
+          if (col + 2 < N) put<TC>(crow + col + 2, v2);
+          if (col + 3 < N) put<TC>(crow + col + 3, v3);
+        }
       }
   }
 }
@@ -433,12 +464,15 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     return 1;
   }
   const unsigned grid = (unsigned)(((tiles + 7) / 8) * 8);
+  // 16-byte (fp32) or 8-byte (16-bit) row pieces of C need ldc % 4 == 0 and a
+  // 16-byte aligned base; otherwise the kernel stores element by element.
+  const int vec_c = (ldc % 4 == 0) && aligned16(C);
   auto go = [&](auto tag, auto ctag, auto akc, auto bkc) {
     using T = decltype(tag);
     using TC = decltype(ctag);
     EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>), dim3(grid),
               dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
-              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles);
+              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c);
     return check_launch(name);
   };
   auto layouts = [&](auto tag, auto ctag) {
