@@ -139,15 +139,13 @@ KERNELS = {
                          "bwd": ["rope_kernel", "attn_dq_kernel", "attn_dkdv_kernel"]},
     "cross_entropy":{"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
                       "bwd": ["xent_bwd_flat_kernel"]},
-    # eg_flce_fwd at 8192 rows of 128256 (two 4096-row chunks; the vocabulary needs no
-    # column padding): per chunk the logits product, the row logsumexp, the unit
-    # gradient and the dx product; then the dweight product over all rows and the
-    # mean. The backward's two dloss / n scalings.
+    # eg_flce_fwd at 8192 rows of 128256 (bf16: one chunk; the vocabulary needs no
+    # column padding): the logits product with its softmax epilogue, the per-row
+    # fix-up (logsumexp, row loss, unit gradient in place), the dx product, the
+    # dweight product and the mean. The backward's two dloss / n scalings.
     "fused_linear_cross_entropy": {
-        "fwd": ["gemm_kernel(logits 0)", "xent_lse_kernel(0)", "xent_bwd_flat_kernel(0)",
-                "gemm_kernel(dx 0)", "gemm_kernel(logits 1)", "xent_lse_kernel(1)",
-                "xent_bwd_flat_kernel(1)", "gemm_kernel(dx 1)", "gemm_kernel(dweight)",
-                "xent_mean_kernel"],
+        "fwd": ["gemm_kernel(logits)", "flce_fixup_kernel", "gemm_kernel(dx)",
+                "gemm_kernel(dweight)", "xent_mean_kernel"],
         "bwd": ["scale_copy_kernel(dx)", "scale_copy_kernel(dweight)"]},
     # bf16 rows of 128256: the forward's x and the backward's y held in registers
     # as raw packs, one kernel each
@@ -161,7 +159,7 @@ DOMINANT = {
     "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
     "llama3_attention": ("bwd", 2),
     "cross_entropy": ("bwd", 0),
-    "fused_linear_cross_entropy": ("fwd", 8),
+    "fused_linear_cross_entropy": ("fwd", 3),
     "softmax@vocab": ("bwd", 0),
 }
 

@@ -234,6 +234,20 @@ int gemm_launch(const void* a, const void* b, void* c, int64_t m, int64_t n, int
                 int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
                 int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name);
 
+// The logits product of the fused linear cross entropy with its softmax terms
+// formed in the epilogue (gemm.hip), 16-bit operands only: for logits = x w^T
+// (x [m][ldx] and w [n][ldw] both k-contiguous, k % 64 == 0) it writes, per
+// 128-column group h of a row (columns 128h .. 128h + 127),
+//   e[row][col] = exp(logit - mx_h) in the operand dtype (ld lde),
+//   hstats[(row * nh2 + h) * 2 + {0, 1}] = mx_h, sum over the group of exp(logit - mx_h),
+// with nh2 = flce_groups(n), and tlogit[row] = logit[row][target[row]] (fp32) when
+// the target is a column of [0, n); nothing for rows whose target is not.
+int64_t flce_groups(int64_t n);
+int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t m, int64_t n,
+                               int64_t k, int64_t ldx, int64_t ldw, int64_t lde,
+                               const int64_t* target, float* hstats, float* tlogit, int dtype,
+                               hipStream_t st, const char* name);
+
 // The RoPE launch behind eg_rope (rope.hip), for entry points that rotate as one
 // step of a longer launch sequence: arguments as eg_rope's, already validated.
 int rope_apply(const void* q, const void* k, void* q_out, void* k_out, const void* cos,

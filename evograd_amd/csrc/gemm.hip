@@ -189,14 +189,33 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles, int& tm, int& tn
   tn = r / gm;
 }
 
+// Softmax epilogue of the logits product (SMX): target [M], per-group statistics
+// [M][nh2][2] and the target logits [M].
+struct SmxArgs {
+  const int64_t* target;
+  float* hstats;
+  float* tlogit;
+  int nh2;
+};
+
+// One accumulator value read out of its AGPR. The "a" operand keeps the
+// accumulators in AGPRs through the k loop when an epilogue feeds them to VALU
+// work (otherwise the allocator moves them to VGPRs and spills inside the loop).
+__device__ __forceinline__ float acc_read(float x) {
+  float r;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
+  return r;
+}
+
 // MFMAs of one k step over which a wave's 16 slice loads are spread.
 template <bool AKC, bool BKC> struct LoadSpread { static constexpr int value = AKC && BKC ? 32 : 40; };
 
-template <typename T, bool AKC, bool BKC, typename TC>
+template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
-                 int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c) {
+                 int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c,
+                 SmxArgs smx) {
   using v8 = typename GM<T>::v8;
   // Two separate buffers per operand, selected at compile time in the unrolled k
   // loop: the LDS reads of one buffer provably do not alias the loads in flight
@@ -300,6 +319,97 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 
   // C tile (i, j): lane l holds row l%32, register r holds column 8(r/4) + 4(l/32) + r%4.
   const int hh = lane >> 5, l32 = lane & 31;
+  if constexpr (SMX) {
+    // The wave's 128 columns of each row are one softmax group: lanes l and l + 32
+    // hold 64 of them each. Max, then e = exp(logit - max) stored in TC and summed;
+    // the target logit is picked by a select chain and stored by its lane.
+    constexpr float kL2e = 1.4426950408889634f;
+    const int cb = n0 + wn;  // first column of the group
+    auto rows_of = [&](auto fullc) {
+      constexpr bool FULL = decltype(fullc)::value;  // all 128 columns below N
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = m0 + wm + 32 * i + l32;
+        const bool rv = row < M;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int col = cb + 32 * j + 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (FULL || col < N) mx = fmaxf(mx, acc_read(acc[i][j][r]));
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // reference point of the exponentials: an infinite max is replaced by 0
+        const float ms = __builtin_isinf(mx) ? 0.f : mx * kL2e;
+        // this lane's offset of the target column among its 64 (-1: not here)
+        const int64_t tgt = rv ? smx.target[row] : -1;
+        const int64_t toff = tgt - cb - 4 * hh;
+        const int tk = (toff >= 0 && toff < 128 && (toff & 4) == 0 && tgt < N) ? (int)toff : -1;
+        float sm = 0.f;
+        TC* crow = C + (int64_t)(rv ? row : 0) * ldc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int col = cb + 32 * j + 8 * q + 4 * hh;
+            float ev[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = acc_read(acc[i][j][4 * q + e]);
+              ev[e] = (FULL || col + e < N) ? __builtin_amdgcn_exp2f(__builtin_fmaf(a, kL2e, -ms))
+                                            : 0.f;
+              sm += ev[e];
+            }
+            if (rv) {
+              if (vec_c && (FULL || col + 3 < N)) {
+                typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+                auto bits = [](TC x) {
+                  uint16_t u;
+                  __builtin_memcpy(&u, &x, 2);
+                  return (unsigned)u;
+                };
+                *reinterpret_cast<u32x2*>(crow + col) =
+                    u32x2{bits(from_f32<TC>(ev[0])) | (bits(from_f32<TC>(ev[1])) << 16),
+                          bits(from_f32<TC>(ev[2])) | (bits(from_f32<TC>(ev[3])) << 16)};
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  if (col + e < N) put<TC>(crow + col + e, ev[e]);
+              }
+            }
+          }
+        sm += __shfl_xor(sm, 32, 64);
+        if (tk >= 0) {
+          // acc[i][tk >> 5][4 ((tk >> 3) & 3) + (tk & 3)] by a select tree
+          const int tj = tk >> 5, tq = (tk >> 3) & 3, te = tk & 3;
+          float w4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = 4 * q + e;
+              const float a0 = acc_read(acc[i][0][r]), a1 = acc_read(acc[i][1][r]);
+              const float a2 = acc_read(acc[i][2][r]), a3 = acc_read(acc[i][3][r]);
+              v4[q] = tj == 0 ? a0 : tj == 1 ? a1 : tj == 2 ? a2 : a3;
+            }
+            w4[e] = tq == 0 ? v4[0] : tq == 1 ? v4[1] : tq == 2 ? v4[2] : v4[3];
+          }
+          smx.tlogit[row] = te == 0 ? w4[0] : te == 1 ? w4[1] : te == 2 ? w4[2] : w4[3];
+        }
+        if (rv && hh == 0 && cb < N) {
+          float* hs = smx.hstats + ((int64_t)row * smx.nh2 + (cb >> 7)) * 2;
+          hs[0] = mx;
+          hs[1] = sm;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (cb + 128 <= N) rows_of(std::true_type{});
+    else rows_of(std::false_type{});
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = m0 + wm + 32 * i + l32;
@@ -472,7 +582,7 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     using TC = decltype(ctag);
     EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>), dim3(grid),
               dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
-              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c);
+              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c, SmxArgs{});
     return check_launch(name);
   };
   auto layouts = [&](auto tag, auto ctag) {
@@ -486,6 +596,47 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
   if (dtype == EG_BF16)
     return c_dtype == EG_F32 ? layouts(bf16_t{}, float{}) : layouts(bf16_t{}, bf16_t{});
   return c_dtype == EG_F32 ? layouts(f16_t{}, float{}) : layouts(f16_t{}, f16_t{});
+}
+
+int64_t flce_groups(int64_t n) { return 2 * ((n + kBN - 1) / kBN); }
+
+int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M, int64_t N,
+                               int64_t K, int64_t ldx, int64_t ldw, int64_t lde,
+                               const int64_t* target, float* hstats, float* tlogit, int dtype,
+                               hipStream_t st, const char* name) {
+  if (M <= 0 || N <= 0) return 0;
+  if (dtype != EG_BF16 && dtype != EG_F16) {
+    set_error("%s: the softmax epilogue takes bf16 or fp16 operands", name);
+    return 1;
+  }
+  if (K <= 0 || K % kBK || ldx % 8 || ldw % 8 || ldx < K || ldw < K || lde < N ||
+      !aligned16(x) || !aligned16(w)) {
+    set_error("%s: logits product needs K %% 64 == 0, strides >= K in multiples of 8 and "
+              "16-byte aligned operands", name);
+    return 1;
+  }
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || 256 * ldx * 2 >= ((int64_t)1 << 31) ||
+      256 * ldw * 2 >= ((int64_t)1 << 31)) {
+    set_error("%s: size out of range", name);
+    return 1;
+  }
+  const int64_t tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  const int64_t tiles = tiles_m * tiles_n;
+  if (tiles > 0x7fffffff / 2 || flce_groups(N) > 0x7fffffff) {
+    set_error("%s: too many tiles", name);
+    return 1;
+  }
+  const unsigned grid = (unsigned)(((tiles + 7) / 8) * 8);
+  const int vec_c = (lde % 4 == 0) && aligned16(e);
+  const SmxArgs smx{target, hstats, tlogit, (int)flce_groups(N)};
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+    EG_LAUNCH((gemm_kernel<T, true, true, T, true>), dim3(grid), dim3(kThreads), 0, st,
+              (const uint16_t*)x, (const uint16_t*)w, (T*)e, (int)M, (int)N, (int)K, ldx, ldw,
+              lde, M, N, (int)tiles_m, (int)tiles, vec_c, smx);
+    return check_launch(name);
+  };
+  return dtype == EG_BF16 ? go(bf16_t{}) : go(f16_t{});
 }
 
 }  // namespace eg

@@ -413,6 +413,84 @@ __global__ __launch_bounds__(256) void zero_cols_kernel(uint16_t* __restrict__ p
 
 constexpr int64_t kFlceChunkElems = (int64_t)1 << 29;
 
+// 16-bit path: the logits product leaves, per 128-column group h of each row,
+// e = exp(logit - mx_h) in the dlogits rows, (mx_h, s_h = sum of e) and the target
+// logit (gemm_logits_softmax_launch). One workgroup per row then forms
+//   lse = M + log(sum_h s_h exp(mx_h - M)),  M = max_h mx_h (0 when infinite),
+//   rowloss = lse - logit[target] (0 on an ignored row, NaN for a target outside
+//   [0, cols)),
+//   dlogits = e * exp(mx_h - lse) - onehot(target) in place (zero on an ignored
+//   row, NaN for a bad target),
+// one read and one write of the 16-bit rows. The group factors exp(mx_h - lse)
+// sit in LDS, so a row holds at most kFixMaxGroups groups.
+constexpr int kFixBlock = 1024;
+constexpr int kFixUnroll = 4;
+constexpr int kFixMaxGroups = 8192;
+
+template <typename T>
+__global__ __launch_bounds__(kFixBlock) void flce_fixup_kernel(
+    T* __restrict__ e, int64_t lde, int cols, const float* __restrict__ hstats, int nh2,
+    const float* __restrict__ tlogit, const int64_t* __restrict__ target,
+    float* __restrict__ lse_out, float* __restrict__ rowloss, int64_t ignore_index) {
+  __shared__ float fac[kFixMaxGroups];
+  __shared__ float red[kFixBlock / kWave];
+  const int64_t row = blockIdx.x;
+  const int nh = (cols + 127) / 128;
+  const float* hs = hstats + row * (int64_t)nh2 * 2;
+  float m = -INFINITY;
+  for (int h = threadIdx.x; h < nh; h += kFixBlock) m = fmaxf(m, hs[2 * h]);
+  m = rowwise::lse_ref(block_reduce<kFixBlock>(m, MaxOp(), red));
+  float s = 0.f;
+  for (int h = threadIdx.x; h < nh; h += kFixBlock)
+    s += hs[2 * h + 1] * __builtin_amdgcn_exp2f((hs[2 * h] - m) * kLog2e);
+  s = block_reduce<kFixBlock>(s, SumOp(), red);
+  const float lse = m + logf(s);
+  const int64_t t = target[row];
+  const bool ignored = t == ignore_index;
+  const bool bad = !ignored && (t < 0 || t >= cols);
+  for (int h = threadIdx.x; h < nh; h += kFixBlock)
+    fac[h] = bad ? NAN : __builtin_amdgcn_exp2f((hs[2 * h] - lse) * kLog2e);
+  if (threadIdx.x == 0) {
+    lse_out[row] = lse;
+    rowloss[row] = ignored ? 0.f : (bad ? NAN : lse - tlogit[row]);
+  }
+  __syncthreads();
+  T* er = e + row * lde;
+  const int tc = bad || ignored ? -1 : (int)t;
+  // packs of 8 columns (8 divides 128: one group per pack)
+  const int np = cols / 8;
+  for (int p0 = threadIdx.x; p0 < np; p0 += kFixBlock * kFixUnroll) {
+    float v[kFixUnroll][8];
+#pragma unroll
+    for (int u = 0; u < kFixUnroll; ++u) {
+      const int p = p0 + u * kFixBlock;
+      if (p < np) load_vec<T, 8, true>(er + 8 * p, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kFixUnroll; ++u) {
+      const int p = p0 + u * kFixBlock;
+      if (p < np) {
+        const float f = fac[p >> 4];
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = ignored ? 0.f : v[u][i] * f;
+        const unsigned k = (unsigned)(tc - 8 * p);
+        if (k < 8u) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i == (int)k) o[i] -= 1.f;
+        }
+        store_vec<T, 8, true>(er + 8 * p, o);
+      }
+    }
+  }
+  for (int c = np * 8 + threadIdx.x; c < cols; c += kFixBlock) {
+    float o = ignored ? 0.f : to_f32(er[c]) * fac[c >> 7];
+    if (c == tc) o -= 1.f;
+    er[c] = from_f32<T>(o);
+  }
+}
+
 // Rows per chunk: as many as kFlceChunkElems logits allow, a power of two when
 // that splits the rows.
 int64_t flce_chunk_rows(int64_t rows, int64_t vocab) {
@@ -427,18 +505,34 @@ int64_t flce_chunk_rows(int64_t rows, int64_t vocab) {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
+// Whether the 16-bit path (softmax terms formed in the logits product's epilogue)
+// takes this call; fp32 inputs, and rows of more than kFixMaxGroups groups, keep fp32
+// logits chunks.
+bool flce_fused(int64_t vocab, int dtype) {
+  return dtype != EG_F32 && (vocab + 127) / 128 <= kFixMaxGroups;
+}
+
+// Workspace: [lse | rowloss] (fp32, rows each), then either one chunk of fp32 logits
+// or (16-bit path) the target logits [rows] and the group statistics of one chunk
+// [rc][flce_groups(vocab)][2], then the dlogits of every row [rows][vp].
 struct FlceLayout {
   int64_t rc, vp;
+  bool fused;
   size_t stats, logits, dl, total;
 };
 
 FlceLayout flce_layout(int64_t rows, int64_t vocab, int64_t chunk_rows, int dtype) {
   FlceLayout l;
-  l.rc = chunk_rows > 0 ? std::min(chunk_rows, rows > 0 ? rows : 1) : flce_chunk_rows(rows, vocab);
+  l.fused = flce_fused(vocab, dtype);
+  const int64_t all = rows > 0 ? rows : 1;
+  l.rc = chunk_rows > 0 ? std::min(chunk_rows, all)
+                        : (l.fused ? all : flce_chunk_rows(rows, vocab));
   l.vp = dtype == EG_F32 ? vocab : (vocab + 63) / 64 * 64;
   const size_t es = dtype == EG_F32 ? 4 : 2;
   l.stats = align_up((size_t)rows * 2 * sizeof(float));
-  l.logits = align_up((size_t)l.rc * vocab * sizeof(float));
+  l.logits = l.fused ? align_up((size_t)rows * sizeof(float)) +
+                           align_up((size_t)l.rc * flce_groups(vocab) * 2 * sizeof(float))
+                     : align_up((size_t)l.rc * vocab * sizeof(float));
   l.dl = align_up((size_t)rows * l.vp * es);
   l.total = l.stats + l.logits + l.dl;
   return l;
@@ -514,6 +608,25 @@ extern "C" int eg_flce_fwd(const void* x, const void* weight, const int64_t* tar
     for (int64_t r0 = 0; r0 < rows; r0 += L.rc) {
       const int64_t n = std::min(L.rc, rows - r0);
       const T* xc = (const T*)x + r0 * hidden;
+      if (L.fused) {
+        float* tlogit = logits;
+        float* hstats = (float*)((char*)logits + align_up((size_t)rows * sizeof(float)));
+        if (int rc = gemm_logits_softmax_launch(xc, weight, dlp + r0 * L.vp, n, vocab, hidden,
+                                                hidden, hidden, L.vp, target + r0, hstats,
+                                                tlogit + r0, dtype, st, name))
+          return rc;
+        if constexpr (!std::is_same<T, float>::value) {
+          EG_LAUNCH((flce_fixup_kernel<T>), dim3((unsigned)n), dim3(kFixBlock), 0, st,
+                    dlp + r0 * L.vp, L.vp, (int)vocab, hstats, (int)flce_groups(vocab),
+                    tlogit + r0, target + r0, lse + r0, rowloss + r0, ignore_index);
+        }
+        if (int rc = check_launch(name)) return rc;
+        if (int rc = gemm_launch(dlp + r0 * L.vp, weight, (T*)dx + r0 * hidden, n, hidden, L.vp,
+                                 L.vp, hidden, hidden, true, false, n, vocab, dtype, dtype, st,
+                                 name))
+          return rc;
+        continue;
+      }
       if (int rc = gemm_launch(xc, weight, logits, n, vocab, hidden, hidden, hidden, vocab, true,
                                true, n, vocab, dtype, EG_F32, st, name))
         return rc;

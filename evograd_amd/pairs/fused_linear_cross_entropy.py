@@ -6,10 +6,13 @@ hard-label cross entropy of ``x @ weight.T`` against ``target``, ignore_index -1
 projection and logsumexp accumulated in fp32) under the contract of
 fused_linear_cross_entropy/__init__.py:91-152: the ``[rows, vocab]`` logits are never
 materialised in full. One C entry point (``eg_flce_fwd``) runs the whole pass on
-this library's kernels: per row chunk the fp32 logits on the MFMA product
-(``gemm.hip``), their logsumexp, the row losses and the unit gradient
-``softmax - onehot`` in the input dtype, and ``dx_c = dlogits @ weight``; then
-``dweight = dlogits.T @ x`` over all rows in one product and the mean loss.
+this library's kernels: for 16-bit inputs the MFMA logits product (``gemm.hip``)
+forms the softmax terms in its epilogue (``exp(logit - group max)`` per 128-column
+group, with the group sums and the target logit, all from the fp32 accumulators),
+one pass per row turns them into the logsumexp, the row loss and the unit gradient
+``softmax - onehot`` in the input dtype, then ``dx = dlogits @ weight`` and
+``dweight = dlogits.T @ x`` and the mean loss. fp32 inputs take fp32 logits chunks
+and separate logsumexp and gradient passes.
 
 The gradient is formed in the forward because the backward's only input is the
 scalar ``dloss``: the backward (``eg_scale_copy``) scales the saved unit gradients
@@ -17,8 +20,9 @@ by ``dloss / n_valid``. The loss is fp32, as the reference's forward returns it.
 Saved state: ``(dx, dweight, n_valid)`` — the gradients in the inputs' dtypes and
 one fp32 count, nothing of size rows x vocab.
 
-Scratch (freed when the forward returns): one chunk of fp32 logits, at most
-``CHUNK_ELEMS`` of them, and the unit gradient of every row in the input dtype.
+Scratch (freed when the forward returns): the unit gradient of every row in the
+input dtype, plus the group statistics of one chunk (16-bit inputs: one chunk of
+all rows by default) or one chunk of fp32 logits (fp32 inputs: at most 2^29).
 16-bit inputs whose hidden size is not a multiple of 64 (the product's k step) are
 copied into zero-padded buffers first.
 """
@@ -41,14 +45,17 @@ from evograd_amd import _lib
 from evograd_amd.pairs._util import as_contiguous, tag, workspace
 
 IGNORE_INDEX = -100
-# Logits per chunk: 2^29 fp32 values = 2 GiB (4096 rows of Llama-3's 128256-entry
-# vocabulary); the C side uses the same bound when chunk_rows is 0.
-CHUNK_ELEMS = 1 << 29
+# Logits per chunk when set; None leaves the split to the library (chunk_rows 0):
+# one chunk for 16-bit inputs, 2^29 fp32 logits per chunk for fp32 inputs.
+CHUNK_ELEMS = None
 
 
 def chunk_rows(rows: int, vocab: int) -> int:
-    """Rows per chunk: as many as CHUNK_ELEMS allows, rounded down to a power of
-    two when that splits the rows."""
+    """Rows per chunk passed to eg_flce_fwd: 0 (the library's default) unless
+    CHUNK_ELEMS is set; then as many rows as CHUNK_ELEMS logits allow, rounded down
+    to a power of two when that splits the rows."""
+    if CHUNK_ELEMS is None:
+        return 0
     rc = max(1, min(rows, CHUNK_ELEMS // max(vocab, 1)))
     if rc < rows:
         rc = 1 << (rc.bit_length() - 1)
