@@ -26,9 +26,11 @@
 //   scale_copy_kernel dst = src * mul / div with a dtype conversion (the fused
 //                     linear cross entropy's dweight conversion and its dloss / n
 //                     scaling).
-// The fused linear cross entropy (eg_flce_fwd) runs xent_lse_kernel and the
-// backward kernels on each chunk's fp32 logits, the backward with unit scale and
-// a padded output row stride.
+// The fused linear cross entropy (eg_flce_fwd) with fp32 inputs runs
+// xent_lse_kernel and the backward kernels on each chunk's fp32 logits, the
+// backward with unit scale and a padded output row stride; with 16-bit inputs the
+// logits product forms the softmax terms itself and flce_fixup_kernel finishes
+// each row.
 // No atomics: every sum has a fixed order, so results are bitwise repeatable.
 //
 // A target outside [0, cols) that is not ignore_index makes that row's loss and
@@ -379,14 +381,17 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
 // forward_ref.py:23-35; gradients declared at fused_linear_cross_entropy/
 // __init__.py:91-152) in one launch sequence. The gradient is formed in the
 // forward (the backward only receives the scalar dloss): per row chunk,
-//   logits = x_c W^T (fp32, MFMA product, gemm.hip) -> lse and row losses
-//   (xent_lse_kernel) -> unit dlogits = softmax - onehot in the input dtype
-//   (xent_bwd_*_kernel), kept for all rows -> dx_c = dl_c W (MFMA);
-// then dW = dl^T x over all rows at once (MFMA, accumulated in registers over
-// every row, rounded once) and the mean loss. Chunks hold at most 2^29 logits
-// (2 GiB of fp32); the dlogits of all rows are kept so that dW is one product.
-// dlogits rows are padded to a multiple of 64 columns with zeros, the product's
-// k step. No atomics: bitwise repeatable.
+//   16-bit inputs: the logits product x_c W^T (MFMA, gemm.hip) with the softmax
+//   epilogue writes exp(logit - group max) into the dlogits rows, the group
+//   statistics and the target logits -> flce_fixup_kernel forms lse, the row
+//   losses and unit dlogits = softmax - onehot in place (one chunk of all rows by
+//   default: no fp32 logits are held);
+//   fp32 inputs: logits = x_c W^T (fp32) -> lse and row losses (xent_lse_kernel)
+//   -> unit dlogits (xent_bwd_*_kernel), chunks of at most 2^29 logits;
+// then dx_c = dl_c W (MFMA), dW = dl^T x over all rows at once (MFMA, accumulated
+// in registers over every row, rounded once) and the mean loss. The dlogits of all
+// rows are kept so that dW is one product; their rows are padded to a multiple of
+// 64 columns with zeros, the product's k step. No atomics: bitwise repeatable.
 
 namespace eg {
 namespace {

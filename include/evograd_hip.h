@@ -281,7 +281,10 @@ int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* los
  * (src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35) and
  * forms its gradient (declared at fused_linear_cross_entropy/__init__.py:91-152)
  * in the same pass, every product on this library's MFMA kernels:
- *   logits = x @ weight.T (fp32, in row chunks of at most 2^29 logits)
+ *   logits = x @ weight.T (fp32 accumulation; 16-bit inputs: the softmax terms are
+ *            formed in the product's epilogue and no fp32 logits are stored, one
+ *            chunk of all rows by default; fp32 inputs: fp32 logits in row chunks of
+ *            at most 2^29)
  *   loss = mean over rows with target != ignore_index of lse - logits[target] (fp32)
  *   dl = softmax(logits) - onehot(target) (dtype; zero on ignored rows)
  *   dx = dl @ weight, dweight = dl.T @ x   (dtype: the unit gradients)
@@ -290,8 +293,9 @@ int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* los
  * target int64 [rows]; a target outside [0, vocab) that is not ignore_index
  * gives NaN. 16-bit inputs need hidden % 64 == 0. The backward scales dx and
  * dweight by dloss / n_valid (eg_scale_copy). chunk_rows <= 0 takes the default
- * chunking; the workspace (eg_flce_workspace_bytes, same chunk_rows) holds the
- * fp32 logits of one chunk and the dlogits of every row. */
+ * chunking; the workspace (eg_flce_workspace_bytes, same chunk_rows and dtype) holds
+ * the dlogits of every row and either the softmax group statistics of one chunk
+ * (16-bit) or the fp32 logits of one chunk (fp32). */
 size_t eg_flce_workspace_bytes(int64_t rows, int64_t hidden, int64_t vocab, int64_t chunk_rows,
                                int dtype);
 int eg_flce_fwd(const void* x, const void* weight, const int64_t* target, float* loss, void* dx,
