@@ -14,12 +14,17 @@
 // 32 x 32 accumulator tiles, 256 fp32 registers per lane, held in AGPRs at one
 // wave per SIMD). Per 64-deep k step a workgroup stages a 256 x 64 slice of each
 // operand in LDS (32 KB each, double-buffered: 128 KB), filled by direct
-// buffer->LDS loads (16 bytes per lane, no VGPR staging) issued one step ahead.
-// Each wave's 16 loads of the next slice are spread over the first 32 (both
-// operands K-contiguous) or 40 of the step's 64 MFMAs: a load instruction holds
-// the wave's issue for several cycles, and issued as one block before the MFMAs
-// they left the matrix unit idle (measured at the benchmark sizes: logits
-// 44.6 -> 49.0%, dx 44.8 -> 52.8%, dweight 42.2 -> 48.7% of bf16 peak).
+// buffer->LDS loads (16 bytes per lane, no VGPR staging) issued about one step
+// ahead. A step's one barrier sits before its last substep: the wave waits for its
+// own loads of the next slice and for its reads of the current one, then issues,
+// among the last 16 MFMAs, the A loads of the slice after next into the buffer
+// just released and the reads for the next step's first substep; the next
+// slice's B loads follow every second MFMA of an earlier substep. A load
+// instruction holds the wave's issue for several cycles: issued as one block
+// before the MFMAs they left the matrix unit idle (measured at the benchmark
+// sizes, logits 44.6 -> 49.0%, dx 44.8 -> 52.8%, dweight 42.2 -> 48.7% of bf16
+// peak), and the barrier before the last substep takes the LDS read latency out
+// of the step boundary (a further 1-5%).
 // Operands reach the MFMA v_mfma_f32_32x32x16_{bf16,f16} (lane l: row/column
 // l%32, k = 8(l/32) .. +7) as
 //   K-contiguous slice [256][64]: one ds_read_b128 per operand, 16-byte chunks
@@ -207,8 +212,10 @@ __device__ __forceinline__ float acc_read(float x) {
   return r;
 }
 
-// MFMAs of one k step over which a wave's 16 slice loads are spread.
-template <bool AKC, bool BKC> struct LoadSpread { static constexpr int value = AKC && BKC ? 32 : 40; };
+// Substep of a k step that carries the B loads of the next slice (the A loads
+// follow the step's barrier, in substep 3): measured at the benchmark sizes,
+// substep 1 suits the product with both operands K-major, substep 0 the others.
+template <bool AKC, bool BKC> struct LoadSpread { static constexpr int b_substep = !AKC && !BKC ? 1 : 0; };
 
 template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -236,16 +243,9 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
   const int nk = (K + kBK - 1) / kBK;
   // The k loop runs an even number of steps (two per iteration, one per buffer). A
-  // slice at or past nk loads through an empty range: the step past K, when nk is
-  // odd, adds zeros, and the load issued in the last step fills nothing.
+  // slice at or past nk loads through an empty buffer range, which fills its LDS
+  // slots with zeros: the step past K, when nk is odd, adds zeros.
   const int nk2 = nk + (nk & 1);
-  auto load = [&](int kt, uint16_t* as, uint16_t* bs) {
-    const int k0 = kt * kBK;
-    const int64_t oa = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
-    const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
-    la.load(A + oa, kt < nk ? (a_end - oa) * 2 : 0, as);
-    lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
-  };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -253,64 +253,97 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  // One k step on the slices in (as, bs): the operands of substep s + 1 are read
-  // while the 16 MFMAs of substep s run; `issue` emits the next slice's loads.
+  // Operand registers ping-pong over the substeps of every step: substep s of a
+  // step computes from set s & 1 while set (s + 1) & 1 is read, and the reads for
+  // the next step's substep 0 are issued during substep 3, after the step's
+  // barrier, so no step starts by waiting for LDS reads.
   OperandReader<AKC> ra;
   OperandReader<BKC> rb;
   ra.init(wm, lane);
   rb.init(wn, lane);
   // LDS read instructions per substep (a K-major operand takes two per block).
   constexpr int NR = 4 * (AKC ? 1 : 2) + 4 * (BKC ? 1 : 2);
-  constexpr int DS = LoadSpread<AKC, BKC>::value;
-  auto compute = [&](const uint16_t* as, const uint16_t* bs, auto&& issue) {
-    v8 a[2][4], b[2][4];
+  // substep that carries the B loads of the next slice
+  constexpr int QB = LoadSpread<AKC, BKC>::b_substep;
+  v8 a[2][4], b[2][4];
+  auto rd = [&](int set, const uint16_t* as, const uint16_t* bs, int s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[set][i] = ra.template read<v8>(as, i, s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[set][j] = rb.template read<v8>(bs, j, s);
+  };
+  auto mma16 = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = GM<T>::mma(b[set][j], a[set][i], acc[i][j]);
+  };
+  // A barrier without a memory fence: the waits before it are explicit, and the
+  // fence of __syncthreads() would also wait for the slice loads in flight.
+  auto bar = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto loadA = [&](int kt, uint16_t* as) {
+    const int k0 = kt * kBK;
+    const int64_t oa = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
+    la.load(A + oa, kt < nk ? (a_end - oa) * 2 : 0, as);
+  };
+  auto loadB = [&](int kt, uint16_t* bs) {
+    const int k0 = kt * kBK;
+    const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
+    lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
+  };
+  loadA(0, As0);
+  loadB(0, Bs0);
+  loadA(1, As1);
+  __builtin_amdgcn_s_waitcnt(0xF78);  // vmcnt(8): slice 0 has landed
+  bar();
+  rd(0, As0, Bs0, 0);
+  // Step kt on buffer (as, bs): substeps 0-2 with the B loads of slice kt + 1 (into
+  // the other buffer) spread over the MFMAs of substep QB; the wait for this wave's
+  // loads of slice kt + 1 and for the reads of substep 3; the barrier (slice kt + 1
+  // complete, every wave done reading this buffer); substep 3 with the A loads of
+  // slice kt + 2 into this buffer and the reads of the next step's substep 0. Each
+  // load slot follows every second MFMA.
+  auto step = [&](auto bufc, int kt) {
+    constexpr bool odd = decltype(bufc)::value;
+    uint16_t* as = odd ? As1 : As0;
+    uint16_t* bs = odd ? Bs1 : Bs0;
+    uint16_t* an = odd ? As0 : As1;
+    uint16_t* bn = odd ? Bs0 : Bs1;
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (QB == 0) loadB(kt + 1, bn);
+    rd(1, as, bs, 1);
+    mma16(0);
+    if constexpr (QB == 1) loadB(kt + 1, bn);
+    rd(0, as, bs, 2);
+    mma16(1);
+    rd(1, as, bs, 3);
+    mma16(0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[0][i] = ra.template read<v8>(as, i, 0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[0][j] = rb.template read<v8>(bs, j, 0);
-    issue();
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      const int cur = s & 1;
-      if (s + 1 < kBK / 16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[cur ^ 1][i] = ra.template read<v8>(as, i, s + 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[cur ^ 1][j] = rb.template read<v8>(bs, j, s + 1);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = GM<T>::mma(b[cur][j], a[cur][i], acc[i][j]);
-    }
-    // Schedule: the reads of substep 0, then the 64 MFMAs with the 16 slice loads
-    // spread over the first DS of them and the NR reads of each next substep over
-    // the 16 MFMAs of the current one.
-    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s)
+    for (int s = 0; s < 3; ++s)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        const int qq = s * 16 + q;
-        // DS >= 16: at most one load after each MFMA
-        if (qq < DS && ((qq + 1) * 16) / DS != (qq * 16) / DS)
-          __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+        if (s == QB && (q & 1)) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
         // NR <= 16: at most one read after each MFMA
-        if (s + 1 < kBK / 16 && ((q + 1) * NR) / 16 != (q * NR) / 16)
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (((q + 1) * NR) / 16 != (q * NR) / 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     __builtin_amdgcn_sched_barrier(0);
-  };
-
-  load(0, As0, Bs0);
-  auto step = [&](auto bufc, int kt) {
-    constexpr bool odd = decltype(bufc)::value;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    compute(odd ? As1 : As0, odd ? Bs1 : Bs0,
-            [&] { load(kt + 1, odd ? As0 : As1, odd ? Bs0 : Bs1); });
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    bar();
+    loadA(kt + 2, as);
+    rd(0, an, bn, 0);
+    mma16(1);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (q & 1) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+      if (((q + 1) * NR) / 16 != (q * NR) / 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   };
   for (int kt = 0; kt < nk2; kt += 2) {
     step(std::false_type{}, kt);
