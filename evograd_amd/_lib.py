@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_abi_version": (_i32, []),
     "eg_last_error": (ctypes.c_char_p, []),
     "eg_time_kernel": (_i32, [_p, _p, _i32]),
+    "eg_time_kernel_missed": (_i32, []),
     "eg_softmax_fwd": (_i32, [_p, _p, _i64, _i64, _i32, _p]),
     "eg_softmax_bwd": (_i32, [_p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_rmsnorm_fwd": (_i32, [_p, _p, _p, _p, _i64, _i64, _f32, _i32, _p]),

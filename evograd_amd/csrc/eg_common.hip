@@ -7,8 +7,9 @@ namespace eg {
 
 static thread_local char g_error[1024] = "";
 
-// Kernel-timing hook: eg_time_kernel arms the next entry-point call on this
-// thread; that call's `index`-th kernel launch records `start` and `stop`.
+// Kernel-timing hook: eg_time_kernel arms this thread's launches from the next
+// entry-point call on; the `index`-th of them (counted across calls) records
+// `start` and `stop`.
 struct TimingArm {
   hipEvent_t start = nullptr, stop = nullptr;
   int index = 0;
@@ -38,9 +39,11 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() {
   g_error[0] = '\0';
-  g_arm.active = g_arm.pending;
-  g_arm.pending = false;
-  g_arm.next = 0;
+  if (g_arm.pending) {  // a fresh arm starts counting at this call
+    g_arm.active = true;
+    g_arm.pending = false;
+    g_arm.next = 0;
+  }
 }
 
 int check_launch(const char* what) {
@@ -68,6 +71,13 @@ int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what) {
 }
 
 }  // namespace eg
+
+extern "C" int eg_time_kernel_missed(void) {
+  const int missed = (eg::g_arm.pending || eg::g_arm.active) ? 1 : 0;
+  eg::g_arm.pending = false;
+  eg::g_arm.active = false;
+  return missed;
+}
 
 extern "C" int eg_abi_version(void) { return 1; }
 

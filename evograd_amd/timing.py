@@ -52,10 +52,13 @@ class KernelTimer:
                 raise RuntimeError(f"hipEventCreate failed ({rc})")
 
     def arm(self, index: int) -> None:
-        """Time kernel number ``index`` of the next library call on this thread."""
+        """Time kernel number ``index`` of this thread's launches, counted from the
+        next library call on (across the calls that follow it)."""
         _lib.call("eg_time_kernel", self.start, self.stop, int(index))
 
     def elapsed_ms(self) -> float:
+        if _lib.query("eg_time_kernel_missed"):
+            raise RuntimeError("the armed kernel launch did not run")
         h = _runtime()
         rc = h.hipEventSynchronize(self.stop)
         if rc != 0:

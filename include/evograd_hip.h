@@ -48,13 +48,18 @@ const char* eg_last_error(void);
 
 /* Measurement hook; no counterpart in the reference (its harness times with
  * torch.cuda.Event around whole calls, src/evograd/bench/harness.py:173-213).
- * Arms the next entry-point call on the calling thread: its `index`-th kernel
- * launch (0-based, in launch order) is made with hipExtLaunchKernelGGL so the
- * dispatch records `start_event` / `stop_event` (hipEvent_t, created with
- * timing) at that kernel's start and end. The arm is consumed by that one call
- * whether or not it reaches the index. For callers that time one kernel of a
- * multi-kernel entry point (bench.py); results are unchanged. */
+ * Arms the calling thread's next kernel launches: the `index`-th launch (0-based,
+ * in launch order, counted from the next entry-point call on and across the calls
+ * that follow it) is made with hipExtLaunchKernelGGL so the dispatch records
+ * `start_event` / `stop_event` (hipEvent_t, created with timing) at that kernel's
+ * start and end. The arm lasts until that launch or the next eg_time_kernel. For
+ * callers that time one kernel of a multi-kernel entry point or of a short
+ * sequence of calls (bench.py); results are unchanged. */
 int eg_time_kernel(void* start_event, void* stop_event, int index);
+
+/* 1 when the launch armed by eg_time_kernel has not run yet (its events hold
+ * nothing of this arm), 0 when it has; drops the arm either way. */
+int eg_time_kernel_missed(void);
 
 /* ---------------------------------------------------------------- softmax
  * Replaces softmax_forward_ref (src/evograd/ops/level1/softmax/forward_ref.py:6-7):
