@@ -319,58 +319,83 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_wave(const T* __restrict__ x,
   if (lane == 0) rstd_out[row] = rs;
 }
 
-// RMSNorm forward, one workgroup of BLOCK threads per row of IT x BLOCK packs
-// (4096 bf16 columns at (256, 2)); ADD: the normalised row is s = x + r. At bf16
-// [16384, 4096] the plain RMSNorm measures 46.7 us against 48.5 us for the
-// one-wave kernel (medians of twelve interleaved rounds).
-template <typename T, int VEC, int IT, int BLOCK, bool ADD = false>
+// RMSNorm forward, RPW rows per workgroup of BLOCK threads, each row IT x BLOCK
+// packs (4096 bf16 columns at (512, 1)), every thread holding its packs of each of
+// the RPW rows; ADD: the normalised row is s = x + r. All loads are issued first
+// (rows past the end read the last row again and are not stored), the RPW rows'
+// reductions share one barrier. At bf16 [16384, 4096], interleaved: 47.5 us for one
+// row per 256-thread workgroup, 46.4 us for two rows per 512-thread workgroup.
+template <typename T, int VEC, int IT, int BLOCK, int RPW, bool ADD = false>
 __global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_row(const T* __restrict__ x,
                                                          const T* __restrict__ r,
                                                          const T* __restrict__ w,
                                                          T* __restrict__ y,
                                                          float* __restrict__ rstd_out,
-                                                         float eps) {
+                                                         int64_t rows, float eps) {
   constexpr int NW = BLOCK / kWave;
   constexpr int H = IT * BLOCK * VEC;
-  __shared__ float red[NW];
+  __shared__ float red[RPW][NW];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  const int64_t row = blockIdx.x;
-  Pack<T, VEC> xp[IT], rp[ADD ? IT : 1];
+  const int64_t row0 = (int64_t)blockIdx.x * RPW;
+  Pack<T, VEC> xp[RPW][IT], rp[ADD ? RPW : 1][ADD ? IT : 1];
 #pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int64_t off = row * H + (it * BLOCK + (int)threadIdx.x) * VEC;
-    xp[it] = ld_raw<T, VEC>(x + off);
-    if (ADD) rp[ADD ? it : 0] = ld_raw<T, VEC>(r + off);
-  }
-  float sv[IT][VEC];
-  float q = 0.f;
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int64_t rc = row0 + rr < rows ? row0 + rr : rows - 1;
 #pragma unroll
-  for (int it = 0; it < IT; ++it)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      float v = to_f32(xp[it].v[i]);
-      if (ADD) v += to_f32(rp[ADD ? it : 0].v[i]);
-      sv[it][i] = v;
-      q += v * v;
+    for (int it = 0; it < IT; ++it) {
+      const int64_t off = rc * H + (it * BLOCK + (int)threadIdx.x) * VEC;
+      xp[rr][it] = ld_raw<T, VEC>(x + off);
+      if (ADD) rp[ADD ? rr : 0][ADD ? it : 0] = ld_raw<T, VEC>(r + off);
     }
-  q = wave_reduce(q, SumOp());
-  if (lane == 0) red[wid] = q;
-  __syncthreads();
-  float u = red[0];
+  }
+  float sv[RPW][IT][VEC];
+  float q[RPW];
 #pragma unroll
-  for (int k = 1; k < NW; ++k) u += red[k];
-  const float rs = rsqrtf(u / (float)H + eps);
-  T* yr = y + row * H;
+  for (int rr = 0; rr < RPW; ++rr) {
+    q[rr] = 0.f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float v = to_f32(xp[rr][it].v[i]);
+        if (ADD) v += to_f32(rp[ADD ? rr : 0][ADD ? it : 0].v[i]);
+        sv[rr][it][i] = v;
+        q[rr] += v * v;
+      }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) q[rr] += __shfl_xor(q[rr], off, kWave);
+  if (lane == 0) {
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) red[rr][wid] = q[rr];
+  }
+  __syncthreads();
+  float rs[RPW];
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    float u = red[rr][0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) u += red[rr][k];
+    rs[rr] = rsqrtf(u / (float)H + eps);
+  }
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
     const Pack<T, VEC> wp = *reinterpret_cast<const Pack<T, VEC>*>(w + c);
-    float o[VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) o[i] = (sv[it][i] * rs) * to_f32(wp.v[i]);
-    st_vec<T, VEC>(yr + c, o);
+    for (int rr = 0; rr < RPW; ++rr) {
+      if (row0 + rr >= rows) continue;
+      float o[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) o[i] = (sv[rr][it][i] * rs[rr]) * to_f32(wp.v[i]);
+      st_vec<T, VEC>(y + (row0 + rr) * H + c, o);
+    }
   }
-  if (threadIdx.x == 0) rstd_out[row] = rs;
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr)
+    if (threadIdx.x == rr && row0 + rr < rows) rstd_out[row0 + rr] = rs[rr];
 }
 
 // LayerNorm forward, one wave per row (rows of ITEMS x 64 lanes x VEC elements):
@@ -428,74 +453,108 @@ __global__ __launch_bounds__(256) void layernorm_fwd_wave(const T* __restrict__ 
   }
 }
 
-// LayerNorm forward, one workgroup of BLOCK threads per row of IT x BLOCK packs
-// (4096 bf16 or 2048 fp32 columns at (256, 2)): mean, then the centred sum of
-// squares, each a wave butterfly plus one LDS exchange. At bf16 [16384, 4096] it
-// measures 48.7 us against 50.2 us for the one-wave kernel (medians of twelve
-// interleaved rounds).
-template <typename T, int VEC, int IT, int BLOCK>
+// LayerNorm forward, RPW rows per workgroup of BLOCK threads, each row IT x BLOCK
+// packs (4096 bf16 columns at (512, 1)): mean, then the centred sum of squares,
+// each a wave butterfly plus one LDS exchange, shared by the RPW rows (rows past the
+// end read the last row again and are not stored). At bf16 [16384, 4096],
+// interleaved: 49.5 us for one row per 256-thread workgroup, 50.2 us for one row per
+// wave, 47.6 us for two rows per 512-thread workgroup.
+template <typename T, int VEC, int IT, int BLOCK, int RPW>
 __global__ __launch_bounds__(BLOCK) void layernorm_fwd_row(const T* __restrict__ x,
                                                            const T* __restrict__ w,
                                                            const T* __restrict__ b,
                                                            T* __restrict__ y,
                                                            float* __restrict__ mean_out,
                                                            float* __restrict__ rstd_out,
-                                                           float eps) {
+                                                           int64_t rows, float eps) {
   constexpr int NW = BLOCK / kWave;
   constexpr int H = IT * BLOCK * VEC;
-  __shared__ float red[2][NW];
+  __shared__ float red[2][RPW][NW];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-  const int64_t row = blockIdx.x;
-  const T* xr = x + row * H;
-  Pack<T, VEC> xp[IT];
+  const int64_t row0 = (int64_t)blockIdx.x * RPW;
+  Pack<T, VEC> xp[RPW][IT];
 #pragma unroll
-  for (int it = 0; it < IT; ++it) xp[it] = ld_raw<T, VEC>(xr + (it * BLOCK + (int)threadIdx.x) * VEC);
-  float sv[IT][VEC];
-  float s = 0.f;
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int64_t rc = row0 + rr < rows ? row0 + rr : rows - 1;
 #pragma unroll
-  for (int it = 0; it < IT; ++it)
+    for (int it = 0; it < IT; ++it)
+      xp[rr][it] = ld_raw<T, VEC>(x + rc * H + (it * BLOCK + (int)threadIdx.x) * VEC);
+  }
+  float sv[RPW][IT][VEC];
+  float s[RPW];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      sv[it][i] = to_f32(xp[it].v[i]);
-      s += sv[it][i];
-    }
-  s = wave_reduce(s, SumOp());
-  if (lane == 0) red[0][wid] = s;
+  for (int rr = 0; rr < RPW; ++rr) {
+    s[rr] = 0.f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        sv[rr][it][i] = to_f32(xp[rr][it].v[i]);
+        s[rr] += sv[rr][it][i];
+      }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) s[rr] += __shfl_xor(s[rr], off, kWave);
+  if (lane == 0) {
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) red[0][rr][wid] = s[rr];
+  }
   __syncthreads();
-  float t = red[0][0];
+  float mean[RPW], q[RPW];
 #pragma unroll
-  for (int k = 1; k < NW; ++k) t += red[0][k];
-  const float mean = t * (1.0f / (float)H);
-  float q = 0.f;
+  for (int rr = 0; rr < RPW; ++rr) {
+    float t = red[0][rr][0];
 #pragma unroll
-  for (int it = 0; it < IT; ++it)
+    for (int k = 1; k < NW; ++k) t += red[0][rr][k];
+    mean[rr] = t * (1.0f / (float)H);
+    q[rr] = 0.f;
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      sv[it][i] -= mean;
-      q += sv[it][i] * sv[it][i];
-    }
-  q = wave_reduce(q, SumOp());
-  if (lane == 0) red[1][wid] = q;
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        sv[rr][it][i] -= mean[rr];
+        q[rr] += sv[rr][it][i] * sv[rr][it][i];
+      }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) q[rr] += __shfl_xor(q[rr], off, kWave);
+  if (lane == 0) {
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) red[1][rr][wid] = q[rr];
+  }
   __syncthreads();
-  float u = red[1][0];
+  float rs[RPW];
 #pragma unroll
-  for (int k = 1; k < NW; ++k) u += red[1][k];
-  const float rs = rsqrtf(u * (1.0f / (float)H) + eps);
-  T* yr = y + row * H;
+  for (int rr = 0; rr < RPW; ++rr) {
+    float u = red[1][rr][0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) u += red[1][rr][k];
+    rs[rr] = rsqrtf(u * (1.0f / (float)H) + eps);
+  }
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int c = (it * BLOCK + (int)threadIdx.x) * VEC;
     const Pack<T, VEC> wp = *reinterpret_cast<const Pack<T, VEC>*>(w + c);
     const Pack<T, VEC> bp = *reinterpret_cast<const Pack<T, VEC>*>(b + c);
-    float o[VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) o[i] = (sv[it][i] * rs) * to_f32(wp.v[i]) + to_f32(bp.v[i]);
-    st_vec<T, VEC>(yr + c, o);
+    for (int rr = 0; rr < RPW; ++rr) {
+      if (row0 + rr >= rows) continue;
+      float o[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) o[i] = (sv[rr][it][i] * rs[rr]) * to_f32(wp.v[i]) + to_f32(bp.v[i]);
+      st_vec<T, VEC>(y + (row0 + rr) * H + c, o);
+    }
   }
-  if (threadIdx.x == 0) {
-    rstd_out[row] = rs;
-    mean_out[row] = mean;
-  }
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr)
+    if (threadIdx.x == rr && row0 + rr < rows) {
+      rstd_out[row0 + rr] = rs[rr];
+      mean_out[row0 + rr] = mean[rr];
+    }
 }
 
 // -------------------------------------------------------------- backward
@@ -910,8 +969,14 @@ static int rms_fwd_impl(const char* name, const void* x, const void* r, const vo
         case 1: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 1, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
         case 2: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 2, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
         case 4: EG_LAUNCH((rmsnorm_fwd_wave<T, V, 4, ADD>), dim3(grid), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps); break;
-        // rows of 512 packs: a 256-thread workgroup per row
-        default: EG_LAUNCH((rmsnorm_fwd_row<T, V, 2, 256, ADD>), dim3((unsigned)rows), dim3(256), 0, st, xp, rp, wp, yp, rstd, eps); break;
+        // rows of 512 packs: two rows per 512-thread workgroup (ADD: one row per 256
+        // threads, the configuration its residual loads were measured at)
+        default:
+          if (ADD)
+            EG_LAUNCH((rmsnorm_fwd_row<T, V, 2, 256, 1, ADD>), dim3((unsigned)rows), dim3(256), 0, st, xp, rp, wp, yp, rstd, rows, eps);
+          else
+            EG_LAUNCH((rmsnorm_fwd_row<T, V, 1, 512, 2, ADD>), dim3((unsigned)((rows + 1) / 2)), dim3(512), 0, st, xp, rp, wp, yp, rstd, rows, eps);
+          break;
       }
     } else if (vec) {
       FwdRing<T, V, false, ADD> f{xp, rp, wp, nullptr, yp, nullptr, rstd, rows, h, eps, st};
@@ -1023,8 +1088,8 @@ extern "C" int eg_layernorm_fwd(const void* x, const void* weight, const void* b
         case 1: EG_LAUNCH((layernorm_fwd_wave<T, V, 1>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
         case 2: EG_LAUNCH((layernorm_fwd_wave<T, V, 2>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
         case 4: EG_LAUNCH((layernorm_fwd_wave<T, V, 4>), dim3(grid), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
-        // rows of 512 packs: a 256-thread workgroup per row
-        default: EG_LAUNCH((layernorm_fwd_row<T, V, 2, 256>), dim3((unsigned)rows), dim3(256), 0, st, xp, wp, bp, yp, mean, rstd, eps); break;
+        // rows of 512 packs: two rows per 512-thread workgroup
+        default: EG_LAUNCH((layernorm_fwd_row<T, V, 1, 512, 2>), dim3((unsigned)((rows + 1) / 2)), dim3(512), 0, st, xp, wp, bp, yp, mean, rstd, rows, eps); break;
       }
     } else if (vec) {
       FwdRing<T, V, true> f{(const T*)x, nullptr, (const T*)weight, (const T*)bias, (T*)y, mean, rstd, rows, h, eps, st};
