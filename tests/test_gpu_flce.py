@@ -132,3 +132,64 @@ def test_flce_with_no_counted_row_has_zero_gradients(rows):
     assert dx.shape == x.shape and dw.shape == wt.shape
     assert torch.equal(dx.float().cpu(), rgx) and torch.equal(dw.float().cpu(), rgw)
     assert not torch.isnan(dw).any().item() and int(torch.count_nonzero(dw)) == 0
+
+
+def _torch_ref32(x, wt, target):
+    xr = x.float().requires_grad_(True)
+    wr = wt.float().requires_grad_(True)
+    loss = torch.nn.functional.cross_entropy(xr @ wr.t(), target, ignore_index=-100)
+    gx, gw = torch.autograd.grad(loss, (xr, wr))
+    return loss.detach(), gx, gw
+
+
+def test_flce_target_out_of_range_gives_nan_row():
+    """A target outside [0, vocab) that is not ignore_index: the loss is NaN (torch
+    raises there) and so is that row's gradient; the other rows of dx stay finite."""
+    mod = pair_module("fused_linear_cross_entropy")
+    _note("bad target")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(40, 128, device="cuda", dtype=torch.bfloat16, generator=g)
+    wt = torch.randn(1000, 128, device="cuda", dtype=torch.bfloat16, generator=g)
+    target = torch.randint(0, 1000, (40,), device="cuda", generator=g)
+    target[7] = 1000
+    loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(x, wt, target)
+    dx, _ = mod.fused_linear_cross_entropy_backward_from_saved(
+        torch.ones((), device="cuda", dtype=torch.float32), saved)
+    torch.cuda.synchronize()
+    assert torch.isnan(loss).item()
+    assert torch.isnan(dx[7].float()).all().item()
+    others = torch.cat([dx[:7], dx[8:]]).float()
+    assert torch.isfinite(others).all().item()
+
+
+def test_flce_vocab_past_the_fused_limit_takes_the_fp32_path():
+    """16-bit inputs whose rows hold more than 8192 softmax groups (vocab > 2^20)
+    run the fp32-logits chunk path; both paths must agree with torch."""
+    mod = pair_module("fused_linear_cross_entropy")
+    vocab = (1 << 20) + 128
+    _note("vocab", vocab)
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x = torch.randn(4, 64, device="cuda", dtype=torch.bfloat16, generator=g)
+    wt = (0.25 * torch.randn(vocab, 64, device="cuda", generator=g)).bfloat16()
+    target = torch.tensor([3, vocab - 1, -100, 1 << 19], device="cuda")
+    loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(x, wt, target)
+    dloss = torch.full((), 2.0, device="cuda", dtype=torch.float32)
+    dx, dw = mod.fused_linear_cross_entropy_backward_from_saved(dloss, saved)
+    ref_loss, rgx, rgw = _torch_ref32(x, wt, target)
+    torch.cuda.synchronize()
+    assert abs(float(loss) - float(ref_loss)) <= 1e-4 * abs(float(ref_loss))
+    # The unit gradient is rounded to bf16 before the products and the results are
+    # rounded twice more (before and after the dloss / n scaling): each entry is
+    # held to 2^-6 of the sum of the absolute terms of its dot product, which
+    # covers that rounding also where the terms cancel (most of the 2^20 columns).
+    logits = x.float() @ wt.float().t()
+    dl = torch.softmax(logits, dim=1)
+    keep = target != -100
+    dl[keep, target[keep]] -= 1.0
+    dl = dl * keep[:, None] * (2.0 / float(keep.sum()))
+    bound_x = 2.0 ** -6 * (dl.abs() @ wt.float().abs())
+    bound_w = 2.0 ** -6 * (dl.abs().t() @ x.float().abs())
+    assert bool(((dx.float() - 2.0 * rgx).abs() <= bound_x + 1e-12).all())
+    assert bool(((dw.float() - 2.0 * rgw).abs() <= bound_w + 1e-12).all())
+    del wt, dw, rgw, dl, bound_w, logits
+    torch.cuda.empty_cache()
