@@ -1,4 +1,4 @@
-"""Parity of the fused linear cross-entropy pair (library GEMMs + HIP chunk kernels).
+"""Parity of the fused linear cross-entropy pair (this library's MFMA products and row kernels).
 
 The declaration's cases run the reference's gate (oracle: fp32 logits, autograd).
 Beyond it: the chunked result equals the single-chunk one and an fp64 evaluation
@@ -82,6 +82,35 @@ def test_flce_chunked_equals_single_chunk_and_fp64():
     assert torch.allclose(one[1].float(), many[1].float(), rtol=2 ** -7, atol=1e-7)
     # saved state: the two gradients and one count, nothing rows x vocab
     assert [tuple(t.shape) for t in many_saved] == [(300, 256), (4096, 256), (1,)]
+
+
+@pytest.mark.parametrize("dtype,hidden", [("bfloat16", 100), ("float16", 200)])
+def test_flce_hidden_not_a_multiple_of_the_k_step(dtype, hidden):
+    """16-bit inputs whose hidden size is not a multiple of 64 go through zero-padded
+    copies; the padding adds nothing to the logits and is cut from dx."""
+    mod = pair_module("fused_linear_cross_entropy")
+    w = Workload(dims=dict(rows=77, hidden=hidden, vocab=1000), dtype=dtype,
+                 extra={"ignore_every": 5})
+    _note("odd hidden", w.dims, dtype)
+    inp = make_case_inputs(OP, w, "cuda")
+    loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(
+        inp["x"], inp["weight"], inp["target"])
+    dx, dw = mod.fused_linear_cross_entropy_backward_from_saved(inp["dloss"], saved)
+    torch.cuda.synchronize()
+    assert dx.shape == inp["x"].shape and dw.shape == inp["weight"].shape
+    ref_loss, ref_dx, ref_dw = _ref64(inp)
+    assert abs(float(loss) - float(ref_loss)) <= 1e-5 * abs(float(ref_loss))
+    # each entry within 2^-6 of the sum of the absolute terms of its dot product
+    # (the unit gradient rounded to 16 bits, the results rounded twice more)
+    x, wt, target = inp["x"].double(), inp["weight"].double(), inp["target"]
+    dl = torch.softmax(x @ wt.t(), dim=1)
+    keep = target != -100
+    dl[keep, target[keep]] -= 1.0
+    dl = dl * keep[:, None] * (float(inp["dloss"]) / float(keep.sum()))
+    bound_x = 2.0 ** -6 * (dl.abs() @ wt.abs())
+    bound_w = 2.0 ** -6 * (dl.abs().t() @ x.abs())
+    assert bool(((dx.double() - ref_dx).abs() <= bound_x + 1e-12).all())
+    assert bool(((dw.double() - ref_dw).abs() <= bound_w + 1e-12).all())
 
 
 def test_flce_through_autograd_binding():
