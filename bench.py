@@ -19,10 +19,18 @@ and medians are reported.
 The CPU baseline is the reference's eager PyTorch autograd path (the oracle
 package's restated forwards, fused ``F.rms_norm``/``F.layer_norm`` where the
 reference declares a runtime forward, ``F.scaled_dot_product_attention`` for
-attention) on a bounded row/head sample of the same workload, timed on this
-host's cores and scaled linearly to the full workload.
+attention) timed on this host's cores: the whole workload for the memory-bound
+operators, a bounded head/row sample scaled to the full workload for attention
+and the fused linear cross entropy, and the T=1024 layer scaled by model FLOPs
+for the larger layers.
+
+The decoder layer (``llama3_decoder_layer``) is timed at the reference's grid, B=1 and
+T in {1024, 2048, 4096} at Llama-3-8B widths, with its MFMA fraction over the
+layer's model FLOPs. ``sweeps`` holds the memory-bound operators over the
+reference's token sweeps (src/evograd/opdecl/models.py:286, :293).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--ops a,b] [--no-cpu]
+                       [--no-sweep]
 """
 
 from __future__ import annotations
@@ -43,9 +51,25 @@ METRIC = "fwd+bwd step latency (us) + % HBM/MFMA roofline per op; saved bytes vs
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/CU/clk
 HEADLINE = "rmsnorm"
+LAYER = "llama3_decoder_layer"
 ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attention",
            "fused_add_rms_norm", "causal_attention_gqa", "llama3_attention", "cross_entropy",
-           "fused_linear_cross_entropy", "softmax@vocab")
+           "fused_linear_cross_entropy", "softmax@vocab", f"{LAYER}@llama3_8b_T1024",
+           f"{LAYER}@llama3_8b_T2048", f"{LAYER}@llama3_8b_T4096")
+# The reference's timed token sweeps (src/evograd/opdecl/models.py:286, :293): the
+# residual-stream and MLP operators over LLAMA_TOKEN_SWEEP, the vocabulary-width
+# ones over LLAMA_VOCAB_TOKEN_SWEEP.
+LLAMA_TOKEN_SWEEP = (1024, 2048, 4096, 8192, 16384)
+LLAMA_VOCAB_TOKEN_SWEEP = (512, 1024, 2048, 4096, 8192)
+SWEEP_OPS = {
+    "rmsnorm": LLAMA_TOKEN_SWEEP, "layernorm": LLAMA_TOKEN_SWEEP, "swiglu": LLAMA_TOKEN_SWEEP,
+    "fused_add_rms_norm": LLAMA_TOKEN_SWEEP, "rope": LLAMA_TOKEN_SWEEP,
+    "cross_entropy": LLAMA_VOCAB_TOKEN_SWEEP, "softmax@vocab": LLAMA_VOCAB_TOKEN_SWEEP,
+}
+# Operators whose CPU step at the full benchmark size costs a few hundred ms to about
+# a second on the host cores: their CPU baseline runs the whole workload.
+CPU_FULL = ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm", "rope",
+            "cross_entropy", "softmax@vocab")
 
 
 def split_name(name: str) -> tuple:
@@ -118,7 +142,20 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
         B, H, S, D = d["B"], d["H"], d["S"], d["D"]  # FLOPs count query heads
         dense = 2.0 * S * S * D * B * H  # one S x S x D product
         return {"unit": "flops", "fwd": 2 * dense / 2, "bwd": 5 * dense / 2}
+    if name == LAYER:
+        # model FLOPs: the seven projections (2 M P forward, 4 M P backward for P
+        # weights) and the causal attention (FlashAttention convention); the
+        # recomputed projections of the backward are not counted
+        return {"unit": "flops", **layer_flops(d)}
     raise KeyError(name)
+
+
+def layer_flops(d: dict) -> dict:
+    M = d["B"] * d["T"]
+    hid, qo, kvo, inter = d["hidden"], d["q_out"], d["kv_out"], d["intermediate"]
+    P = hid * (qo + 2 * kvo) + qo * hid + 3 * hid * inter
+    dense = 2.0 * d["T"] * d["T"] * d["head_dim"] * d["B"] * (qo // d["head_dim"])
+    return {"fwd": 2.0 * M * P + dense, "bwd": 4.0 * M * P + 5 * dense / 2}
 
 
 # Kernels each entry point launches, in launch order (index = position).
@@ -151,6 +188,27 @@ KERNELS = {
     # as raw packs, one kernel each
     "softmax@vocab": {"fwd": ["softmax_fwd_lds"], "bwd": ["softmax_bwd_lds"]},
 }
+# The decoder layer's launches at Llama-3-8B widths (no k-padding of the
+# intermediate or kv widths): evograd_amd/pairs/llama3_decoder_layer.py in order.
+_QKV = ["gemm_kernel(q)", "gemm_kernel(k)", "gemm_kernel(v)", "heads_kernel(q,rope)",
+        "heads_kernel(k,rope)", "heads_kernel(v)"]
+_LAYER_KERNELS = {
+    "fwd": ["rmsnorm_fwd_row(h1)", *_QKV, "attn_fwd_kernel", "heads_kernel(o merge)",
+            "gemm_kernel(o,+x)", "rmsnorm_fwd_row(h2)", "gemm_kernel(gate)", "gemm_kernel(up)",
+            "silu_mul_kernel", "gemm_kernel(down,+x1)"],
+    "bwd": ["rmsnorm_fwd_row(h2)", "gemm_kernel(gate)", "gemm_kernel(up)", "silu_mul_kernel",
+            "gemm_kernel(d_act)", "gemm_kernel(dWd)", "swiglu_bwd_kernel", "gemm_kernel(dh2)",
+            "gemm_kernel(dh2+=)", "gemm_kernel(dWg)", "gemm_kernel(dWu)", "norm_bwd_ring(post)",
+            "colsum_wide_kernel(post)", "add_kernel(dx1)", "gemm_kernel(do)", "gemm_kernel(dWo)",
+            "rmsnorm_fwd_row(h1)", *_QKV, "heads_kernel(o split)", "heads_kernel(do split)",
+            "attn_dq_kernel", "attn_dkdv_kernel", "heads_kernel(dq merge,rope)",
+            "heads_kernel(dk merge,rope)", "heads_kernel(dv merge)", "gemm_kernel(dh1)",
+            "gemm_kernel(dh1+=dk)", "gemm_kernel(dh1+=dv)", "gemm_kernel(dWq)",
+            "gemm_kernel(dWk)", "gemm_kernel(dWv)", "norm_bwd_ring(in)", "colsum_wide_kernel(in)",
+            "add_kernel(dx)"],
+}
+for _t in (1024, 2048, 4096):
+    KERNELS[f"{LAYER}@llama3_8b_T{_t}"] = _LAYER_KERNELS
 
 # The kernel whose roofline each op reports, with its algorithmic work per launch.
 DOMINANT = {
@@ -161,6 +219,7 @@ DOMINANT = {
     "cross_entropy": ("bwd", 0),
     "fused_linear_cross_entropy": ("fwd", 3),
     "softmax@vocab": ("bwd", 0),
+    **{f"{LAYER}@llama3_8b_T{t}": ("fwd", 11) for t in (1024, 2048, 4096)},
 }
 
 
@@ -180,6 +239,8 @@ def dominant_work(name: str, w, work: dict) -> float:
     if name in ("causal_attention", "causal_attention_gqa", "llama3_attention"):
         # dK/dV kernel: S, dP, dV, dK of the five products
         return work["bwd"] * 4 / 5
+    if name == LAYER:  # the gate projection h2 Wg^T
+        return 2.0 * d["B"] * d["T"] * d["hidden"] * d["intermediate"]
     phase = DOMINANT[name][0]
     return work[phase]
 
@@ -298,6 +359,9 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
         "saved_tensors": report["saved_tensors"],
         "kernels_us": kt,
     }
+    if base == LAYER:
+        out["saved"]["peak_scratch_note"] = ("forward and backward intermediates are "
+                                             "torch.empty buffers freed when each call returns")
     phase, idx = DOMINANT[name]
     kname = KERNELS[name][phase][idx]
     k_us = kt[f"{phase}:{kname}"]
@@ -333,6 +397,45 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     return out
 
 
+def sweep_op(name: str, tokens: tuple, steps: int, warmup: int, flush) -> dict:
+    """Full-step latency (forward + backward, cold cache, median) and the HBM
+    fraction of an operator at each token count of the reference's sweep, the
+    other dims at the benchmark workload's (RoPE: one q tensor of 32 heads, B=1)."""
+    import dataclasses
+
+    import torch
+
+    from evograd_amd import decls, pair_module
+    from evograd_amd.bind import backward_inactive_kwargs, lookup_pair
+    from evograd_amd.harness import summarize, time_regions
+    from evograd_amd.inputs import make_case_inputs
+
+    base, label = split_name(name)
+    op = decls.get_op(base)
+    f, b = lookup_pair(op, pair_module(base))
+    w0 = bench_workload(op, label)
+    out = {}
+    for t in tokens:
+        if base == "rope":
+            dims = dict(w0.dims, B=1, T=t)
+        else:
+            dims = dict(w0.dims, rows=t)
+        w = dataclasses.replace(w0, dims=dims)
+        inputs = make_case_inputs(op, w, "cuda")
+        args = [inputs.get(a.name, getattr(a, "default", None)) for a in op.args]
+        kw = backward_inactive_kwargs(op, b, inputs)
+        dy = inputs[op.upstream_grad_name]
+        ms = summarize(time_regions(lambda: b(dy, f(*args)[1], **kw), reps=steps,
+                                    warmup=warmup, flush=flush))["median_ms"]
+        work = algorithmic_work(base, w)
+        gbs = (work["fwd"] + work["bwd"]) / (ms * 1e-3) / 1e9
+        out[str(t)] = {"full_us": round(ms * 1e3, 2), "hbm_frac_full": round(gbs / HBM_PEAK_GBS, 4),
+                       "dims": dims}
+        del inputs, args, dy
+        torch.cuda.empty_cache()
+    return out
+
+
 # ----------------------------------------------------------------- CPU side
 def cpu_baseline(name: str) -> dict:
     """Eager PyTorch autograd on the host cores over a bounded sample, scaled."""
@@ -350,20 +453,30 @@ def cpu_baseline(name: str) -> dict:
     w = bench_workload(op, label)
     d = w.dims
     # The sample: leading slices of the benchmark's own GPU-seeded tensors.
-    if name == "fused_linear_cross_entropy":
+    full_name = name + (f"@{label}" if label else "")
+    if full_name in CPU_FULL:
+        cut, scale = {}, 1.0
+        sample = "full workload"
+        if name == "rope":
+            # q [B, n_heads, T, D] of the declared recipe; the joint launch's k heads
+            # are the same computation on B * k_heads more rows
+            full = d["B"] * (d["n_heads"] + int(w.extra["k_heads"]))
+            scale = full / (d["B"] * d["n_heads"])
+            sample = (f"full q [{d['B']}, {d['n_heads']}, {d['T']}, {d['head_dim']}], scaled "
+                      f"x{scale:g} for the k heads of the joint q/k workload")
+    elif name == LAYER:
+        # the first 1024 tokens (the whole T=1024 workload), scaled by model FLOPs
+        t = min(d["T"], 1024)
+        cut = {"T": t}
+        small = dict(d, T=t)
+        f_full, f_small = layer_flops(d), layer_flops(small)
+        scale = (f_full["fwd"] + f_full["bwd"]) / (f_small["fwd"] + f_small["bwd"])
+        sample = ("full workload" if t == d["T"] else
+                  f"first {t} of {d['T']} tokens, scaled x{scale:.3g} by model FLOPs")
+    elif name == "fused_linear_cross_entropy":
         cut = {"rows": 64}
         scale = d["rows"] / 64
         sample = f"first 64 of {d['rows']} rows"
-    elif name in ("softmax", "rmsnorm", "layernorm", "swiglu", "fused_add_rms_norm",
-                  "cross_entropy"):
-        cut = {"rows": max(1, d["rows"] // 8)}
-        scale = d["rows"] / cut["rows"]
-        sample = f"first {cut['rows']} of {d['rows']} rows"
-    elif name == "rope":
-        full = d["B"] * (d["n_heads"] + int(w.extra["k_heads"]))
-        cut = {"B": 1, "n_heads": 8}
-        scale = full / 8
-        sample = f"8 of {full} (batch, head) rows of q and k (batch 0, query heads 0-7)"
     elif name in ("causal_attention_gqa", "llama3_attention"):
         # kv head 0 of batch 0 and its group of query heads
         full = d["B"] * d["KVH"]
@@ -415,9 +528,10 @@ def cpu_baseline(name: str) -> dict:
     us = statistics.median(samples) * scale
     verified = (f"runtime forward held to {op.forward} on {checked} correctness workloads"
                 if checked else "the declared forward itself")
+    how = (f"{len(samples)} reps, median" if scale == 1.0 else
+           f"{len(samples)} reps, median scaled x{scale:.4g} to the full workload")
     return {"value": us, "unit": "us", "cores": cores, "kind": "port",
-            "sample": (f"{sample} of the benchmark's GPU-seeded inputs copied to the host, "
-                       f"{len(samples)} reps, median scaled x{scale:g} to the full workload"),
+            "sample": f"{sample} of the benchmark's GPU-seeded inputs copied to the host, {how}",
             "timed_forward": f"{op.runtime_forward or op.forward} ({verified})",
             "what": f"eager torch autograd on CPU of {op.runtime_forward or op.forward}"}
 
@@ -507,6 +621,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ops", default=",".join(ALL_OPS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the token sweeps of the memory-bound operators")
     ap.add_argument("--profile", metavar="OP",
                     help="rocprofv3 workload: STEPS x (flush, fwd, bwd) of OP plus copy calibration")
     args = ap.parse_args()
@@ -547,6 +663,19 @@ def main() -> int:
         log(f"gpu {name}: " + json.dumps({k: v for k, v in results[name].items()
                                           if k in ("fwd_us", "bwd_us", "full_us", "error")}))
     torch.cuda.synchronize()
+    sweeps = {}
+    if not args.no_sweep:
+        for name in SWEEP_OPS:
+            if name.split("@")[0] not in [o.split("@")[0] for o in ops]:
+                continue
+            log(f"sweep {name} ...")
+            try:
+                sweeps[name] = sweep_op(name, SWEEP_OPS[name], max(5, args.steps // 2),
+                                        min(args.warmup, 3), flush)
+            except Exception as e:
+                sweeps[name] = {"error": f"{type(e).__name__}: {e}"}
+            log(f"sweep {name}: " + json.dumps({k: v.get("hbm_frac_full") if isinstance(v, dict)
+                                                else v for k, v in sweeps[name].items()}))
 
     cpu = {}
     if not args.no_cpu:
@@ -603,6 +732,7 @@ def main() -> int:
                          if HEADLINE in cpu and "value" in cpu[HEADLINE] else None),
         "cpu_model": cpu_model(),
         "ops": results,
+        "sweeps": sweeps,
     }
     traffic = load_traffic("norm_bwd_ring")
     if traffic is not None:

@@ -7,7 +7,8 @@ Layout:
 * ``opdecl``    the torch-free declaration contract (Active, Inactive, Workload, OpDecl)
 * ``decls``     declarations of softmax, rmsnorm, layernorm, swiglu, rope, causal_attention,
                 fused_add_rms_norm, causal_attention_gqa, llama3_attention (RoPE on q, k
-                then grouped causal attention), cross_entropy, fused_linear_cross_entropy
+                then grouped causal attention), cross_entropy, fused_linear_cross_entropy,
+                llama3_decoder_layer (one whole Llama-3 decoder layer)
 * ``pairs``     one module per operator with the reference's
                 ``<op>_forward_with_saved`` / ``<op>_backward_from_saved`` functions
 * ``bind``      ``bind(op, module)`` -> a ``torch.autograd.Function``-backed callable
@@ -28,6 +29,7 @@ PAIR_MODULES = {
     "llama3_attention": "evograd_amd.pairs.llama3_attention",
     "cross_entropy": "evograd_amd.pairs.cross_entropy",
     "fused_linear_cross_entropy": "evograd_amd.pairs.fused_linear_cross_entropy",
+    "llama3_decoder_layer": "evograd_amd.pairs.llama3_decoder_layer",
 }
 
 

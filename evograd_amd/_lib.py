@@ -20,7 +20,7 @@ import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libevograd_hip.so")
 
 EG_F32, EG_F16, EG_BF16 = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _DTYPE_TAG = {
     torch.float32: EG_F32,
@@ -69,7 +69,12 @@ SIGNATURES: dict[str, tuple] = {
     "eg_flce_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i32]),
     "eg_flce_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p]),
     "eg_scale_copy": (_i32, [_p, _i32, _p, _i32, _i64, _p, _i32, _p, _p]),
-    "eg_gemm": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p]),
+    "eg_gemm": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                       _i32, _i32, _p]),
+    "eg_split_heads": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
+    "eg_merge_heads": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
+    "eg_add": (_i32, [_p, _p, _p, _i64, _i32, _p]),
+    "eg_silu_mul": (_i32, [_p, _p, _p, _i64, _i32, _p]),
 }
 
 _lib = None

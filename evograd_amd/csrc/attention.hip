@@ -935,16 +935,28 @@ constexpr int kDkdvRows = 32;
 // workgroups of 256 keys are 3-4% slower).
 template <int D> constexpr int dkdv_waves() { return 4; }
 
+// The MFMA kernels take 16-bit tensors with head_dim 64 or 128; everything else
+// (fp32, other even head sizes up to 128) runs on the generic kernels
+// (attn_generic.hip).
+bool mfma_shape(int64_t D, int dtype) {
+  return (D == 64 || D == 128) && (dtype == EG_BF16 || dtype == EG_F16);
+}
+
 int check_attn(const char* what, int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D,
-               int dtype) {
+               int dtype, bool mfma_only = false) {
   if (B < 0 || H < 0 || S < 0) { set_error("%s: negative size", what); return 1; }
   if (H > 0 && (Hkv <= 0 || H % Hkv != 0)) {
     set_error("%s: heads (%lld) must be a positive multiple of kv_heads (%lld)", what,
               (long long)H, (long long)Hkv);
     return 1;
   }
-  if (D != 64 && D != 128) { set_error("%s: head_dim must be 64 or 128, got %lld", what, (long long)D); return 1; }
-  if (dtype != EG_BF16 && dtype != EG_F16) { set_error("%s: dtype must be bf16 or fp16", what); return 1; }
+  if (mfma_only) {
+    if (D != 64 && D != 128) { set_error("%s: head_dim must be 64 or 128, got %lld", what, (long long)D); return 1; }
+    if (dtype != EG_BF16 && dtype != EG_F16) { set_error("%s: dtype must be bf16 or fp16", what); return 1; }
+  } else {
+    if (D < 2 || D > 128 || D % 2) { set_error("%s: head_dim must be even and at most 128, got %lld", what, (long long)D); return 1; }
+    if (dtype != EG_BF16 && dtype != EG_F16 && dtype != EG_F32) { set_error("%s: dtype must be fp32, bf16 or fp16", what); return 1; }
+  }
   // One (b, h) slice is addressed with 32-bit buffer offsets: S * D * 2 < 2^31.
   if (S > ((int64_t)1 << 22) || B * H > ((int64_t)1 << 24)) {
     set_error("%s: size out of range (seq <= 4194304, batch*heads <= 16777216)", what);
@@ -1048,8 +1060,11 @@ extern "C" int eg_attn_gqa_fwd(const void* q, const void* k, const void* v, void
   if (check_attn("eg_attn_fwd", batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
   if (batch == 0 || heads == 0 || seq == 0) return 0;
   if (!q || !k || !v || !o || !lse) { set_error("eg_attn_fwd: null pointer"); return 1; }
-  if (!attn_aligned({q, k, v, o})) { set_error("eg_attn_fwd: tensors must be 16-byte aligned"); return 1; }
   hipStream_t st = as_stream(stream);
+  if (!mfma_shape(head_dim, dtype))
+    return attn_generic_fwd(q, k, v, o, lse, batch, heads, kv_heads, seq, head_dim, scale, dtype,
+                            st);
+  if (!attn_aligned({q, k, v, o})) { set_error("eg_attn_fwd: tensors must be 16-byte aligned"); return 1; }
   const int64_t BH = batch * heads;
   const int group = (int)(heads / kv_heads);
   if (dtype == EG_BF16)
@@ -1071,14 +1086,17 @@ extern "C" int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, c
     set_error("eg_attn_bwd: null pointer");
     return 1;
   }
+  hipStream_t st = as_stream(stream);
+  float* delta = (float*)workspace;
+  if (!mfma_shape(head_dim, dtype))
+    return attn_generic_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, batch, heads, kv_heads, seq,
+                            head_dim, scale, dtype, st);
   if (!attn_aligned({dout, q, k, v, o, dq, dk, dv})) {
     set_error("eg_attn_bwd: tensors must be 16-byte aligned");
     return 1;
   }
-  hipStream_t st = as_stream(stream);
   const int64_t BH = batch * heads;
   const int group = (int)(heads / kv_heads);
-  float* delta = (float*)workspace;
   if (dtype == EG_BF16)
     return head_dim == 128
                ? attn_bwd_launch<bf16_t, 128>(dout, q, k, v, o, lse, dq, dk, dv, delta, BH, seq, group, scale, st)
@@ -1137,7 +1155,7 @@ extern "C" int eg_llama3_attn_fwd(const void* q, const void* k, const void* v, c
                                   int64_t head_dim, float scale, int dtype, void* stream) {
   static const char* name = "eg_llama3_attn_fwd";
   clear_error();
-  if (check_attn(name, batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
+  if (check_attn(name, batch, heads, kv_heads, seq, head_dim, dtype, true)) return 1;
   if (batch == 0 || heads == 0 || seq == 0) return 0;
   if (!q || !k || !v || !cos || !sin || !o || !lse || !workspace) {
     set_error("%s: null pointer", name);
@@ -1168,7 +1186,7 @@ extern "C" int eg_llama3_attn_bwd(const void* dout, const void* q, const void* k
                                   int64_t head_dim, float scale, int dtype, void* stream) {
   static const char* name = "eg_llama3_attn_bwd";
   clear_error();
-  if (check_attn(name, batch, heads, kv_heads, seq, head_dim, dtype)) return 1;
+  if (check_attn(name, batch, heads, kv_heads, seq, head_dim, dtype, true)) return 1;
   if (batch == 0 || heads == 0 || seq == 0) return 0;
   if (!dout || !q || !k || !v || !o || !lse || !cos || !sin || !dq || !dk || !dv || !workspace) {
     set_error("%s: null pointer", name);

@@ -79,7 +79,7 @@ extern "C" int eg_time_kernel_missed(void) {
   return missed;
 }
 
-extern "C" int eg_abi_version(void) { return 1; }
+extern "C" int eg_abi_version(void) { return 2; }
 
 extern "C" const char* eg_last_error(void) { return eg::g_error; }
 

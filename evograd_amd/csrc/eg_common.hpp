@@ -230,9 +230,13 @@ int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
 // fp32 accumulation. a_kc: a is [a_rows][lda] holding rows m, else rows k; b_kc:
 // b is [b_rows][ldb] holding rows n, else rows k; rows at or past a_rows / b_rows
 // read as zero. bf16/fp16 operands need k % 64 == 0 for a k-contiguous operand.
+// With r non-null the output is c = r + a b (r of c_dtype, or fp32 with r_f32; row
+// stride ldr; added in fp32 before c is rounded); r == c with ldr == ldc
+// accumulates in place.
 int gemm_launch(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
                 int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
-                int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name);
+                int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
+                const void* r = nullptr, int64_t ldr = 0, bool r_f32 = false);
 
 // The logits product of the fused linear cross entropy with its softmax terms
 // formed in the epilogue (gemm.hip), 16-bit operands only: for logits = x w^T
@@ -247,6 +251,21 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t m,
                                int64_t k, int64_t ldx, int64_t ldw, int64_t lde,
                                const int64_t* target, float* hstats, float* tlogit, int dtype,
                                hipStream_t st, const char* name);
+
+// Causal GQA attention on plain fp32 arithmetic (attn_generic.hip) for the shapes
+// the MFMA kernels do not take: any dtype, even head_dim <= 128. Arguments as
+// eg_attn_gqa_fwd / eg_attn_gqa_bwd, already validated; delta is the backward's
+// fp32 [B, H, S] workspace. With tables rc, rs (fp32 [S, D]) the forward rotates q
+// as it loads it (k already rotated) and the backward takes the rotated q, k and
+// writes dq, dk for the pre-rotation ones.
+int attn_generic_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                     int64_t H, int64_t Hkv, int64_t S, int64_t D, float scale, int dtype,
+                     hipStream_t st, const float* rc = nullptr, const float* rs = nullptr);
+int attn_generic_bwd(const void* dout, const void* q, const void* k, const void* v,
+                     const void* o, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                     int64_t B, int64_t H, int64_t Hkv, int64_t S, int64_t D, float scale,
+                     int dtype, hipStream_t st, const float* rc = nullptr,
+                     const float* rs = nullptr);
 
 // The RoPE launch behind eg_rope (rope.hip), for entry points that rotate as one
 // step of a longer launch sequence: arguments as eg_rope's, already validated.

@@ -220,9 +220,9 @@ template <bool AKC, bool BKC> struct LoadSpread { static constexpr int b_substep
 template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                 TC* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+                 TC* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                  int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c,
-                 SmxArgs smx) {
+                 SmxArgs smx, const void* R, int64_t ldr, int r_f32) {
   using v8 = typename GM<T>::v8;
   // Two separate buffers per operand, selected at compile time in the unrolled k
   // loop: the LDS reads of one buffer provably do not alias the loads in flight
@@ -448,13 +448,30 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const int row = m0 + wm + 32 * i + l32;
     if (row >= M) continue;
     TC* crow = C + (int64_t)row * ldc;
+    // residual row: of TC, or fp32 (r_f32: a running fp32 sum rounded into C)
+    const TC* rrow = R ? (const TC*)R + (int64_t)row * ldr : nullptr;
+    const float* rrow32 = R ? (const float*)R + (int64_t)row * ldr : nullptr;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int col = n0 + wn + 32 * j + 8 * q + 4 * hh;
-        const float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1];
-        const float v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1];
+        float v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        if (rrow) {
+          // C = R + A B: the residual (or, with R = C, the running sum) is read by
+          // the lane that writes the same elements, and added in fp32.
+          float r4[4] = {0.f, 0.f, 0.f, 0.f};
+          if (vec_c && col + 3 < N) {
+            if (r_f32) load_f32<float, 4>(rrow32 + col, r4);
+            else load_f32<TC, 4>(rrow + col, r4);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) r4[e] = r_f32 ? rrow32[col + e] : to_f32(rrow[col + e]);
+          }
+          v0 += r4[0], v1 += r4[1], v2 += r4[2], v3 += r4[3];
+        }
         if (vec_c && col + 3 < N) {
           if constexpr (std::is_same<TC, float>::value) {
             typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -487,9 +504,10 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 template <bool AKC, bool BKC>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A,
                                                        const float* __restrict__ B,
-                                                       float* __restrict__ C, int M, int N, int K,
+                                                       float* C, int M, int N, int K,
                                                        int64_t lda, int64_t ldb, int64_t ldc,
-                                                       int64_t a_rows, int64_t b_rows) {
+                                                       int64_t a_rows, int64_t b_rows,
+                                                       const float* R, int64_t ldr) {
   __shared__ float As[16][65], Bs[16][65];
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
@@ -524,7 +542,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
-      if (m < M && n < N) C[(int64_t)m * ldc + n] = acc[i][j];
+      if (m < M && n < N)
+        C[(int64_t)m * ldc + n] = R ? acc[i][j] + R[(int64_t)m * ldr + n] : acc[i][j];
     }
 }
 
@@ -535,7 +554,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 // holding rows n (else rows k). Rows at or past a_rows / b_rows read as zero.
 int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
-                int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name) {
+                int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
+                const void* R, int64_t ldr, bool r_f32) {
   if (M <= 0 || N <= 0) return 0;
   if (K <= 0) {
     set_error("%s: K must be positive", name);
@@ -549,12 +569,14 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     set_error("%s: an operand holds more rows than the product reads", name);
     return 1;
   }
+  if (R && r_f32 && c_dtype == EG_F32) r_f32 = false;  // the same thing
   if (dtype == EG_F32) {
     if (c_dtype != EG_F32) {
       set_error("%s: fp32 operands give an fp32 output", name);
       return 1;
     }
-    if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N) {
+    if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N ||
+        (R && ldr < N)) {
       set_error("%s: a leading dimension is smaller than its row", name);
       return 1;
     }
@@ -566,7 +588,7 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     auto go32 = [&](auto akc, auto bkc) {
       EG_LAUNCH((gemm_f32_kernel<decltype(akc)::value, decltype(bkc)::value>), grid, dim3(256),
                 0, st, (const float*)A, (const float*)B, (float*)C, (int)M, (int)N, (int)K, lda,
-                ldb, ldc, a_rows, b_rows);
+                ldb, ldc, a_rows, b_rows, (const float*)R, ldr);
       return check_launch(name);
     };
     using TT = std::true_type;
@@ -584,12 +606,20 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     set_error("%s: output must be fp32 or the operand dtype", name);
     return 1;
   }
-  if (((a_kc || b_kc) && K % kBK) || lda % 8 || ldb % 8 || !aligned16(A) || !aligned16(B)) {
-    set_error("%s: K-contiguous operands need K %% 64 == 0; strides must be multiples of 8 "
+  // A k-contiguous operand is read in whole 64-deep slices. With K % 64 != 0 that
+  // reads its columns K .. roundup(K, 64): allowed when the row stride covers them
+  // and the other operand is k-major (its rows past K read as zero, so those
+  // columns, which must hold finite values, add nothing).
+  const int64_t kpad = (K + kBK - 1) / kBK * kBK;
+  const bool k_ok = (!a_kc && !b_kc) || K % kBK == 0 ||
+                    (a_kc != b_kc && (a_kc ? lda : ldb) >= kpad);
+  if (!k_ok || lda % 8 || ldb % 8 || !aligned16(A) || !aligned16(B)) {
+    set_error("%s: K-contiguous operands need K %% 64 == 0 (or, against a k-major operand, a "
+              "row stride of at least K rounded up to 64); strides must be multiples of 8 "
               "elements and bases 16-byte aligned", name);
     return 1;
   }
-  if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N) {
+  if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N || (R && ldr < N)) {
     set_error("%s: a leading dimension is smaller than its row", name);
     return 1;
   }
@@ -609,13 +639,15 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
   const unsigned grid = (unsigned)(((tiles + 7) / 8) * 8);
   // 16-byte (fp32) or 8-byte (16-bit) row pieces of C need ldc % 4 == 0 and a
   // 16-byte aligned base; otherwise the kernel stores element by element.
-  const int vec_c = (ldc % 4 == 0) && aligned16(C);
+  const int vec_c = (ldc % 4 == 0) && aligned16(C) &&
+                    (!R || ((ldr % 4 == 0) && aligned16(R)));
   auto go = [&](auto tag, auto ctag, auto akc, auto bkc) {
     using T = decltype(tag);
     using TC = decltype(ctag);
     EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>), dim3(grid),
               dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
-              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c, SmxArgs{});
+              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c,
+              SmxArgs{}, R, ldr, (int)r_f32);
     return check_launch(name);
   };
   auto layouts = [&](auto tag, auto ctag) {
@@ -666,7 +698,8 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M,
     using T = decltype(tag);
     EG_LAUNCH((gemm_kernel<T, true, true, T, true>), dim3(grid), dim3(kThreads), 0, st,
               (const uint16_t*)x, (const uint16_t*)w, (T*)e, (int)M, (int)N, (int)K, ldx, ldw,
-              lde, M, N, (int)tiles_m, (int)tiles, vec_c, smx);
+              lde, M, N, (int)tiles_m, (int)tiles, vec_c, smx, (const void*)nullptr, (int64_t)0,
+              0);
     return check_launch(name);
   };
   return dtype == EG_BF16 ? go(bf16_t{}) : go(f16_t{});
@@ -676,9 +709,10 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M,
 
 using namespace eg;
 
-extern "C" int eg_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
-                       int64_t lda, int64_t ldb, int64_t ldc, int a_k_contiguous,
-                       int b_k_contiguous, int dtype, int c_dtype, void* stream) {
+extern "C" int eg_gemm(const void* a, const void* b, void* c, const void* r, int64_t m,
+                       int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t ldr,
+                       int a_k_contiguous, int b_k_contiguous, int dtype, int c_dtype,
+                       void* stream) {
   clear_error();
   if (m < 0 || n < 0 || k < 0) {
     set_error("eg_gemm: negative size");
@@ -690,5 +724,5 @@ extern "C" int eg_gemm(const void* a, const void* b, void* c, int64_t m, int64_t
   }
   const bool akc = a_k_contiguous != 0, bkc = b_k_contiguous != 0;
   return gemm_launch(a, b, c, m, n, k, lda, ldb, ldc, akc, bkc, akc ? m : k, bkc ? n : k, dtype,
-                     c_dtype, as_stream(stream), "eg_gemm");
+                     c_dtype, as_stream(stream), "eg_gemm", r, ldr);
 }

@@ -388,10 +388,13 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
 //   default: no fp32 logits are held);
 //   fp32 inputs: logits = x_c W^T (fp32) -> lse and row losses (xent_lse_kernel)
 //   -> unit dlogits (xent_bwd_*_kernel), chunks of at most 2^29 logits;
-// then dx_c = dl_c W (MFMA), dW = dl^T x over all rows at once (MFMA, accumulated
-// in registers over every row, rounded once) and the mean loss. The dlogits of all
-// rows are kept so that dW is one product; their rows are padded to a multiple of
-// 64 columns with zeros, the product's k step. No atomics: bitwise repeatable.
+// then dx_c = dl_c W and dW (+)= dl_c^T x_c (MFMA; with more than one chunk the
+// products accumulate in an fp32 [vocab, hidden] buffer, added in each product's
+// epilogue, and the last chunk's product rounds the sum once into dW; fp32 inputs
+// accumulate in dW itself), and the mean loss. Only one chunk of dlogits exists
+// at a time (at most kFlceDlChunkBytes by default), so scratch grows with the chunk
+// and the vocabulary, not with rows x vocab; dlogits rows are padded to a multiple
+// of 64 columns with zeros, the product's k step. No atomics: bitwise repeatable.
 
 namespace eg {
 namespace {
@@ -416,7 +419,9 @@ __global__ __launch_bounds__(256) void zero_cols_kernel(uint16_t* __restrict__ p
     p[(i / w) * ld + c0 + i % w] = 0;
 }
 
-constexpr int64_t kFlceChunkElems = (int64_t)1 << 29;
+// Default chunking: the dlogits of one chunk take at most this many bytes (the
+// fp32 path holds as many bytes again of fp32 logits).
+constexpr int64_t kFlceDlChunkBytes = (int64_t)1 << 30;
 
 // 16-bit path: the logits product leaves, per 128-column group h of each row,
 // e = exp(logit - mx_h) in the dlogits rows, (mx_h, s_h = sum of e) and the target
@@ -496,12 +501,14 @@ __global__ __launch_bounds__(kFixBlock) void flce_fixup_kernel(
   }
 }
 
-// Rows per chunk: as many as kFlceChunkElems logits allow, a power of two when
-// that splits the rows.
-int64_t flce_chunk_rows(int64_t rows, int64_t vocab) {
-  int64_t rc = kFlceChunkElems / (vocab > 0 ? vocab : 1);
+// Rows per chunk by default: as many as kFlceDlChunkBytes of dlogits rows allow
+// (row_bytes each), all rows when they fit, else a multiple of 256 (the product's
+// row tile) or, below that, a power of two.
+int64_t flce_chunk_rows(int64_t rows, int64_t row_bytes) {
+  int64_t rc = kFlceDlChunkBytes / (row_bytes > 0 ? row_bytes : 1);
   if (rc < 1) rc = 1;
   if (rc >= rows) return rows > 0 ? rows : 1;
+  if (rc >= 256) return rc / 256 * 256;
   int64_t p = 1;
   while (p * 2 <= rc) p *= 2;
   return p;
@@ -519,27 +526,29 @@ bool flce_fused(int64_t vocab, int dtype) {
 
 // Workspace: [lse | rowloss] (fp32, rows each), then either one chunk of fp32 logits
 // or (16-bit path) the target logits [rows] and the group statistics of one chunk
-// [rc][flce_groups(vocab)][2], then the dlogits of every row [rows][vp].
+// [rc][flce_groups(vocab)][2], then the dlogits of one chunk [rc][vp], then (16-bit
+// inputs over more than one chunk) the fp32 dW sum [vocab][hidden].
 struct FlceLayout {
   int64_t rc, vp;
   bool fused;
-  size_t stats, logits, dl, total;
+  size_t stats, logits, dl, acc, total;
 };
 
-FlceLayout flce_layout(int64_t rows, int64_t vocab, int64_t chunk_rows, int dtype) {
+FlceLayout flce_layout(int64_t rows, int64_t hidden, int64_t vocab, int64_t chunk_rows,
+                       int dtype) {
   FlceLayout l;
   l.fused = flce_fused(vocab, dtype);
   const int64_t all = rows > 0 ? rows : 1;
-  l.rc = chunk_rows > 0 ? std::min(chunk_rows, all)
-                        : (l.fused ? all : flce_chunk_rows(rows, vocab));
   l.vp = dtype == EG_F32 ? vocab : (vocab + 63) / 64 * 64;
   const size_t es = dtype == EG_F32 ? 4 : 2;
+  l.rc = chunk_rows > 0 ? std::min(chunk_rows, all) : flce_chunk_rows(rows, l.vp * (int64_t)es);
   l.stats = align_up((size_t)rows * 2 * sizeof(float));
   l.logits = l.fused ? align_up((size_t)rows * sizeof(float)) +
                            align_up((size_t)l.rc * flce_groups(vocab) * 2 * sizeof(float))
                      : align_up((size_t)l.rc * vocab * sizeof(float));
-  l.dl = align_up((size_t)rows * l.vp * es);
-  l.total = l.stats + l.logits + l.dl;
+  l.dl = align_up((size_t)l.rc * l.vp * es);
+  l.acc = (dtype != EG_F32 && rows > l.rc) ? align_up((size_t)vocab * hidden * sizeof(float)) : 0;
+  l.total = l.stats + l.logits + l.dl + l.acc;
   return l;
 }
 
@@ -548,9 +557,8 @@ FlceLayout flce_layout(int64_t rows, int64_t vocab, int64_t chunk_rows, int dtyp
 
 extern "C" size_t eg_flce_workspace_bytes(int64_t rows, int64_t hidden, int64_t vocab,
                                           int64_t chunk_rows, int dtype) {
-  (void)hidden;
   if (rows <= 0 || vocab <= 0) return 0;
-  return flce_layout(rows, vocab, chunk_rows, dtype).total;
+  return flce_layout(rows, hidden, vocab, chunk_rows, dtype).total;
 }
 
 extern "C" int eg_flce_fwd(const void* x, const void* weight, const int64_t* target, float* loss,
@@ -582,7 +590,7 @@ extern "C" int eg_flce_fwd(const void* x, const void* weight, const int64_t* tar
     set_error("%s: x, weight and workspace must be 16-byte aligned", name);
     return 1;
   }
-  const FlceLayout L = flce_layout(rows, vocab, chunk_rows, dtype);
+  const FlceLayout L = flce_layout(rows, hidden, vocab, chunk_rows, dtype);
   if (L.rc * vocab / kFlatPer >= ((int64_t)1 << 32) / kFlatBlock) {
     set_error("%s: vocab=%lld exceeds the launch grid", name, (long long)vocab);
     return 1;
@@ -601,13 +609,15 @@ extern "C" int eg_flce_fwd(const void* x, const void* weight, const int64_t* tar
   float* rowloss = lse + rows;
   float* logits = (float*)(ws + L.stats);
   char* dl = ws + L.stats + L.logits;
+  float* acc = L.acc ? (float*)(dl + L.dl) : nullptr;
   return dispatch_type(dtype, name, [&](auto tag) {
     using T = decltype(tag);
     T* dlp = (T*)dl;
     if (L.vp > vocab) {
-      const int64_t n = rows * (L.vp - vocab);
+      // padding columns of the chunk's dlogits rows: zero once, never written after
+      const int64_t n = L.rc * (L.vp - vocab);
       const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
-      EG_LAUNCH(zero_cols_kernel, dim3(grid), dim3(256), 0, st, (uint16_t*)dl, rows, (int)vocab,
+      EG_LAUNCH(zero_cols_kernel, dim3(grid), dim3(256), 0, st, (uint16_t*)dl, L.rc, (int)vocab,
                 (int)L.vp, L.vp);
     }
     for (int64_t r0 = 0; r0 < rows; r0 += L.rc) {
@@ -616,47 +626,48 @@ extern "C" int eg_flce_fwd(const void* x, const void* weight, const int64_t* tar
       if (L.fused) {
         float* tlogit = logits;
         float* hstats = (float*)((char*)logits + align_up((size_t)rows * sizeof(float)));
-        if (int rc = gemm_logits_softmax_launch(xc, weight, dlp + r0 * L.vp, n, vocab, hidden,
-                                                hidden, hidden, L.vp, target + r0, hstats,
-                                                tlogit + r0, dtype, st, name))
+        if (int rc = gemm_logits_softmax_launch(xc, weight, dlp, n, vocab, hidden, hidden, hidden,
+                                                L.vp, target + r0, hstats, tlogit + r0, dtype, st,
+                                                name))
           return rc;
         if constexpr (!std::is_same<T, float>::value) {
-          EG_LAUNCH((flce_fixup_kernel<T>), dim3((unsigned)n), dim3(kFixBlock), 0, st,
-                    dlp + r0 * L.vp, L.vp, (int)vocab, hstats, (int)flce_groups(vocab),
-                    tlogit + r0, target + r0, lse + r0, rowloss + r0, ignore_index);
+          EG_LAUNCH((flce_fixup_kernel<T>), dim3((unsigned)n), dim3(kFixBlock), 0, st, dlp, L.vp,
+                    (int)vocab, hstats, (int)flce_groups(vocab), tlogit + r0, target + r0,
+                    lse + r0, rowloss + r0, ignore_index);
         }
         if (int rc = check_launch(name)) return rc;
-        if (int rc = gemm_launch(dlp + r0 * L.vp, weight, (T*)dx + r0 * hidden, n, hidden, L.vp,
-                                 L.vp, hidden, hidden, true, false, n, vocab, dtype, dtype, st,
-                                 name))
-          return rc;
-        continue;
-      }
-      if (int rc = gemm_launch(xc, weight, logits, n, vocab, hidden, hidden, hidden, vocab, true,
-                               true, n, vocab, dtype, EG_F32, st, name))
-        return rc;
-      const float* none = nullptr;
-      if (vocab % 4 == 0) {
-        pick_row_block(vocab / 4, LseLaunch<float, 4>{logits, target + r0, lse + r0,
-                                                      rowloss + r0, n, (int)vocab,
-                                                      ignore_index, st});
-        launch_bwd<float, T, float, 4>(none, logits, target + r0, lse + r0, nullptr,
-                                       dlp + r0 * L.vp, n, (int)vocab, ignore_index, st, L.vp);
       } else {
-        pick_row_block(vocab, LseLaunch<float, 1>{logits, target + r0, lse + r0, rowloss + r0,
-                                                  n, (int)vocab, ignore_index, st});
-        launch_bwd<float, T, float, 1>(none, logits, target + r0, lse + r0, nullptr,
-                                       dlp + r0 * L.vp, n, (int)vocab, ignore_index, st, L.vp);
+        if (int rc = gemm_launch(xc, weight, logits, n, vocab, hidden, hidden, hidden, vocab, true,
+                                 true, n, vocab, dtype, EG_F32, st, name))
+          return rc;
+        const float* none = nullptr;
+        if (vocab % 4 == 0) {
+          pick_row_block(vocab / 4, LseLaunch<float, 4>{logits, target + r0, lse + r0,
+                                                        rowloss + r0, n, (int)vocab,
+                                                        ignore_index, st});
+          launch_bwd<float, T, float, 4>(none, logits, target + r0, lse + r0, nullptr, dlp, n,
+                                         (int)vocab, ignore_index, st, L.vp);
+        } else {
+          pick_row_block(vocab, LseLaunch<float, 1>{logits, target + r0, lse + r0, rowloss + r0,
+                                                    n, (int)vocab, ignore_index, st});
+          launch_bwd<float, T, float, 1>(none, logits, target + r0, lse + r0, nullptr, dlp, n,
+                                         (int)vocab, ignore_index, st, L.vp);
+        }
+        if (int rc = check_launch(name)) return rc;
       }
-      if (int rc = check_launch(name)) return rc;
-      if (int rc = gemm_launch(dlp + r0 * L.vp, weight, (T*)dx + r0 * hidden, n, hidden, L.vp,
-                               L.vp, hidden, hidden, true, false, n, vocab, dtype, dtype, st,
-                               name))
+      if (int rc = gemm_launch(dlp, weight, (T*)dx + r0 * hidden, n, hidden, L.vp, L.vp, hidden,
+                               hidden, true, false, n, vocab, dtype, dtype, st, name))
+        return rc;
+      // dW = sum over chunks of dl_c^T x_c: into dW directly (one chunk, or fp32
+      // inputs), else into the fp32 sum, the last chunk rounding it once into dW
+      const bool first = r0 == 0, last = r0 + n >= rows;
+      void* out = (acc && !last) ? (void*)acc : dweight;
+      const void* res = first ? nullptr : (acc ? (const void*)acc : dweight);
+      if (int rc = gemm_launch(dlp, xc, out, vocab, hidden, n, L.vp, hidden, hidden, false,
+                               false, n, n, dtype, out == acc ? EG_F32 : dtype, st, name, res,
+                               hidden, acc != nullptr))
         return rc;
     }
-    if (int rc = gemm_launch(dlp, x, dweight, vocab, hidden, rows, L.vp, hidden, hidden, false,
-                             false, rows, rows, dtype, dtype, st, name))
-      return rc;
     EG_LAUNCH((xent_mean_kernel<float>), dim3(1), dim3(kMeanBlock), 0, st, target, rowloss, loss,
               n_valid, rows, ignore_index);
     return check_launch(name);

@@ -12,6 +12,7 @@ drop-in the reference's harness looks up:
 * fused_add_rms_norm  src/evograd/ops/level2/fused_add_rms_norm/__init__.py:76-122
 * cross_entropy  src/evograd/ops/level1/cross_entropy/__init__.py:76-111
 * fused_linear_cross_entropy  src/evograd/ops/level2/fused_linear_cross_entropy/__init__.py:91-152
+* llama3_decoder_layer  src/evograd/ops/level3/llama3_decoder_layer/__init__.py:136-235
 * causal_attention: the reference has no standalone declaration; its semantics
   are F.scaled_dot_product_attention(q, k, v, is_causal=True) inside
   src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:101-108. It is
@@ -23,7 +24,8 @@ Differences from the reference declarations, all deliberate:
 * Tolerances are the stricter gate of this build: fp32 (1e-5, 1e-5),
   fp16 (1e-2, 1e-2), bf16 (2e-2, 2e-2), flat for every output and gradient (the
   reference uses fp32 2e-5, fp16 5e-2, bf16 8e-2, src/evograd/ops/_common.py:13-17,
-  and widens bf16 parameter gradients by sqrt(rows/8)).
+  and widens bf16 parameter gradients by sqrt(rows/8)). The one exception is the
+  decoder layer, which keeps the reference's own block-level gate (below).
 * ``reference_dtype="float32"``: the oracle runs reduced-precision cases in fp32
   and casts back (the promotion of src/evograd/opdecl/oracle.py:70-110), so a
   comparison measures the kernel's error, not the oracle's own bf16 rounding.
@@ -340,6 +342,16 @@ CAUSAL_ATTENTION = declare_op(
             (1, 4, 1024, 128),
         )
         for dt in ("bfloat16", "float16")
+    ) + (
+        # the generic kernels: fp32, and head sizes off the MFMA path (the decoder
+        # layer's correctness gate runs head_dim 32 and 16 in fp32 and bf16)
+        Workload(dims=dict(B=1, H=2, S=64, D=64), dtype="float32"),
+        Workload(dims=dict(B=1, H=2, S=129, D=128), dtype="float32"),
+        Workload(dims=dict(B=1, H=2, S=100, D=32), dtype="float32"),
+        Workload(dims=dict(B=2, H=3, S=77, D=16), dtype="float32"),
+        Workload(dims=dict(B=1, H=2, S=100, D=32), dtype="bfloat16"),
+        Workload(dims=dict(B=2, H=3, S=77, D=16), dtype="bfloat16"),
+        Workload(dims=dict(B=1, H=2, S=70, D=48), dtype="float16"),
     ),
     benchmark=(
         Workload(dims=dict(B=4, H=32, S=4096, D=128), dtype="bfloat16", label="baseline"),
@@ -385,6 +397,12 @@ CAUSAL_ATTENTION_GQA = declare_op(
             (1, 32, 8, 512, 128),
         )
         for dt in ("bfloat16", "float16")
+    ) + (
+        Workload(dims=dict(B=1, H=4, KVH=1, S=32, D=32), dtype="float32"),
+        Workload(dims=dict(B=2, H=4, KVH=1, S=17, D=16), dtype="float32"),
+        Workload(dims=dict(B=1, H=4, KVH=2, S=100, D=64), dtype="float32"),
+        Workload(dims=dict(B=1, H=4, KVH=1, S=32, D=32), dtype="bfloat16"),
+        Workload(dims=dict(B=2, H=4, KVH=1, S=17, D=16), dtype="bfloat16"),
     ),
     benchmark=(
         Workload(dims=dict(B=4, H=32, KVH=8, S=4096, D=128), dtype="bfloat16",
@@ -535,7 +553,9 @@ FUSED_LINEAR_CROSS_ENTROPY = declare_op(
     ),
     backward_semantics=(
         "dlogits = dloss * (softmax(logits) - onehot(target)) / n_valid; dx = dlogits @ "
-        "weight, dweight = dlogits.T @ x, in the inputs' dtypes, fp32 accumulation."
+        "weight, dweight = dlogits.T @ x, in the inputs' dtypes, fp32 accumulation. The "
+        "same chunking the forward uses applies here: dlogits must not be materialized "
+        "in full either."
     ),
     correctness=tuple(
         Workload(dims=dict(rows=r, hidden=h, vocab=v), dtype=dt)
@@ -564,10 +584,92 @@ FUSED_LINEAR_CROSS_ENTROPY = declare_op(
     regime_split=LLAMA_VOCAB_REGIME_SPLIT,
 )
 
+# ------------------------------------------------------- llama3_decoder_layer
+# src/evograd/ops/level3/llama3_decoder_layer/__init__.py:136-235: one Llama-3-8B
+# decoder layer as one autograd pair. Its gate is the reference's own (fp32 1e-4;
+# bf16 atol 5e-2 / rtol 2e-2 against the fp32 reference; atol x1.5 for the three
+# widest reductions), not this build's flat per-op tolerance: at block depth the
+# gradients span a dynamic range where a flat bf16 2e-2 would gate the fp32
+# oracle's own rounding of ten composed operators. Correctness at the reference's
+# four small workloads (:55-65); timed at its grid, B=1 and T in {1024, 2048,
+# 4096} bf16 at Llama-3-8B widths (:36-44, src/evograd/opdecl/models.py:250-264).
+_LAYER_SMALL = dict(B=1, T=32, hidden=128, head_dim=32, q_out=128, kv_out=32, intermediate=352)
+_LAYER_SMALL_2 = dict(B=2, T=17, hidden=64, head_dim=16, q_out=64, kv_out=16, intermediate=176)
+
+
+def _llama3_8b_layer(tokens: int) -> dict:
+    return dict(B=1, T=tokens, hidden=4096, head_dim=128, q_out=4096, kv_out=1024,
+                intermediate=14336)
+
+
+def _layer_tokens_feature(workload) -> float:
+    return float(workload.dims["B"] * workload.dims["T"])
+
+
+LLAMA3_DECODER_LAYER = declare_op(
+    name="llama3_decoder_layer",
+    forward="oracle.forward_refs:llama3_decoder_layer_forward_ref",
+    runtime_forward="oracle.forward_refs:llama3_decoder_layer_runtime_ref",
+    reference_dtype="float32",
+    dims=("B", "T", "hidden", "head_dim", "q_out", "kv_out", "intermediate"),
+    args=(
+        Active("x", "[B, T, hidden]"),
+        Active("input_norm_weight", "[hidden]", note="RMSNorm gain before attention"),
+        Active("q_weight", "[q_out, hidden]"),
+        Active("k_weight", "[kv_out, hidden]", note="fewer heads than q under GQA"),
+        Active("v_weight", "[kv_out, hidden]"),
+        Active("o_weight", "[hidden, q_out]"),
+        Active("post_norm_weight", "[hidden]", note="RMSNorm gain before the MLP"),
+        Active("gate_weight", "[intermediate, hidden]"),
+        Active("up_weight", "[intermediate, hidden]"),
+        Active("down_weight", "[hidden, intermediate]"),
+        Inactive("cos", "[T, head_dim]", note="rotary table, duplicated halves"),
+        Inactive("sin", "[T, head_dim]", note="rotary table, duplicated halves"),
+        Inactive("eps", default=1e-5),
+    ),
+    output=Active("out", "[B, T, hidden]"),
+    forward_semantics=(
+        "One Llama-3 decoder layer over x [batch, tokens, hidden]: RMSNorm -> Q/K/V "
+        "projections -> half-rotated RoPE on Q and K -> causal grouped-query attention -> "
+        "output projection -> residual add -> RMSNorm -> SwiGLU MLP (silu(gate) * up, then "
+        "down) -> residual add. Weights in nn.Linear [out, in] orientation; head counts "
+        "q_out // head_dim and kv_out // head_dim. RMSNorm statistics, the SiLU and the "
+        "attention softmax in fp32; causal; no KV cache, no dropout."
+    ),
+    backward_semantics=(
+        "Gradients of all ten Active inputs in declaration order: dx, dinput_norm_weight, "
+        "dq_weight, dk_weight, dv_weight, do_weight, dpost_norm_weight, dgate_weight, "
+        "dup_weight, ddown_weight; dx accumulates the two residual paths and the norm "
+        "inputs; key/value gradients summed over each query group; reductions in fp32."
+    ),
+    correctness=(
+        Workload(dims=_LAYER_SMALL, dtype="float32", atol=1e-4, rtol=1e-4),
+        Workload(dims=_LAYER_SMALL_2, dtype="float32", atol=1e-4, rtol=1e-4),
+        Workload(dims=_LAYER_SMALL, dtype="bfloat16"),
+        Workload(dims=_LAYER_SMALL_2, dtype="bfloat16"),
+    ),
+    benchmark=tuple(
+        Workload(dims=_llama3_8b_layer(t), dtype="bfloat16", label=f"llama3_8b_T{t}")
+        for t in (1024, 2048, 4096)
+    ),
+    tolerances={"float32": (1e-4, 1e-4), "bfloat16": (5e-2, 2e-2)},
+    tolerance_multipliers={
+        "dk_weight": (1.5, 1.0),
+        "dv_weight": (1.5, 1.0),
+        "ddown_weight": (1.5, 1.0),
+    },
+    make_inputs="evograd_amd.inputs:make_llama3_decoder_layer_inputs",
+    memory_inputs=("x", "input_norm_weight", "q_weight", "k_weight", "v_weight", "o_weight",
+                   "post_norm_weight", "gate_weight", "up_weight", "down_weight"),
+    regime_feature=_layer_tokens_feature,
+    regime_split=LLAMA_REGIME_SPLIT,
+)
+
 OPS: dict[str, OpDecl] = {
     op.name: op
     for op in (SOFTMAX, RMSNORM, LAYERNORM, SWIGLU, ROPE, CAUSAL_ATTENTION, FUSED_ADD_RMS_NORM,
-               CAUSAL_ATTENTION_GQA, LLAMA3_ATTENTION, CROSS_ENTROPY, FUSED_LINEAR_CROSS_ENTROPY)
+               CAUSAL_ATTENTION_GQA, LLAMA3_ATTENTION, CROSS_ENTROPY, FUSED_LINEAR_CROSS_ENTROPY,
+               LLAMA3_DECODER_LAYER)
 }
 
 

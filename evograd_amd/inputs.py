@@ -211,6 +211,52 @@ def make_flce_inputs(op, workload, device="cuda"):
     return {"x": x, "weight": weight, "target": target, "dloss": dloss}
 
 
+def make_llama3_decoder_layer_inputs(op, workload, device="cuda"):
+    """llama3_decoder_layer/__init__.py:68-133: seed T*100003 + hidden*1009 + head_dim;
+    drawn in this order: x = 0.5 N(0,1) [B, T, hidden]; input_norm_weight = 1 + 0.1
+    N(0,1) (fp32 draw, cast); q/k/v/o weights N(0,1) * in^-0.5 (fp32 draw, cast,
+    [out, in]); post_norm_weight; gate, up, down weights; then dout = 0.5 N(0,1) *
+    (B*T)^-0.5. cos/sin [T, head_dim] at Llama-3's theta in x's dtype; eps 1e-5.
+    The shape checks of :73-86 are kept (q_out, kv_out multiples of head_dim, whole
+    GQA groups, q_out == hidden)."""
+    d = workload.dims
+    batch, tokens, hidden = d["B"], d["T"], d["hidden"]
+    head_dim, q_out, kv_out, inter = d["head_dim"], d["q_out"], d["kv_out"], d["intermediate"]
+    if q_out % head_dim or kv_out % head_dim:
+        raise ValueError("q_out and kv_out must be whole multiples of head_dim")
+    n_heads, n_kv = q_out // head_dim, kv_out // head_dim
+    if n_heads % n_kv:
+        raise ValueError(f"GQA needs n_heads divisible by n_kv_heads, got {n_heads} and {n_kv}")
+    if q_out != hidden:
+        raise ValueError("Llama-3 ties n_heads*head_dim to hidden")
+    dt = resolve_dtype(workload.dtype)
+    torch.manual_seed(tokens * 100003 + hidden * 1009 + head_dim)
+
+    def weight(out_features, in_features):
+        return (torch.randn((out_features, in_features), device=device, dtype=torch.float32)
+                * in_features ** -0.5).to(dt)
+
+    def gain(width):
+        return (1.0 + 0.1 * torch.randn((width,), device=device, dtype=torch.float32)).to(dt)
+
+    out = {"x": torch.randn((batch, tokens, hidden), device=device, dtype=dt) * 0.5}
+    out["input_norm_weight"] = gain(hidden)
+    out["q_weight"] = weight(q_out, hidden)
+    out["k_weight"] = weight(kv_out, hidden)
+    out["v_weight"] = weight(kv_out, hidden)
+    out["o_weight"] = weight(hidden, q_out)
+    out["post_norm_weight"] = gain(hidden)
+    out["gate_weight"] = weight(inter, hidden)
+    out["up_weight"] = weight(inter, hidden)
+    out["down_weight"] = weight(hidden, inter)
+    theta = float(workload.extra.get("theta", LLAMA3_ROPE_THETA))
+    out["cos"], out["sin"] = rope_tables(tokens, head_dim, theta, dt, device)
+    out["eps"] = 1e-5
+    out["dout"] = (torch.randn((batch, tokens, hidden), device=device, dtype=dt) * 0.5
+                   * (batch * tokens) ** -0.5)
+    return out
+
+
 RECIPES = {
     "make_softmax_inputs": make_softmax_inputs,
     "make_rmsnorm_inputs": make_rmsnorm_inputs,
@@ -223,6 +269,7 @@ RECIPES = {
     "make_llama3_attention_inputs": make_llama3_attention_inputs,
     "make_cross_entropy_inputs": make_cross_entropy_inputs,
     "make_flce_inputs": make_flce_inputs,
+    "make_llama3_decoder_layer_inputs": make_llama3_decoder_layer_inputs,
 }
 
 

@@ -116,6 +116,9 @@ class OpDecl:
     correctness: tuple = ()
     benchmark: tuple = ()
     tolerances: dict = field(default_factory=dict)
+    # Per-result (atol, rtol) factors applied to the base tolerance before the hook
+    # (activity.py:245, :524-525).
+    tolerance_multipliers: dict = field(default_factory=dict)
     tolerance_hook: Callable | None = None
     make_inputs: str | None = None
     memory_inputs: tuple | None = None
@@ -161,6 +164,8 @@ class OpDecl:
             atol, rtol = workload.atol, workload.rtol
         else:
             atol, rtol = self.tolerances[workload.dtype]
+        scale = self.tolerance_multipliers.get(result_name or "", (1.0, 1.0))
+        atol, rtol = atol * scale[0], rtol * scale[1]
         if self.tolerance_hook is not None:
             atol, rtol = self.tolerance_hook(workload, result_name, atol, rtol)
         return float(atol), float(rtol)
@@ -193,6 +198,14 @@ class OpDecl:
                 raise ValueError(f"{self.name}: workload {w.dims} misses dims {sorted(missing)}")
             if w.atol is None and w.dtype not in self.tolerances:
                 raise ValueError(f"{self.name}: no tolerance for dtype {w.dtype}")
+        unknown = set(self.tolerance_multipliers) - set(self.grad_names())
+        if unknown:
+            raise ValueError(f"{self.name}: tolerance multipliers name unknown gradients "
+                             f"{sorted(unknown)}")
+        for name, factors in self.tolerance_multipliers.items():
+            if len(factors) != 2 or any(f <= 0 for f in factors):
+                raise ValueError(f"{self.name}: tolerance multiplier for {name} must be two "
+                                 "positive values")
         for name in self.backward_may_overwrite:
             if name not in [a.name for a in self.active_args()]:
                 raise ValueError(f"{self.name}: backward_may_overwrite names non-Active {name!r}")

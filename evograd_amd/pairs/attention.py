@@ -30,15 +30,19 @@ from evograd_amd.pairs._util import as_contiguous, tag, workspace
 
 
 def check_operands(q, k, v) -> None:
-    """dtype and head_dim rules the MFMA kernels share (MHA and GQA)."""
+    """dtype and head_dim rules of the attention entry points (MHA and GQA): fp32,
+    bf16 or fp16, an even head_dim up to 128. bf16/fp16 at head_dim 64 or 128 run on
+    the MFMA kernels, every other case on the library's generic fp32 kernels."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError(f"attention expects 4-d [B, heads, S, D] tensors; got "
                          f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
-    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise TypeError(f"attention supports bfloat16/float16 only, got "
+    if (q.dtype not in (torch.float32, torch.bfloat16, torch.float16) or k.dtype != q.dtype
+            or v.dtype != q.dtype):
+        raise TypeError(f"attention supports float32/bfloat16/float16, got "
                         f"{q.dtype}/{k.dtype}/{v.dtype}")
-    if q.shape[-1] not in (64, 128):
-        raise ValueError(f"head_dim must be 64 or 128, got {q.shape[-1]}")
+    D = q.shape[-1]
+    if D < 2 or D > 128 or D % 2:
+        raise ValueError(f"head_dim must be even and at most 128, got {D}")
 
 
 def causal_attention_forward_with_saved(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):

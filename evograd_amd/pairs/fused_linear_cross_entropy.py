@@ -5,14 +5,16 @@ Replaces fused_linear_cross_entropy_forward_ref
 hard-label cross entropy of ``x @ weight.T`` against ``target``, ignore_index -100,
 projection and logsumexp accumulated in fp32) under the contract of
 fused_linear_cross_entropy/__init__.py:91-152: the ``[rows, vocab]`` logits are never
-materialised in full. One C entry point (``eg_flce_fwd``) runs the whole pass on
-this library's kernels: for 16-bit inputs the MFMA logits product (``gemm.hip``)
-forms the softmax terms in its epilogue (``exp(logit - group max)`` per 128-column
-group, with the group sums and the target logit, all from the fp32 accumulators),
-one pass per row turns them into the logsumexp, the row loss and the unit gradient
-``softmax - onehot`` in the input dtype, then ``dx = dlogits @ weight`` and
-``dweight = dlogits.T @ x`` and the mean loss. fp32 inputs take fp32 logits chunks
-and separate logsumexp and gradient passes.
+materialised in full, and neither is ``dlogits`` (its ``backward_semantics``: "dlogits
+must not be materialized in full either"). One C entry point (``eg_flce_fwd``) runs
+the whole pass on this library's kernels, one chunk of rows at a time: for 16-bit
+inputs the MFMA logits product (``gemm.hip``) forms the softmax terms in its
+epilogue (``exp(logit - group max)`` per 128-column group, with the group sums and
+the target logit, all from the fp32 accumulators), one pass per row turns them into
+the logsumexp, the row loss and the chunk's unit gradient ``softmax - onehot`` in
+the input dtype, then ``dx_c = dl_c @ weight`` and ``dweight += dl_c.T @ x_c`` (the
+product's epilogue adds the running sum in fp32), and at the end the mean loss.
+fp32 inputs take fp32 logits chunks and separate logsumexp and gradient passes.
 
 The gradient is formed in the forward because the backward's only input is the
 scalar ``dloss``: the backward (``eg_scale_copy``) scales the saved unit gradients
@@ -20,11 +22,13 @@ by ``dloss / n_valid``. The loss is fp32, as the reference's forward returns it.
 Saved state: ``(dx, dweight, n_valid)`` — the gradients in the inputs' dtypes and
 one fp32 count, nothing of size rows x vocab.
 
-Scratch (freed when the forward returns): the unit gradient of every row in the
-input dtype, plus the group statistics of one chunk (16-bit inputs: one chunk of
-all rows by default) or one chunk of fp32 logits (fp32 inputs: at most 2^29).
-16-bit inputs whose hidden size is not a multiple of 64 (the product's k step) are
-copied into zero-padded buffers first.
+Scratch (freed when the forward returns): the unit gradient of one chunk in the
+input dtype, plus the group statistics of one chunk (16-bit inputs) or one chunk
+of fp32 logits (fp32 inputs), and two fp32 values per row. By default a chunk holds
+as many rows as 1 GiB of dlogits allows (4096 rows at the Llama-3 vocabulary in
+bf16), so scratch grows with the chunk, not with rows x vocab. 16-bit inputs whose
+hidden size is not a multiple of 64 (the product's k step) are copied into
+zero-padded buffers first.
 """
 
 from __future__ import annotations
@@ -46,7 +50,7 @@ from evograd_amd.pairs._util import as_contiguous, tag, workspace
 
 IGNORE_INDEX = -100
 # Logits per chunk when set; None leaves the split to the library (chunk_rows 0):
-# one chunk for 16-bit inputs, 2^29 fp32 logits per chunk for fp32 inputs.
+# as many rows per chunk as 1 GiB of dlogits allows.
 CHUNK_ELEMS = None
 
 

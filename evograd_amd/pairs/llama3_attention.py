@@ -46,10 +46,19 @@ def _tables(q, cos, sin):
             as_contiguous("sin", sin.to(torch.float32)))
 
 
+def _check_mfma(q):
+    """The fused RoPE -> attention kernels are the MFMA ones: bf16/fp16, head_dim 64
+    or 128."""
+    if q.dtype not in (torch.bfloat16, torch.float16) or q.shape[-1] not in (64, 128):
+        raise ValueError(f"llama3_attention: bfloat16/float16 with head_dim 64 or 128, got "
+                         f"{q.dtype} at head_dim {q.shape[-1]}")
+
+
 def llama3_attention_forward_with_saved(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                         cos: torch.Tensor, sin: torch.Tensor):
     _lib.require_gpu("llama3_attention_forward_with_saved", q, k, v, cos, sin)
     group_size(q, k, v)
+    _check_mfma(q)
     cos, sin = _tables(q, cos, sin)
     q, k, v = (as_contiguous(n, t) for n, t in (("q", q), ("k", k), ("v", v)))
     B, H, S, D = q.shape

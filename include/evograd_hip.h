@@ -184,8 +184,11 @@ int eg_rope(const void* q, const void* k, void* q_out, void* k_out, const void* 
  * Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True) as used by
  * src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:107:
  *   o = softmax(q k^T * scale + causal mask) v
- * q, k, v, o [batch, heads, seq, head_dim] (EG_BF16 or EG_F16); lse [batch, heads, seq]
- * fp32 = logsumexp of the scaled, masked scores (saved). head_dim must be 64 or 128. */
+ * q, k, v, o [batch, heads, seq, head_dim]; lse [batch, heads, seq] fp32 = logsumexp
+ * of the scaled, masked scores (saved). bf16/fp16 at head_dim 64 or 128 run on MFMA;
+ * fp32, and any other even head_dim up to 128, on plain fp32 arithmetic (the shapes
+ * of the decoder layer's correctness gate,
+ * src/evograd/ops/level3/llama3_decoder_layer/__init__.py:55-65). */
 int eg_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float scale,
                 int dtype, void* stream);
@@ -285,22 +288,27 @@ int eg_cross_entropy_mean(const int64_t* target, const float* rowloss, void* los
  * Replaces fused_linear_cross_entropy_forward_ref
  * (src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35) and
  * forms its gradient (declared at fused_linear_cross_entropy/__init__.py:91-152)
- * in the same pass, every product on this library's MFMA kernels:
- *   logits = x @ weight.T (fp32 accumulation; 16-bit inputs: the softmax terms are
- *            formed in the product's epilogue and no fp32 logits are stored, one
- *            chunk of all rows by default; fp32 inputs: fp32 logits in row chunks of
- *            at most 2^29)
+ * in the same pass, one chunk of rows at a time, every product on this library's
+ * MFMA kernels:
+ *   logits_c = x_c @ weight.T (fp32 accumulation; 16-bit inputs: the softmax terms
+ *            are formed in the product's epilogue and no fp32 logits are stored;
+ *            fp32 inputs: one chunk of fp32 logits)
  *   loss = mean over rows with target != ignore_index of lse - logits[target] (fp32)
- *   dl = softmax(logits) - onehot(target) (dtype; zero on ignored rows)
- *   dx = dl @ weight, dweight = dl.T @ x   (dtype: the unit gradients)
+ *   dl_c = softmax(logits_c) - onehot(target) (dtype; zero on ignored rows)
+ *   dx_c = dl_c @ weight; dweight = sum over chunks of dl_c.T @ x_c (16-bit inputs
+ *            over several chunks: summed in an fp32 [vocab, hidden] buffer of the
+ *            workspace and rounded once; fp32 inputs: summed in dweight)
  *   n_valid = the number of counted rows (fp32)
+ * Neither the logits nor dl of all rows exist at once: the workspace
+ * (eg_flce_workspace_bytes, same chunk_rows and dtype) holds dl of one chunk, the
+ * softmax group statistics of one chunk (16-bit) or one chunk of fp32 logits
+ * (fp32), two fp32 values per row and, for 16-bit inputs over more than one
+ * chunk, the fp32 dweight sum. chunk_rows <= 0 takes the default: as many rows as
+ * 1 GiB of dl allows.
  * x [rows, hidden], weight [vocab, hidden], dx, dweight as their inputs (dtype);
  * target int64 [rows]; a target outside [0, vocab) that is not ignore_index
  * gives NaN. 16-bit inputs need hidden % 64 == 0. The backward scales dx and
- * dweight by dloss / n_valid (eg_scale_copy). chunk_rows <= 0 takes the default
- * chunking; the workspace (eg_flce_workspace_bytes, same chunk_rows and dtype) holds
- * the dlogits of every row and either the softmax group statistics of one chunk
- * (16-bit) or the fp32 logits of one chunk (fp32). */
+ * dweight by dloss / n_valid (eg_scale_copy). */
 size_t eg_flce_workspace_bytes(int64_t rows, int64_t hidden, int64_t vocab, int64_t chunk_rows,
                                int dtype);
 int eg_flce_fwd(const void* x, const void* weight, const int64_t* target, float* loss, void* dx,
@@ -319,17 +327,55 @@ int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int6
 /* ------------------------------------------------------------ dense product
  * The products inside fused_linear_cross_entropy (the logits x @ weight.T of
  * src/evograd/ops/level2/fused_linear_cross_entropy/forward_ref.py:23-35 and the
- * dx = dlogits @ weight, dweight = dlogits.T @ x of its gradient), on MFMA:
- *   c[m][n] = sum_k a(m, k) b(k, n)   (fp32 accumulation; bf16/fp16 operands on
- *                                      MFMA, fp32 operands on a plain tiled path)
+ * dx = dlogits @ weight, dweight = dlogits.T @ x of its gradient) and inside the
+ * Llama-3 decoder layer (the F.linear projections and residual adds of
+ * src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:91-117 and their
+ * gradients), on MFMA:
+ *   c[m][n] = r[m][n] + sum_k a(m, k) b(k, n)   (fp32 accumulation; bf16/fp16
+ *             operands on MFMA, fp32 operands on a plain tiled path; r may be NULL
+ *             for none, and r == c with ldr == ldc accumulates in place)
  * a_k_contiguous: a(m, k) = a[m * lda + k], else a[k * lda + m];
  * b_k_contiguous: b(k, n) = b[n * ldb + k], else b[k * ldb + n];
- * c [m][ldc] in c_dtype (EG_F32 or dtype). A k-contiguous operand needs k % 64 == 0
- * (pad its rows with zeros); strides are multiples of 8 elements and a, b are
+ * c [m][ldc] and r [m][ldr] in c_dtype (EG_F32 or dtype); r is added in fp32
+ * before c is rounded. A 16-bit k-contiguous operand needs k % 64 == 0, or, when the
+ * other operand is k-major, a row stride of at least k rounded up to 64 whose columns
+ * past k hold finite values (zeros); strides are multiples of 8 elements and a, b are
  * 16-byte aligned. */
-int eg_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
-            int64_t lda, int64_t ldb, int64_t ldc, int a_k_contiguous, int b_k_contiguous,
-            int dtype, int c_dtype, void* stream);
+int eg_gemm(const void* a, const void* b, void* c, const void* r, int64_t m, int64_t n,
+            int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t ldr, int a_k_contiguous,
+            int b_k_contiguous, int dtype, int c_dtype, void* stream);
+
+/* ---------------------------------------------- decoder layer: layout, adds
+ * The steps of the Llama-3 decoder layer
+ * (src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:91-117) between its
+ * products (eg_gemm), norms (eg_rmsnorm_*) and attention (eg_attn_gqa_*).
+ *
+ * eg_split_heads: src [batch * tokens, ld] (each token row holds heads x head_dim
+ * values from column 0) -> dst [batch, heads, tokens, head_dim]: the
+ * .view(batch, tokens, heads, head_dim).transpose(1, 2) of :94-96. rope = 1 also
+ * applies _apply_rope (:43-47, :98-99): y = x cos + [-x2, x1] sin in fp32, cast
+ * back, with cos, sin [tokens, head_dim] of table_dtype (EG_F32 or dtype); rope = 0
+ * copies (tables may be NULL).
+ * eg_merge_heads: the inverse layout change, src [batch, heads, tokens, head_dim] ->
+ * dst [batch * tokens, ld] (attn.transpose(1, 2).reshape(...) of :109); rope = 2
+ * applies the rotation's transpose dx = dy cos + [dy2, -dy1] sin on the way (the
+ * gradient of the rotated q and k), rope = 0 copies. Columns of dst past
+ * heads x head_dim are not written. */
+int eg_split_heads(const void* src, void* dst, const void* cos, const void* sin, int64_t batch,
+                   int64_t tokens, int64_t heads, int64_t head_dim, int64_t ld, int rope,
+                   int table_dtype, int dtype, void* stream);
+int eg_merge_heads(const void* src, void* dst, const void* cos, const void* sin, int64_t batch,
+                   int64_t tokens, int64_t heads, int64_t head_dim, int64_t ld, int rope,
+                   int table_dtype, int dtype, void* stream);
+
+/* c = a + b over n elements (fp32 sum, one rounding): where a residual
+ * connection's gradient meets a norm's (forward_ref.py:110 and :117, backward). */
+int eg_add(const void* a, const void* b, void* c, int64_t n, int dtype, void* stream);
+
+/* out = (silu(gate.float()) * up.float()).to(dtype) over n elements, one rounding:
+ * the MLP activation of forward_ref.py:115-116 (unlike the level-1 SwiGLU, which
+ * rounds silu first). Its backward is eg_swiglu_bwd's formula. */
+int eg_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -174,6 +174,75 @@ def fused_linear_cross_entropy_forward_ref(x: torch.Tensor, weight: torch.Tensor
     return F.cross_entropy(logits, target, reduction="mean")
 
 
+def _layer_rms_norm(x, weight, eps):
+    """The decoder layer's RMSNorm (llama3_decoder_layer/forward_ref.py:36-40): fp32
+    statistics, x * rrms cast back to x's dtype, then the gain in that dtype."""
+    x32 = x.float()
+    rrms = torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)
+    return ((x32 * rrms).to(x.dtype)) * weight
+
+
+def _layer_rms_norm_fused(x, weight, eps):
+    """forward_ref.py:131-133: PyTorch's fused RMSNorm."""
+    return F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
+
+
+def _layer_rope(x, cos, sin):
+    """forward_ref.py:43-47: rotate-half RoPE in fp32, cast back."""
+    x32 = x.float()
+    return (x32 * cos[None, None].float() + _rotate_half(x32) * sin[None, None].float()).to(
+        x.dtype)
+
+
+def _llama3_decoder_layer(rms_norm, x, input_norm_weight, q_weight, k_weight, v_weight,
+                          o_weight, post_norm_weight, gate_weight, up_weight, down_weight,
+                          cos, sin, eps=1e-5):
+    """One Llama-3 decoder layer, restating
+    src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:53-117: RMSNorm ->
+    Q/K/V projections -> RoPE on q and k -> causal GQA attention (kv heads repeated
+    over each query group) -> output projection -> residual -> RMSNorm -> SwiGLU MLP
+    (silu in fp32, one rounding) -> residual. Weights in nn.Linear [out, in]
+    orientation; head counts from q_out // head_dim and kv_out // head_dim."""
+    batch, tokens, hidden = x.shape
+    head_dim = cos.shape[-1]
+    n_heads = q_weight.shape[0] // head_dim
+    n_kv_heads = k_weight.shape[0] // head_dim
+    if q_weight.shape[0] % head_dim or k_weight.shape[0] % head_dim:
+        raise ValueError("q_out and kv_out must be whole multiples of head_dim")
+    if n_heads % n_kv_heads:
+        raise ValueError(f"GQA needs n_heads divisible by n_kv_heads, got {n_heads} and "
+                         f"{n_kv_heads}")
+    h = rms_norm(x, input_norm_weight, eps)
+    q = F.linear(h, q_weight).view(batch, tokens, n_heads, head_dim).transpose(1, 2)
+    k = F.linear(h, k_weight).view(batch, tokens, n_kv_heads, head_dim).transpose(1, 2)
+    v = F.linear(h, v_weight).view(batch, tokens, n_kv_heads, head_dim).transpose(1, 2)
+    q = _layer_rope(q, cos, sin)
+    k = _layer_rope(k, cos, sin)
+    repeat = n_heads // n_kv_heads
+    if repeat > 1:
+        k = k.repeat_interleave(repeat, dim=1)
+        v = v.repeat_interleave(repeat, dim=1)
+    attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    attn = attn.transpose(1, 2).reshape(batch, tokens, n_heads * head_dim)
+    x = x + F.linear(attn, o_weight)
+    h = rms_norm(x, post_norm_weight, eps)
+    gate = F.linear(h, gate_weight)
+    up = F.linear(h, up_weight)
+    act = (F.silu(gate.float()) * up.float()).to(h.dtype)
+    return x + F.linear(act, down_weight)
+
+
+def llama3_decoder_layer_forward_ref(*args, **kwargs):
+    """The definition, norms spelled out in primitives (forward_ref.py:136-142)."""
+    return _llama3_decoder_layer(_layer_rms_norm, *args, **kwargs)
+
+
+def llama3_decoder_layer_runtime_ref(*args, **kwargs):
+    """The same layer with PyTorch's fused RMSNorm, timed as the eager baseline
+    (forward_ref.py:145-152)."""
+    return _llama3_decoder_layer(_layer_rms_norm_fused, *args, **kwargs)
+
+
 FORWARDS = {
     "softmax_forward_ref": softmax_forward_ref,
     "rmsnorm_forward_ref": rmsnorm_forward_ref,
@@ -192,4 +261,6 @@ FORWARDS = {
     "llama3_attention_runtime_ref": llama3_attention_runtime_ref,
     "cross_entropy_forward_ref": cross_entropy_forward_ref,
     "fused_linear_cross_entropy_forward_ref": fused_linear_cross_entropy_forward_ref,
+    "llama3_decoder_layer_forward_ref": llama3_decoder_layer_forward_ref,
+    "llama3_decoder_layer_runtime_ref": llama3_decoder_layer_runtime_ref,
 }

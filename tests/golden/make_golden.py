@@ -94,6 +94,26 @@ def flce(x, weight, target):
     return cross_entropy(x @ weight.T, target)
 
 
+def decoder_layer(x, input_norm_weight, q_weight, k_weight, v_weight, o_weight,
+                  post_norm_weight, gate_weight, up_weight, down_weight, cos, sin, eps=1e-5):
+    """One Llama-3 decoder layer in fp64: x [B, T, hidden], weights [out, in]."""
+    B, T, hid = x.shape
+    D = cos.shape[-1]
+    H, KVH = q_weight.shape[0] // D, k_weight.shape[0] // D
+
+    def heads(lin, n):
+        return lin.reshape(B, T, n, D).transpose(0, 2, 1, 3)
+
+    h1 = rmsnorm(x, input_norm_weight, eps)
+    q = rope(heads(h1 @ q_weight.T, H), cos, sin)
+    k = rope(heads(h1 @ k_weight.T, KVH), cos, sin)
+    v = heads(h1 @ v_weight.T, KVH)
+    attn = causal_attention(q, k, v).transpose(0, 2, 1, 3).reshape(B, T, H * D)
+    x1 = x + attn @ o_weight.T
+    h2 = rmsnorm(x1, post_norm_weight, eps)
+    return x1 + swiglu(h2 @ gate_weight.T, h2 @ up_weight.T) @ down_weight.T
+
+
 # --------------------------------------------------------------- gradients
 def fd_grads(f, inputs: dict, active, dy, h=1e-6):
     """d<dy, f>/d input for every Active input, by central differences."""
@@ -178,6 +198,27 @@ def main():
           "v": draw(rng, (1, 2, 5, 64)), "cos": cos, "sin": sin}
     save("llama3_attention", la, ["q", "k", "v"], draw(rng, (1, 4, 5, 64)),
          lambda q, k, v, cos, sin: causal_attention(rope(q, cos, sin), rope(k, cos, sin), v))
+
+    # one decoder layer: B=1, T=3, hidden 8, head_dim 4, two query heads over one kv
+    # head, intermediate 12; weights at fan-in scale, gains near 1
+    hid, D, qo, kvo, inter, T = 8, 4, 8, 4, 12, 3
+    cos, sin = rope_tables(T, D, 500000.0)
+    layer = {
+        "x": draw(rng, (1, T, hid), 0.5),
+        "input_norm_weight": bf16_exact(1 + 0.1 * rng.standard_normal(hid)),
+        "q_weight": draw(rng, (qo, hid), hid ** -0.5),
+        "k_weight": draw(rng, (kvo, hid), hid ** -0.5),
+        "v_weight": draw(rng, (kvo, hid), hid ** -0.5),
+        "o_weight": draw(rng, (hid, qo), qo ** -0.5),
+        "post_norm_weight": bf16_exact(1 + 0.1 * rng.standard_normal(hid)),
+        "gate_weight": draw(rng, (inter, hid), hid ** -0.5),
+        "up_weight": draw(rng, (inter, hid), hid ** -0.5),
+        "down_weight": draw(rng, (hid, inter), inter ** -0.5),
+        "cos": cos, "sin": sin,
+    }
+    save("llama3_decoder_layer", layer, [n for n in layer if n not in ("cos", "sin")],
+         draw(rng, (1, T, hid), 0.5),
+         lambda **kw: decoder_layer(**kw, eps=1e-5), {"eps": 1e-5})
 
 
 if __name__ == "__main__":

@@ -10,8 +10,9 @@ from evograd_amd import decls
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "fused_add_rms_norm",
        "causal_attention", "causal_attention_gqa", "llama3_attention", "cross_entropy",
-       "fused_linear_cross_entropy")
-TABLE_ARGS = {"rope": ("cos", "sin"), "llama3_attention": ("cos", "sin")}
+       "fused_linear_cross_entropy", "llama3_decoder_layer")
+TABLE_ARGS = {"rope": ("cos", "sin"), "llama3_attention": ("cos", "sin"),
+              "llama3_decoder_layer": ("cos", "sin")}
 
 
 def load(op_name: str) -> dict:

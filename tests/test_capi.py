@@ -51,6 +51,41 @@ def test_library_loads_and_exports_every_symbol():
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_flce_scratch_grows_with_the_chunk_not_with_rows_times_vocab():
+    """The fused linear cross entropy holds the dlogits of one row chunk at a time
+    (fused_linear_cross_entropy/__init__.py: "dlogits must not be materialized in
+    full"): at the Llama-3 lm_head size its scratch is one chunk of dlogits, one
+    chunk of group statistics, 12 bytes per row and, over several chunks, the fp32
+    dweight sum, whatever the row count."""
+    vocab, hidden, bf16 = 128256, 4096, _lib.EG_BF16
+
+    def al(n):
+        return (n + 255) // 256 * 256
+
+    def expect(rows, rc):
+        nh2 = 2 * ((vocab + 255) // 256)
+        acc = al(vocab * hidden * 4) if rows > rc else 0  # the fp32 dweight sum
+        return al(rows * 8) + al(rows * 4) + al(rc * nh2 * 8) + al(rc * vocab * 2) + acc
+
+    ws = lambda rows, rc: _lib.query("eg_flce_workspace_bytes", rows, hidden, vocab, rc, bf16)
+    # default: as many rows as 1 GiB of dlogits allows, a multiple of 256 -> 4096
+    assert ws(8192, 0) == expect(8192, 4096)
+    assert ws(65536, 0) == expect(65536, 4096)
+    assert ws(65536, 0) - ws(8192, 0) == al(65536 * 8) + al(65536 * 4) - al(8192 * 8) - al(8192 * 4)
+    # one chunk of dlogits (at most 1 GiB) and a weight-sized fp32 sum, nothing rows x vocab
+    assert ws(8192, 0) - al(vocab * hidden * 4) < 1.1 * (1 << 30)
+    # an explicit chunk sets the size; it is capped by the rows
+    assert ws(8192, 1024) == expect(8192, 1024)
+    assert ws(8192, 2048) - ws(8192, 1024) == expect(8192, 2048) - expect(8192, 1024)
+    assert ws(100, 4096) == expect(100, 100)
+    # fp32 inputs: one chunk of fp32 logits and one of fp32 dlogits (2^28 each)
+    f32 = _lib.query("eg_flce_workspace_bytes", 8192, hidden, vocab, 0, _lib.EG_F32)
+    rc32 = (1 << 28) // vocab
+    rc32 = 1 << (rc32.bit_length() - 1)
+    assert f32 == al(8192 * 8) + 2 * al(rc32 * vocab * 4)
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
 def test_host_side_validation_errors_without_gpu():
     """Argument errors are reported before any launch (no device needed)."""
     with pytest.raises(RuntimeError, match="negative"):

@@ -77,9 +77,11 @@ def test_flce_chunked_equals_single_chunk_and_fp64():
         assert ok, f"dx max err {e:.3g}"
         ok, e = _close(dw, ref_dw, 2.0 ** -6)
         assert ok, f"dweight max err {e:.3g}"
-    # the chunk split only reorders fp32 accumulations
-    assert torch.allclose(one[0].float(), many[0].float(), rtol=2 ** -7, atol=1e-7)
-    assert torch.allclose(one[1].float(), many[1].float(), rtol=2 ** -7, atol=1e-7)
+    # dx rows do not depend on the split; dweight takes one more rounding per chunk
+    # (each chunk's product is added to the running sum in fp32, then rounded)
+    assert torch.equal(one[0], many[0])
+    ok, e = _close(many[1], one[1].double(), 2.0 ** -6)
+    assert ok, f"chunked dweight differs from one chunk by {e:.3g}"
     # saved state: the two gradients and one count, nothing rows x vocab
     assert [tuple(t.shape) for t in many_saved] == [(300, 256), (4096, 256), (1,)]
 

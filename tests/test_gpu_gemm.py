@@ -48,8 +48,8 @@ def _operands(M, N, K, akc, bkc, dtype, seed):
 def _run(a, b, M, N, K, lda, ldb, akc, bkc, dtype, cdt):
     ldc = N + 3 if cdt == torch.float32 else _r8(N)
     c = torch.full((M, ldc), float("nan"), device="cuda", dtype=cdt)
-    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, lda, ldb, ldc,
-              int(akc), int(bkc), _lib.dtype_tag(dtype), _lib.dtype_tag(cdt),
+    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), None, M, N, K, lda, ldb,
+              ldc, 0, int(akc), int(bkc), _lib.dtype_tag(dtype), _lib.dtype_tag(cdt),
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return c
@@ -102,5 +102,52 @@ def test_gemm_refuses_unsupported_shapes_on_the_host():
     x = torch.zeros(64, 64, device="cuda", dtype=torch.bfloat16)
     c = torch.zeros(64, 64, device="cuda")
     with pytest.raises(RuntimeError, match="K % 64"):
-        _lib.call("eg_gemm", x.data_ptr(), x.data_ptr(), c.data_ptr(), 64, 64, 40, 64, 64, 64,
-                  1, 1, _lib.EG_BF16, _lib.EG_F32, torch.cuda.current_stream().cuda_stream)
+        _lib.call("eg_gemm", x.data_ptr(), x.data_ptr(), c.data_ptr(), None, 64, 64, 40, 64, 64,
+                  64, 0, 1, 1, _lib.EG_BF16, _lib.EG_F32, torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("cdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("akc,bkc", [(True, True), (False, False), (True, False)])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_gemm_residual_epilogue(cdt, akc, bkc, inplace):
+    """c = r + a b with r added in fp32 before the one rounding of c; r == c
+    accumulates in place (the fused linear cross entropy's dweight over row chunks,
+    the decoder layer's residual adds)."""
+    M, N, K = 300, 520, 128
+    print(f"\n[gpu-gemm] residual {cdt} akc={akc} bkc={bkc} inplace={inplace}", flush=True)
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, torch.bfloat16, 21)
+    ldc = _r8(N) + 8
+    g = torch.Generator(device="cuda").manual_seed(3)
+    r = (torch.randn(M, ldc, device="cuda", generator=g) * 4).to(cdt)
+    r0 = r.clone()
+    if inplace:
+        c, ldr = r, ldc
+    else:
+        c, ldr = torch.full((M, ldc), float("nan"), device="cuda", dtype=cdt), ldc
+    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K, lda,
+              ldb, ldc, ldr, int(akc), int(bkc), _lib.EG_BF16, _lib.dtype_tag(cdt),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = r0[:, :N].double() + A.double() @ B.double()
+    err = (c[:, :N].double() - ref).abs()
+    if cdt == torch.float32:
+        assert err.max().item() <= 4e-6 * K + 1e-6 * ref.abs().max().item()
+    else:
+        assert (err <= 2.0 ** -8 * ref.abs() + 1e-5 * K).all(), err.max().item()
+    # columns past N: untouched (the residual's own values when in place)
+    if inplace:
+        assert torch.equal(c[:, N:], r0[:, N:])
+    else:
+        assert torch.isnan(c[:, N:]).all()
+        assert torch.equal(r, r0)
+
+
+def test_gemm_residual_fp32_path():
+    M, N, K = 70, 90, 33
+    A, B, a, b, lda, ldb = _operands(M, N, K, True, False, torch.float32, 8)
+    r = torch.randn(M, N, device="cuda")
+    c = torch.empty(M, N, device="cuda")
+    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K, lda,
+              ldb, N, N, 1, 0, _lib.EG_F32, _lib.EG_F32, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.allclose(c.double(), r.double() + A.double() @ B.double(), atol=1e-4, rtol=1e-5)

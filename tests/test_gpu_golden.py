@@ -13,7 +13,11 @@ from tests.golden_cases import OPS, assert_close, case_inputs
 
 pytestmark = pytest.mark.gpu
 
-MFMA_ONLY = ("causal_attention", "causal_attention_gqa", "llama3_attention")
+# the fused RoPE -> attention kernels are MFMA-only (bf16/fp16); the layer's golden
+# case has hidden 8, below the 16-bit products' 64-deep k step (its bf16 gates run on
+# the declared correctness workloads, hidden 128 and 64)
+FP32_SKIP = ("llama3_attention",)
+BF16_SKIP = ("llama3_decoder_layer",)
 # (output/gradient rtol, atol as a fraction of the largest expected magnitude)
 BOUNDS = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 1e-2)}
 
@@ -21,7 +25,8 @@ BOUNDS = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 1e-2)}
 def _cases():
     for name in OPS:
         for dt in (torch.float32, torch.bfloat16):
-            if dt == torch.float32 and name in MFMA_ONLY:
+            if (dt == torch.float32 and name in FP32_SKIP) or (dt == torch.bfloat16
+                                                               and name in BF16_SKIP):
                 continue
             yield pytest.param(name, dt, id=f"{name}-{str(dt).split('.')[-1]}")
 

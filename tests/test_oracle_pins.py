@@ -666,3 +666,118 @@ def test_llama3_attention_gradient_fd_and_chain_rule():
                        use_reference_dtype=False)
         assert torch.allclose(g[name], gr["dx"])
     assert torch.allclose(g["dv"], ga["dv"])
+
+
+# ---------------------------------------------------------- llama3 decoder layer
+_LAYER_TINY = dict(B=2, T=5, hidden=16, head_dim=4, q_out=16, kv_out=8, intermediate=24)
+
+
+def _layer_inputs(dims=_LAYER_TINY, theta=100.0):
+    w = Workload(dims=dims, dtype="float32", extra={"theta": theta})
+    return _f64(make_case_inputs(decls.LLAMA3_DECODER_LAYER, w, "cpu"))
+
+
+def _layer_args(inp):
+    return [inp.get(a.name, getattr(a, "default", None)) for a in decls.LLAMA3_DECODER_LAYER.args]
+
+
+def _layer_by_pieces(inp):
+    """The layer assembled from the separately pinned pieces (level-1 RMSNorm, RoPE,
+    grouped attention checked against per-head loops), with the head split and merge
+    written as explicit index loops and the products as explicit matmuls."""
+    x, cos, sin, eps = inp["x"], inp["cos"], inp["sin"], inp["eps"]
+    B, T, hid = x.shape
+    D = cos.shape[-1]
+    H, KVH = inp["q_weight"].shape[0] // D, inp["k_weight"].shape[0] // D
+
+    def heads(lin, n):  # [B, T, n*D] -> [B, n, T, D]
+        out = torch.empty(B, n, T, D, dtype=lin.dtype)
+        for b in range(B):
+            for h in range(n):
+                for t in range(T):
+                    out[b, h, t] = lin[b, t, h * D:(h + 1) * D]
+        return out
+
+    h1 = fr.rmsnorm_forward_ref(x.reshape(B * T, hid), inp["input_norm_weight"], eps)
+    h1 = h1.reshape(B, T, hid)
+    q = fr.rope_forward_ref(heads(h1 @ inp["q_weight"].t(), H), cos, sin)
+    k = fr.rope_forward_ref(heads(h1 @ inp["k_weight"].t(), KVH), cos, sin)
+    v = heads(h1 @ inp["v_weight"].t(), KVH)
+    o = fr.causal_attention_gqa_forward_ref(q, k, v)
+    attn = torch.empty(B, T, H * D, dtype=x.dtype)
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                attn[b, t, h * D:(h + 1) * D] = o[b, h, t]
+    x1 = x + attn @ inp["o_weight"].t()
+    h2 = fr.rmsnorm_forward_ref(x1.reshape(B * T, hid), inp["post_norm_weight"], eps)
+    h2 = h2.reshape(B, T, hid)
+    g, u = h2 @ inp["gate_weight"].t(), h2 @ inp["up_weight"].t()
+    act = g / (1.0 + torch.exp(-g)) * u
+    return x1 + act @ inp["down_weight"].t()
+
+
+def test_llama3_decoder_layer_reduces_to_pinned_pieces():
+    inp = _layer_inputs()
+    out = fr.llama3_decoder_layer_forward_ref(*_layer_args(inp))
+    # the restated forwards evaluate norms, rotations and scores in fp32
+    assert torch.allclose(out, _layer_by_pieces(inp), atol=2e-5)
+    # the eager spelling with F.rms_norm agrees
+    assert torch.allclose(fr.llama3_decoder_layer_runtime_ref(*_layer_args(inp)), out, atol=2e-5)
+    # a single kv head per query head (kv_out == q_out) is plain multi-head attention
+    mha = _layer_inputs(dict(B=1, T=4, hidden=8, head_dim=4, q_out=8, kv_out=8, intermediate=12))
+    assert torch.allclose(fr.llama3_decoder_layer_forward_ref(*_layer_args(mha)),
+                          _layer_by_pieces(mha), atol=2e-5)
+
+
+def test_llama3_decoder_layer_residual_closed_forms():
+    """With Wo = 0 and Wd = 0 both blocks add nothing: out = x exactly, and the
+    gradient flows through the two residuals alone (dx = dout, every other
+    gradient but dWo's and dWd's is zero; dWd = dout^T act)."""
+    inp = _layer_inputs()
+    inp["o_weight"] = torch.zeros_like(inp["o_weight"])
+    inp["down_weight"] = torch.zeros_like(inp["down_weight"])
+    out, g = oracle(decls.LLAMA3_DECODER_LAYER, inp, use_reference_dtype=False)
+    assert torch.equal(out, inp["x"])
+    assert torch.allclose(g["dx"], inp["dout"], atol=1e-12)
+    for name in ("dinput_norm_weight", "dq_weight", "dk_weight", "dv_weight",
+                 "dpost_norm_weight", "dgate_weight", "dup_weight"):
+        assert float(g[name].abs().max()) == 0.0, name
+    x = inp["x"]
+    B, T, hid = x.shape
+    h2 = fr.rmsnorm_forward_ref(x.reshape(B * T, hid), inp["post_norm_weight"], inp["eps"])
+    gt, up = h2 @ inp["gate_weight"].t(), h2 @ inp["up_weight"].t()
+    act = gt / (1.0 + torch.exp(-gt)) * up
+    assert torch.allclose(g["ddown_weight"], inp["dout"].reshape(B * T, hid).t() @ act,
+                          atol=1e-5)
+
+
+def test_llama3_decoder_layer_gradient_fd():
+    _fd_check(decls.LLAMA3_DECODER_LAYER, _layer_inputs())
+    _fd_check(decls.LLAMA3_DECODER_LAYER,
+              _layer_inputs(dict(B=1, T=7, hidden=8, head_dim=8, q_out=8, kv_out=8,
+                                 intermediate=20)))
+
+
+def test_llama3_decoder_layer_inputs_follow_recipe():
+    op = decls.LLAMA3_DECODER_LAYER
+    w = op.correctness[0]
+    d = w.dims
+    inp = make_case_inputs(op, w, "cpu")
+    torch.manual_seed(d["T"] * 100003 + d["hidden"] * 1009 + d["head_dim"])
+    x = torch.randn(d["B"], d["T"], d["hidden"]) * 0.5
+    gain = 1.0 + 0.1 * torch.randn(d["hidden"])
+    wq = torch.randn(d["q_out"], d["hidden"]) * d["hidden"] ** -0.5
+    assert torch.equal(inp["x"], x) and torch.equal(inp["input_norm_weight"], gain)
+    assert torch.equal(inp["q_weight"], wq)
+    assert inp["cos"].shape == (d["T"], d["head_dim"]) and inp["cos"].dtype == torch.float32
+    cos, sin = rope_tables(d["T"], d["head_dim"], 500000.0, torch.float32, "cpu")
+    assert torch.equal(inp["cos"], cos) and torch.equal(inp["sin"], sin)
+    assert inp["eps"] == 1e-5
+    # dout scaled by (B T)^-1/2 (the reference's mean-over-tokens loss scaling)
+    assert 0.3 < float(inp["dout"].std()) * (d["B"] * d["T"]) ** 0.5 / 0.5 < 3.0
+    assert op.grad_names() == ("dx", "dinput_norm_weight", "dq_weight", "dk_weight",
+                               "dv_weight", "do_weight", "dpost_norm_weight", "dgate_weight",
+                               "dup_weight", "ddown_weight")
+    assert op.tolerance_for(op.correctness[2], "dk_weight") == (5e-2 * 1.5, 2e-2)
+    assert op.tolerance_for(op.correctness[0], "dx") == (1e-4, 1e-4)
