@@ -150,6 +150,16 @@ def algorithmic_work(name: str, w, extra_k_heads: int = 0) -> dict:
     raise KeyError(name)
 
 
+def flce_chunk_rows(d: dict) -> int:
+    """Rows per chunk of eg_flce_fwd's default split for 16-bit inputs: as many as
+    1 GiB of dlogits rows (the vocabulary padded to 64) allows, a multiple of 256."""
+    vp = (d["vocab"] + 63) // 64 * 64
+    rc = (1 << 30) // (vp * 2)
+    if rc >= d["rows"]:
+        return d["rows"]
+    return rc // 256 * 256 if rc >= 256 else 1 << (rc.bit_length() - 1)
+
+
 def layer_flops(d: dict) -> dict:
     M = d["B"] * d["T"]
     hid, qo, kvo, inter = d["hidden"], d["q_out"], d["kv_out"], d["intermediate"]
@@ -158,68 +168,27 @@ def layer_flops(d: dict) -> dict:
     return {"fwd": 2.0 * M * P + dense, "bwd": 4.0 * M * P + 5 * dense / 2}
 
 
-# Kernels each entry point launches, in launch order (index = position).
-KERNELS = {
-    "softmax": {"fwd": ["softmax_fwd"], "bwd": ["softmax_bwd"]},
-    "rmsnorm": {"fwd": ["rmsnorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
-    "layernorm": {"fwd": ["layernorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
-    "swiglu": {"fwd": ["swiglu_fwd_kernel"], "bwd": ["swiglu_bwd_kernel"]},
-    "rope": {"fwd": ["rope_kernel"], "bwd": ["rope_kernel"]},
-    "causal_attention": {"fwd": ["attn_fwd_kernel"],
-                         "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
-    "fused_add_rms_norm": {"fwd": ["rmsnorm_fwd_row"], "bwd": ["norm_bwd_ring", "colsum_wide_kernel"]},
-    "causal_attention_gqa": {"fwd": ["attn_fwd_kernel"],
-                             "bwd": ["attn_dq_kernel", "attn_dkdv_kernel"]},
-    # k rotated into the workspace, then the forward rotating q as it loads it;
-    # the backward rotates q and k again before the two attention kernels
-    "llama3_attention": {"fwd": ["rope_kernel", "attn_fwd_kernel"],
-                         "bwd": ["rope_kernel", "attn_dq_kernel", "attn_dkdv_kernel"]},
-    "cross_entropy":{"fwd": ["xent_lse_kernel", "xent_mean_kernel"],
-                      "bwd": ["xent_bwd_flat_kernel"]},
-    # eg_flce_fwd at 8192 rows of 128256 (bf16: one chunk; the vocabulary needs no
-    # column padding): the logits product with its softmax epilogue, the per-row
-    # fix-up (logsumexp, row loss, unit gradient in place), the dx product, the
-    # dweight product and the mean. The backward's two dloss / n scalings.
-    "fused_linear_cross_entropy": {
-        "fwd": ["gemm_kernel(logits)", "flce_fixup_kernel", "gemm_kernel(dx)",
-                "gemm_kernel(dweight)", "xent_mean_kernel"],
-        "bwd": ["scale_copy_kernel(dx)", "scale_copy_kernel(dweight)"]},
-    # bf16 rows of 128256: the forward's x and the backward's y held in registers
-    # as raw packs, one kernel each
-    "softmax@vocab": {"fwd": ["softmax_fwd_lds"], "bwd": ["softmax_bwd_lds"]},
-}
-# The decoder layer's launches at Llama-3-8B widths (no k-padding of the
-# intermediate or kv widths): evograd_amd/pairs/llama3_decoder_layer.py in order.
-_QKV = ["gemm_kernel(q)", "gemm_kernel(k)", "gemm_kernel(v)", "heads_kernel(q,rope)",
-        "heads_kernel(k,rope)", "heads_kernel(v)"]
-_LAYER_KERNELS = {
-    "fwd": ["rmsnorm_fwd_row(h1)", *_QKV, "attn_fwd_kernel", "heads_kernel(o merge)",
-            "gemm_kernel(o,+x)", "rmsnorm_fwd_row(h2)", "gemm_kernel(gate)", "gemm_kernel(up)",
-            "silu_mul_kernel", "gemm_kernel(down,+x1)"],
-    "bwd": ["rmsnorm_fwd_row(h2)", "gemm_kernel(gate)", "gemm_kernel(up)", "silu_mul_kernel",
-            "gemm_kernel(d_act)", "gemm_kernel(dWd)", "swiglu_bwd_kernel", "gemm_kernel(dh2)",
-            "gemm_kernel(dh2+=)", "gemm_kernel(dWg)", "gemm_kernel(dWu)", "norm_bwd_ring(post)",
-            "colsum_wide_kernel(post)", "add_kernel(dx1)", "gemm_kernel(do)", "gemm_kernel(dWo)",
-            "rmsnorm_fwd_row(h1)", *_QKV, "heads_kernel(o split)", "heads_kernel(do split)",
-            "attn_dq_kernel", "attn_dkdv_kernel", "heads_kernel(dq merge,rope)",
-            "heads_kernel(dk merge,rope)", "heads_kernel(dv merge)", "gemm_kernel(dh1)",
-            "gemm_kernel(dh1+=dk)", "gemm_kernel(dh1+=dv)", "gemm_kernel(dWq)",
-            "gemm_kernel(dWk)", "gemm_kernel(dWv)", "norm_bwd_ring(in)", "colsum_wide_kernel(in)",
-            "add_kernel(dx)"],
-}
-for _t in (1024, 2048, 4096):
-    KERNELS[f"{LAYER}@llama3_8b_T{_t}"] = _LAYER_KERNELS
-
-# The kernel whose roofline each op reports, with its algorithmic work per launch.
+# The kernel whose roofline each op reports: (phase, kernel name, occurrence of that
+# name among the phase's launches), with its algorithmic work per launch from
+# dominant_work. Launch sequences are discovered by the timing hook (every launch
+# of a phase is timed and named), so split products and chunk loops need no list.
 DOMINANT = {
-    "softmax": ("bwd", 0), "rmsnorm": ("bwd", 0), "layernorm": ("bwd", 0),
-    "swiglu": ("bwd", 0), "rope": ("fwd", 0), "causal_attention": ("bwd", 1),
-    "fused_add_rms_norm": ("bwd", 0), "causal_attention_gqa": ("bwd", 1),
-    "llama3_attention": ("bwd", 2),
-    "cross_entropy": ("bwd", 0),
-    "fused_linear_cross_entropy": ("fwd", 3),
-    "softmax@vocab": ("bwd", 0),
-    **{f"{LAYER}@llama3_8b_T{t}": ("fwd", 11) for t in (1024, 2048, 4096)},
+    "softmax": ("bwd", "softmax_bwd_reg", 0), "rmsnorm": ("bwd", "norm_bwd_ring", 0),
+    "layernorm": ("bwd", "norm_bwd_ring", 0), "swiglu": ("bwd", "swiglu_bwd_kernel", 0),
+    "rope": ("fwd", "rope_kernel", 0), "causal_attention": ("bwd", "attn_dkdv_kernel", 0),
+    "fused_add_rms_norm": ("bwd", "norm_bwd_ring", 0),
+    "causal_attention_gqa": ("bwd", "attn_dkdv_kernel", 0),
+    "llama3_attention": ("bwd", "attn_dkdv_kernel", 0),
+    "cross_entropy": ("bwd", "xent_bwd_flat_kernel", 0),
+    # eg_flce_fwd at 8192 rows of 128256 (bf16: two chunks of 4096 rows, 1 GiB of
+    # dlogits each): per chunk the logits product (softmax epilogue), the fix-up,
+    # the dx product and the dweight product; the last chunk's dweight product
+    # (adding the fp32 sum of the first) is the 6th product
+    "fused_linear_cross_entropy": ("fwd", "gemm_kernel", 5),
+    # bf16 rows of 128256: the backward's y held in registers as raw packs
+    "softmax@vocab": ("bwd", "softmax_bwd_lds", 0),
+    # the decoder layer's gate projection h2 Wg^T: its 5th product (after q, k, v, o)
+    **{f"{LAYER}@llama3_8b_T{t}": ("fwd", "gemm_kernel", 4) for t in (1024, 2048, 4096)},
 }
 
 
@@ -228,8 +197,8 @@ def dominant_work(name: str, w, work: dict) -> float:
     d = w.dims
     es = {"float32": 4, "float16": 2, "bfloat16": 2}[w.dtype]
     if name == "fused_linear_cross_entropy":
-        # the dweight product: dlogits.T @ x over every row
-        return 2.0 * d["rows"] * d["hidden"] * d["vocab"]
+        # the last chunk's dweight product: dlogits_c.T @ x_c over its rows
+        return 2.0 * flce_chunk_rows(d) * d["hidden"] * d["vocab"]
     if name == "rmsnorm":  # the column sum writes dweight
         return work["bwd"] - d["hidden"] * es
     if name == "fused_add_rms_norm":
@@ -246,9 +215,10 @@ def dominant_work(name: str, w, work: dict) -> float:
 
 
 def kernel_times(name: str, fwd, bwd_call, setup_bwd, state, flush, steps: int) -> dict:
-    """Median microseconds of every kernel of the forward and backward entry
-    points, each timed by events the dispatch records (evograd_amd.timing) on a
-    cold cache."""
+    """Median microseconds of every kernel of the forward and backward calls, each
+    timed by events the dispatch records (evograd_amd.timing) on a cold cache, keyed
+    "phase:index:kernel". Launches are numbered from 0 until an armed index is not
+    reached."""
     import torch
 
     from evograd_amd.timing import KernelTimer
@@ -257,8 +227,8 @@ def kernel_times(name: str, fwd, bwd_call, setup_bwd, state, flush, steps: int) 
     out = {}
     try:
         for phase in ("fwd", "bwd"):
-            for idx, kname in enumerate(KERNELS[name][phase]):
-                samples = []
+            for idx in range(512):
+                samples, label = [], ""
                 for _ in range(steps):
                     if phase == "bwd":
                         setup_bwd()
@@ -268,12 +238,26 @@ def kernel_times(name: str, fwd, bwd_call, setup_bwd, state, flush, steps: int) 
                         fwd()
                     else:
                         bwd_call(state["saved"])
+                    label = timer.label()
+                    if not label:  # the phase launches fewer kernels
+                        timer.fired()
+                        break
                     samples.append(timer.elapsed_ms() * 1e3)
-                out[f"{phase}:{kname}"] = statistics.median(samples)
+                if not samples:
+                    break
+                out[f"{phase}:{idx}:{label}"] = statistics.median(samples)
         torch.cuda.synchronize()
     finally:
         timer.close()
     return out
+
+
+def find_kernel(kt: dict, phase: str, kname: str, occurrence: int) -> str:
+    """Key of the occurrence-th launch of kernel kname in a phase."""
+    hits = [k for k in kt if k.split(":")[0] == phase and k.split(":")[2] == kname]
+    if len(hits) <= occurrence:
+        raise KeyError(f"{phase} has {len(hits)} launches of {kname}, not {occurrence + 1}")
+    return hits[occurrence]
 
 
 # ----------------------------------------------------------------- GPU side
@@ -362,18 +346,18 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
     if base == LAYER:
         out["saved"]["peak_scratch_note"] = ("forward and backward intermediates are "
                                              "torch.empty buffers freed when each call returns")
-    phase, idx = DOMINANT[name]
-    kname = KERNELS[name][phase][idx]
-    k_us = kt[f"{phase}:{kname}"]
+    phase, kname, occurrence = DOMINANT[name]
+    kkey = find_kernel(kt, phase, kname, occurrence)
+    k_us = kt[kkey]
     k_work = dominant_work(base, w, work)
     k_unit = work["unit"]
     if k_unit == "bytes":
         k_rate = k_work / (k_us * 1e-6) / 1e9
-        out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "bytes": k_work,
+        out["dominant_kernel"] = {"name": kkey, "phase": phase, "us": k_us, "bytes": k_work,
                                   "achieved_gbs": k_rate, "frac": k_rate / HBM_PEAK_GBS}
     else:
         k_rate = k_work / (k_us * 1e-6) / 1e12
-        out["dominant_kernel"] = {"name": kname, "phase": phase, "us": k_us, "flops": k_work,
+        out["dominant_kernel"] = {"name": kkey, "phase": phase, "us": k_us, "flops": k_work,
                                   "achieved_tflops": k_rate, "frac": k_rate / BF16_PEAK_TFLOPS}
     mem_inputs = sum(values[n].numel() * values[n].element_size()
                      for n in op.memory_input_names() if n in values and torch.is_tensor(values[n]))

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libevograd_hip.so")
 
 EG_F32, EG_F16, EG_BF16 = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPE_TAG = {
     torch.float32: EG_F32,
@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_last_error": (ctypes.c_char_p, []),
     "eg_time_kernel": (_i32, [_p, _p, _i32]),
     "eg_time_kernel_missed": (_i32, []),
+    "eg_time_kernel_label": (ctypes.c_char_p, []),
     "eg_softmax_fwd": (_i32, [_p, _p, _i64, _i64, _i32, _p]),
     "eg_softmax_bwd": (_i32, [_p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_rmsnorm_fwd": (_i32, [_p, _p, _p, _p, _i64, _i64, _f32, _i32, _p]),
@@ -69,8 +70,9 @@ SIGNATURES: dict[str, tuple] = {
     "eg_flce_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i32]),
     "eg_flce_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p]),
     "eg_scale_copy": (_i32, [_p, _i32, _p, _i32, _i64, _p, _i32, _p, _p]),
+    "eg_gemm_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
     "eg_gemm": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
-                       _i32, _i32, _p]),
+                       _i32, _i32, _p, _size, _p]),
     "eg_split_heads": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
     "eg_merge_heads": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
     "eg_add": (_i32, [_p, _p, _p, _i64, _i32, _p]),

@@ -18,6 +18,19 @@ struct TimingArm {
   bool active = false;
 };
 static thread_local TimingArm g_arm;
+static thread_local char g_label[64] = "";
+
+void set_timed_label(const char* expr) {
+  // "(name<T, ...>)" or "name": keep the identifier
+  while (*expr == '(' || *expr == ' ') ++expr;
+  size_t n = 0;
+  while (n + 1 < sizeof(g_label) &&
+         ((expr[n] >= 'a' && expr[n] <= 'z') || (expr[n] >= 'A' && expr[n] <= 'Z') ||
+          (expr[n] >= '0' && expr[n] <= '9') || expr[n] == '_'))
+    ++n;
+  memcpy(g_label, expr, n);
+  g_label[n] = '\0';
+}
 
 bool timed_launch(hipEvent_t* start, hipEvent_t* stop) {
   if (!g_arm.active) return false;
@@ -79,7 +92,9 @@ extern "C" int eg_time_kernel_missed(void) {
   return missed;
 }
 
-extern "C" int eg_abi_version(void) { return 2; }
+extern "C" int eg_abi_version(void) { return 3; }
+
+extern "C" const char* eg_time_kernel_label(void) { return eg::g_label; }
 
 extern "C" const char* eg_last_error(void) { return eg::g_error; }
 
@@ -91,6 +106,7 @@ extern "C" int eg_time_kernel(void* start_event, void* stop_event, int index) {
   eg::g_arm.start = reinterpret_cast<hipEvent_t>(start_event);
   eg::g_arm.stop = reinterpret_cast<hipEvent_t>(stop_event);
   eg::g_arm.index = index;
+  eg::g_label[0] = '\0';
   eg::g_arm.pending = true;
   eg::g_arm.active = false;
   return 0;

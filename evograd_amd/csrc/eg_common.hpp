@@ -208,6 +208,9 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // True when this launch is the one eg_time_kernel armed for the current call;
 // then *start / *stop are the events to record around it.
 bool timed_launch(hipEvent_t* start, hipEvent_t* stop);
+// Records the kernel expression of the timed launch (its name is kept for
+// eg_time_kernel_label).
+void set_timed_label(const char* kernel_expr);
 
 // Every kernel is launched through EG_LAUNCH: a plain launch, or, for the launch
 // armed by eg_time_kernel, hipExtLaunchKernelGGL with the caller's events, which
@@ -215,10 +218,11 @@ bool timed_launch(hipEvent_t* start, hipEvent_t* stop);
 #define EG_LAUNCH(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                              \
   do {                                                                                \
     hipEvent_t eg_t0_ = nullptr, eg_t1_ = nullptr;                                    \
-    if (::eg::timed_launch(&eg_t0_, &eg_t1_))                                         \
+    if (::eg::timed_launch(&eg_t0_, &eg_t1_)) {                                       \
+      ::eg::set_timed_label(#KERNEL);                                                 \
       hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, eg_t0_, eg_t1_, 0,     \
                             __VA_ARGS__);                                             \
-    else                                                                              \
+    } else                                                                            \
       hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);            \
   } while (0)
 
@@ -232,11 +236,14 @@ int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
 // read as zero. bf16/fp16 operands need k % 64 == 0 for a k-contiguous operand.
 // With r non-null the output is c = r + a b (r of c_dtype, or fp32 with r_f32; row
 // stride ldr; added in fp32 before c is rounded); r == c with ldr == ldc
-// accumulates in place.
+// accumulates in place. With a workspace of at least gemm_workspace_bytes(m, n, k)
+// a product of few output tiles splits k (fp32 partials, a fixed-order sum).
+size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
 int gemm_launch(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
                 int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
                 int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
-                const void* r = nullptr, int64_t ldr = 0, bool r_f32 = false);
+                const void* r = nullptr, int64_t ldr = 0, bool r_f32 = false,
+                void* ws = nullptr, size_t ws_bytes = 0);
 
 // The logits product of the fused linear cross entropy with its softmax terms
 // formed in the epilogue (gemm.hip), 16-bit operands only: for logits = x w^T

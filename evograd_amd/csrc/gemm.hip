@@ -222,7 +222,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                  int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c,
-                 SmxArgs smx, const void* R, int64_t ldr, int r_f32) {
+                 SmxArgs smx, const void* R, int64_t ldr, int r_f32, int kt_per,
+                 float* __restrict__ part) {
   using v8 = typename GM<T>::v8;
   // Two separate buffers per operand, selected at compile time in the unrolled k
   // loop: the LDS reads of one buffer provably do not alias the loads in flight
@@ -241,11 +242,15 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   la.init(lda);
   lb.init(ldb);
   const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
-  const int nk = (K + kBK - 1) / kBK;
+  // Split K (part != nullptr): workgroup row blockIdx.y takes k slices
+  // [kb, kb + kt_per) and writes its fp32 partial tile to part[blockIdx.y].
+  const int nk_all = (K + kBK - 1) / kBK;
+  const int kb = part ? (int)blockIdx.y * kt_per : 0;
+  const int nk = part ? min(nk_all, kb + kt_per) : nk_all;
   // The k loop runs an even number of steps (two per iteration, one per buffer). A
   // slice at or past nk loads through an empty buffer range, which fills its LDS
-  // slots with zeros: the step past K, when nk is odd, adds zeros.
-  const int nk2 = nk + (nk & 1);
+  // slots with zeros: the step past the range, when its length is odd, adds zeros.
+  const int nk2 = kb + (nk - kb) + ((nk - kb) & 1);
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -295,10 +300,10 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
     lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
   };
-  loadA(0, As0);
-  loadB(0, Bs0);
-  loadA(1, As1);
-  __builtin_amdgcn_s_waitcnt(0xF78);  // vmcnt(8): slice 0 has landed
+  loadA(kb, As0);
+  loadB(kb, Bs0);
+  loadA(kb + 1, As1);
+  __builtin_amdgcn_s_waitcnt(0xF78);  // vmcnt(8): slice kb has landed
   bar();
   rd(0, As0, Bs0, 0);
   // Step kt on buffer (as, bs): substeps 0-2 with the B loads of slice kt + 1 (into
@@ -345,13 +350,40 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int kt = 0; kt < nk2; kt += 2) {
+  for (int kt = kb; kt < nk2; kt += 2) {
     step(std::false_type{}, kt);
     step(std::true_type{}, kt + 1);
   }
 
   // C tile (i, j): lane l holds row l%32, register r holds column 8(r/4) + 4(l/32) + r%4.
   const int hh = lane >> 5, l32 = lane & 31;
+  if (part) {
+    // split-K partial: fp32 [M][N] slab of this k range, summed by splitk_reduce_kernel
+    float* slab = part + (int64_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + wm + 32 * i + l32;
+      if (row >= M) continue;
+      float* prow = slab + (int64_t)row * N;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = n0 + wn + 32 * j + 8 * q + 4 * hh;
+          if ((N & 3) == 0 && col + 3 < N) {
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<f32x4*>(prow + col) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                      acc[i][j][4 * q + 3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) prow[col + e] = acc[i][j][4 * q + e];
+          }
+        }
+    }
+    return;
+  }
   if constexpr (SMX) {
     // The wave's 128 columns of each row are one softmax group: lanes l and l + 32
     // hold 64 of them each. Max, then e = exp(logit - max) stored in TC and summed;
@@ -547,7 +579,58 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
     }
 }
 
+// Split-K reduction: c[m][n] = r[m][n] + sum over s (in order) of part[s][m][n],
+// rounded once to TC. Four consecutive columns per thread when N % 4 == 0.
+template <typename TC, int V>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const float* __restrict__ part, int splits, int M, int N, TC* C, int64_t ldc, const void* R,
+    int64_t ldr, int r_f32) {
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  const int64_t MN = (int64_t)M * N;
+  if (idx >= MN) return;
+  const int row = (int)(idx / N), col = (int)(idx - (int64_t)row * N);
+  float v[V];
+  load_f32<float, V>(part + idx, v);
+  for (int s = 1; s < splits; ++s) {
+    float w[V];
+    load_f32<float, V>(part + s * MN + idx, w);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] += w[e];
+  }
+  if (R) {
+    float r[V];
+    if (r_f32) load_f32<float, V>((const float*)R + (int64_t)row * ldr + col, r);
+    else load_f32<TC, V>((const TC*)R + (int64_t)row * ldr + col, r);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] += r[e];
+  }
+  store_f32<TC, V>(C + (int64_t)row * ldc + col, v);
+}
+
 }  // namespace
+
+// Split-K: when the output has fewer tiles than kSplitTarget (one per CU of an
+// MI355X; a constant, so the summation order depends on the shape only) and the
+// caller's workspace holds the fp32 partials, K is cut into `splits` ranges of
+// whole 64-deep slices, at least kMinSliceRun each.
+constexpr int kSplitTarget = 256, kMaxSplits = 16, kMinSliceRun = 4;
+
+int gemm_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  const int64_t nk = (K + kBK - 1) / kBK;
+  if (tiles >= kSplitTarget / 2) return 1;
+  int64_t s = std::min<int64_t>(kMaxSplits, kSplitTarget / tiles);
+  s = std::min<int64_t>(s, nk / kMinSliceRun);
+  if (s < 2) return 1;
+  const int64_t per = (nk + s - 1) / s;
+  return (int)((nk + per - 1) / per);
+}
+
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int s = gemm_splits(M, N, K);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
 
 // C[M][N] = A B in fp32 accumulation; see the file comment for the layouts.
 // a_kc: A is [a_rows][lda] holding rows m (else rows k); b_kc: B is [b_rows][ldb]
@@ -555,7 +638,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
                 int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
-                const void* R, int64_t ldr, bool r_f32) {
+                const void* R, int64_t ldr, bool r_f32, void* ws, size_t ws_bytes) {
   if (M <= 0 || N <= 0) return 0;
   if (K <= 0) {
     set_error("%s: K must be positive", name);
@@ -641,13 +724,30 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
   // 16-byte aligned base; otherwise the kernel stores element by element.
   const int vec_c = (ldc % 4 == 0) && aligned16(C) &&
                     (!R || ((ldr % 4 == 0) && aligned16(R)));
+  int splits = gemm_splits(M, N, K);
+  if (splits > 1 && (!ws || ws_bytes < gemm_workspace_bytes(M, N, K) || !aligned16(ws)))
+    splits = 1;
+  const int nk = (int)((K + kBK - 1) / kBK);
+  const int kt_per = (nk + splits - 1) / splits;
   auto go = [&](auto tag, auto ctag, auto akc, auto bkc) {
     using T = decltype(tag);
     using TC = decltype(ctag);
-    EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>), dim3(grid),
-              dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
-              (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c,
-              SmxArgs{}, R, ldr, (int)r_f32);
+    float* part = splits > 1 ? (float*)ws : nullptr;
+    EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>),
+              dim3(grid, (unsigned)splits), dim3(kThreads), 0, st, (const uint16_t*)A,
+              (const uint16_t*)B, (TC*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows,
+              (int)tiles_m, (int)tiles, vec_c, SmxArgs{}, R, ldr, (int)r_f32, kt_per, part);
+    if (int e = check_launch(name)) return e;
+    if (splits == 1) return 0;
+    const bool v4 = (N % 4 == 0) && vec_c;
+    const int64_t n = M * N / (v4 ? 4 : 1);
+    const unsigned rg = (unsigned)((n + 255) / 256);
+    if (v4)
+      EG_LAUNCH((splitk_reduce_kernel<TC, 4>), dim3(rg), dim3(256), 0, st, part, splits, (int)M,
+                (int)N, (TC*)C, ldc, R, ldr, (int)r_f32);
+    else
+      EG_LAUNCH((splitk_reduce_kernel<TC, 1>), dim3(rg), dim3(256), 0, st, part, splits, (int)M,
+                (int)N, (TC*)C, ldc, R, ldr, (int)r_f32);
     return check_launch(name);
   };
   auto layouts = [&](auto tag, auto ctag) {
@@ -699,7 +799,7 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M,
     EG_LAUNCH((gemm_kernel<T, true, true, T, true>), dim3(grid), dim3(kThreads), 0, st,
               (const uint16_t*)x, (const uint16_t*)w, (T*)e, (int)M, (int)N, (int)K, ldx, ldw,
               lde, M, N, (int)tiles_m, (int)tiles, vec_c, smx, (const void*)nullptr, (int64_t)0,
-              0);
+              0, 0, (float*)nullptr);
     return check_launch(name);
   };
   return dtype == EG_BF16 ? go(bf16_t{}) : go(f16_t{});
@@ -709,10 +809,15 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M,
 
 using namespace eg;
 
+extern "C" size_t eg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int dtype) {
+  if (dtype != EG_BF16 && dtype != EG_F16) return 0;
+  return gemm_workspace_bytes(m, n, k);
+}
+
 extern "C" int eg_gemm(const void* a, const void* b, void* c, const void* r, int64_t m,
                        int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t ldr,
                        int a_k_contiguous, int b_k_contiguous, int dtype, int c_dtype,
-                       void* stream) {
+                       void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (m < 0 || n < 0 || k < 0) {
     set_error("eg_gemm: negative size");
@@ -724,5 +829,6 @@ extern "C" int eg_gemm(const void* a, const void* b, void* c, const void* r, int
   }
   const bool akc = a_k_contiguous != 0, bkc = b_k_contiguous != 0;
   return gemm_launch(a, b, c, m, n, k, lda, ldb, ldc, akc, bkc, akc ? m : k, bkc ? n : k, dtype,
-                     c_dtype, as_stream(stream), "eg_gemm", r, ldr);
+                     c_dtype, as_stream(stream), "eg_gemm", r, ldr, false, workspace,
+                     workspace_bytes);
 }

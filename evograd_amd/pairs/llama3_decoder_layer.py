@@ -136,8 +136,12 @@ class _Ops:
         return t
 
     def gemm(self, a, b, c, m, n, k, lda, ldb, ldc, akc, bkc, r=None, ldr=0):
+        # products of few output tiles split k over a workspace (fp32 partials)
+        nbytes = _lib.query("eg_gemm_workspace_bytes", m, n, k, self.tg)
+        ws = workspace(nbytes, self.dev) if nbytes else None
         _lib.call("eg_gemm", _lib.ptr(a), _lib.ptr(b), _lib.ptr(c), _lib.ptr(r), m, n, k, lda,
-                  ldb, ldc, ldr, int(akc), int(bkc), self.tg, self.tg, self.st)
+                  ldb, ldc, ldr, int(akc), int(bkc), self.tg, self.tg, _lib.ptr(ws), nbytes,
+                  self.st)
 
     def linear(self, h, w, out, m, n, k, ldh, ldo, r=None):
         """out[m, :n] = r + h[m, :k] w^T, w [n, k] (F.linear)."""

@@ -56,6 +56,15 @@ class KernelTimer:
         next library call on (across the calls that follow it)."""
         _lib.call("eg_time_kernel", self.start, self.stop, int(index))
 
+    def label(self) -> str:
+        """Name of the kernel the last arm launched ("" before that launch)."""
+        raw = _lib.query("eg_time_kernel_label")
+        return raw.decode() if raw else ""
+
+    def fired(self) -> bool:
+        """Whether the armed launch has run (drops the arm either way)."""
+        return not _lib.query("eg_time_kernel_missed")
+
     def elapsed_ms(self) -> float:
         if _lib.query("eg_time_kernel_missed"):
             raise RuntimeError("the armed kernel launch did not run")

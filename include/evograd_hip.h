@@ -61,6 +61,10 @@ int eg_time_kernel(void* start_event, void* stop_event, int index);
  * nothing of this arm), 0 when it has; drops the arm either way. */
 int eg_time_kernel_missed(void);
 
+/* Name of the kernel the calling thread's last eg_time_kernel arm launched ("" until
+ * that launch has happened). */
+const char* eg_time_kernel_label(void);
+
 /* ---------------------------------------------------------------- softmax
  * Replaces softmax_forward_ref (src/evograd/ops/level1/softmax/forward_ref.py:6-7):
  *   y = softmax(x.float(), dim=-1).to(x.dtype), x and y [rows, cols].
@@ -340,10 +344,17 @@ int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int6
  * before c is rounded. A 16-bit k-contiguous operand needs k % 64 == 0, or, when the
  * other operand is k-major, a row stride of at least k rounded up to 64 whose columns
  * past k hold finite values (zeros); strides are multiples of 8 elements and a, b are
- * 16-byte aligned. */
+ * 16-byte aligned.
+ * Products with fewer output tiles (256 x 256) than an MI355X has CUs split k over
+ * workgroups when `workspace` holds at least eg_gemm_workspace_bytes(m, n, k, dtype)
+ * bytes (else, or with workspace NULL, they run unsplit): each k range writes an
+ * fp32 partial, and a second pass sums them in a fixed order, adds r and rounds c
+ * once. The split depends on the shape only, so results are bitwise repeatable. */
+size_t eg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int dtype);
 int eg_gemm(const void* a, const void* b, void* c, const void* r, int64_t m, int64_t n,
             int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t ldr, int a_k_contiguous,
-            int b_k_contiguous, int dtype, int c_dtype, void* stream);
+            int b_k_contiguous, int dtype, int c_dtype, void* workspace, size_t workspace_bytes,
+            void* stream);
 
 /* ---------------------------------------------- decoder layer: layout, adds
  * The steps of the Llama-3 decoder layer

@@ -49,7 +49,7 @@ def _run(a, b, M, N, K, lda, ldb, akc, bkc, dtype, cdt):
     ldc = N + 3 if cdt == torch.float32 else _r8(N)
     c = torch.full((M, ldc), float("nan"), device="cuda", dtype=cdt)
     _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), None, M, N, K, lda, ldb,
-              ldc, 0, int(akc), int(bkc), _lib.dtype_tag(dtype), _lib.dtype_tag(cdt),
+              ldc, 0, int(akc), int(bkc), _lib.dtype_tag(dtype), _lib.dtype_tag(cdt), None, 0,
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return c
@@ -103,7 +103,8 @@ def test_gemm_refuses_unsupported_shapes_on_the_host():
     c = torch.zeros(64, 64, device="cuda")
     with pytest.raises(RuntimeError, match="K % 64"):
         _lib.call("eg_gemm", x.data_ptr(), x.data_ptr(), c.data_ptr(), None, 64, 64, 40, 64, 64,
-                  64, 0, 1, 1, _lib.EG_BF16, _lib.EG_F32, torch.cuda.current_stream().cuda_stream)
+                  64, 0, 1, 1, _lib.EG_BF16, _lib.EG_F32, None, 0,
+                  torch.cuda.current_stream().cuda_stream)
 
 
 @pytest.mark.parametrize("cdt", [torch.float32, torch.bfloat16])
@@ -125,7 +126,7 @@ def test_gemm_residual_epilogue(cdt, akc, bkc, inplace):
     else:
         c, ldr = torch.full((M, ldc), float("nan"), device="cuda", dtype=cdt), ldc
     _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K, lda,
-              ldb, ldc, ldr, int(akc), int(bkc), _lib.EG_BF16, _lib.dtype_tag(cdt),
+              ldb, ldc, ldr, int(akc), int(bkc), _lib.EG_BF16, _lib.dtype_tag(cdt), None, 0,
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     ref = r0[:, :N].double() + A.double() @ B.double()
@@ -148,6 +149,48 @@ def test_gemm_residual_fp32_path():
     r = torch.randn(M, N, device="cuda")
     c = torch.empty(M, N, device="cuda")
     _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K, lda,
-              ldb, N, N, 1, 0, _lib.EG_F32, _lib.EG_F32, torch.cuda.current_stream().cuda_stream)
+              ldb, N, N, 1, 0, _lib.EG_F32, _lib.EG_F32, None, 0,
+              torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.allclose(c.double(), r.double() + A.double() @ B.double(), atol=1e-4, rtol=1e-5)
+
+
+@pytest.mark.parametrize("cdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,akc,bkc", [(1024, 1024, 4096, True, True),
+                                           (300, 700, 2048, True, False),
+                                           (512, 256, 1000, False, False),
+                                           (1024, 4096, 14336, True, True)])
+def test_gemm_split_k_matches_unsplit_and_is_repeatable(cdt, M, N, K, akc, bkc):
+    """Few output tiles and a workspace: k splits into fp32 partials summed in a fixed
+    order, the residual added and c rounded once. Against the unsplit product: the
+    same sum in another order (fp32), and bitwise equal run to run."""
+    print(f"\n[gpu-gemm] split-K {M}x{N}x{K} {cdt}", flush=True)
+    need = _lib.query("eg_gemm_workspace_bytes", M, N, K, _lib.EG_BF16)
+    assert need > 0
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, torch.bfloat16, M + N + K)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    r = torch.randn(M, N, device="cuda").to(cdt)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for work, nbytes in ((ws, need), (ws, need), (None, 0)):
+        c = torch.full((M, N), float("nan"), device="cuda", dtype=cdt)
+        _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K,
+                  lda, ldb, N, N, int(akc), int(bkc), _lib.EG_BF16, _lib.dtype_tag(cdt),
+                  None if work is None else work.data_ptr(), nbytes, st)
+        outs.append(c)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = r.double() + A.double() @ B.double()
+    for c in (outs[0], outs[2]):
+        err = (c.double() - ref).abs()
+        if cdt == torch.float32:
+            assert err.max().item() <= 4e-6 * K, err.max().item()
+        else:
+            assert (err <= 2.0 ** -8 * ref.abs() + 4e-6 * K).all(), err.max().item()
+    # a workspace one byte short runs unsplit (the same result as no workspace)
+    c = torch.empty((M, N), device="cuda", dtype=cdt)
+    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), c.data_ptr(), r.data_ptr(), M, N, K, lda,
+              ldb, N, N, int(akc), int(bkc), _lib.EG_BF16, _lib.dtype_tag(cdt), ws.data_ptr(),
+              need - 1, st)
+    torch.cuda.synchronize()
+    assert torch.equal(c, outs[2])
