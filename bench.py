@@ -389,7 +389,7 @@ def sweep_op(name: str, tokens: tuple, steps: int, warmup: int, flush) -> dict:
 
     import torch
 
-    from evograd_amd import decls, pair_module
+    from evograd_amd import DISPATCH_MODULES, decls, dispatch_module, pair_module
     from evograd_amd.bind import backward_inactive_kwargs, lookup_pair
     from evograd_amd.harness import summarize, time_regions
     from evograd_amd.inputs import make_case_inputs
@@ -397,6 +397,11 @@ def sweep_op(name: str, tokens: tuple, steps: int, warmup: int, flush) -> dict:
     base, label = split_name(name)
     op = decls.get_op(base)
     f, b = lookup_pair(op, pair_module(base))
+    # with a shape dispatcher (small-shape program below the regime split), the
+    # dispatched pair is timed too
+    disp = None
+    if base in DISPATCH_MODULES and not label:
+        disp = lookup_pair(op, dispatch_module(base))
     w0 = bench_workload(op, label)
     out = {}
     for t in tokens:
@@ -413,8 +418,23 @@ def sweep_op(name: str, tokens: tuple, steps: int, warmup: int, flush) -> dict:
                                     warmup=warmup, flush=flush))["median_ms"]
         work = algorithmic_work(base, w)
         gbs = (work["fwd"] + work["bwd"]) / (ms * 1e-3) / 1e9
+        state = {}
+
+        def setup_bwd():
+            state["saved"] = f(*args)[1]
+
+        kt = kernel_times(name, lambda: f(*args), lambda saved: b(dy, saved, **kw), setup_bwd,
+                          state, flush, max(3, steps // 2))
         out[str(t)] = {"full_us": round(ms * 1e3, 2), "hbm_frac_full": round(gbs / HBM_PEAK_GBS, 4),
-                       "dims": dims}
+                       "kernels_us": {k: round(v, 2) for k, v in kt.items()}, "dims": dims}
+        if disp is not None:
+            df, db = disp
+            dms = summarize(time_regions(lambda: db(dy, df(*args)[1], **kw), reps=steps,
+                                         warmup=warmup, flush=flush))["median_ms"]
+            dgbs = (work["fwd"] + work["bwd"]) / (dms * 1e-3) / 1e9
+            out[str(t)].update(dispatch_full_us=round(dms * 1e3, 2),
+                               dispatch_hbm_frac_full=round(dgbs / HBM_PEAK_GBS, 4),
+                               dispatch_route=int(df(*args)[1][0]))
         del inputs, args, dy
         torch.cuda.empty_cache()
     return out

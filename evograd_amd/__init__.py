@@ -32,6 +32,24 @@ PAIR_MODULES = {
     "llama3_decoder_layer": "evograd_amd.pairs.llama3_decoder_layer",
 }
 
+# Small-shape programs and the shape dispatchers that route to them below the
+# declaration's regime split (the registered PAIR_MODULES program above it).
+SMALL_PROGRAMS = {
+    "rmsnorm": "evograd_amd.pairs.rmsnorm_small",
+    "layernorm": "evograd_amd.pairs.layernorm_small",
+}
+DISPATCH_MODULES = {
+    "rmsnorm": "evograd_amd.pairs.rmsnorm_dispatch",
+    "layernorm": "evograd_amd.pairs.layernorm_dispatch",
+}
+
+
+def dispatch_module(op_name: str):
+    """The shape-dispatched pair of ``op_name`` (KeyError when it has none)."""
+    import importlib
+
+    return importlib.import_module(DISPATCH_MODULES[op_name])
+
 
 def pair_module(op_name: str):
     """Import the HIP-backed pair module for ``op_name``."""

@@ -1143,6 +1143,205 @@ extern "C" int eg_layernorm_bwd(const void* dy, const void* x, const void* weigh
   });
 }
 
+// ------------------------------------------- small-shape backward, one launch
+// For few rows (the reference's small regime, under 4096 tokens) the ring backward
+// and its column sum are two latency-bound launches: at bf16 [1024, 4096] 10.2 and
+// 4.0 us, for 25 MB. This kernel does the whole backward in one launch with no
+// partial rows, in two kinds of workgroups:
+//   column workgroups (first): 4 packs of columns each, 64 row lanes; lane walks
+//     rows rl, rl + 64, ... (8 rows' loads in flight) summing dy * xhat (and dy) per
+//     column in fp32 (compensated), then the 64 lane sums are added in a fixed
+//     pairwise tree ->
+//     dweight (dbias): bitwise repeatable, and read from dy, x and the saved row
+//     statistics alone;
+//   row workgroups: one row each, two passes over the row (the second from L2):
+//     the row sums, then dx.
+// dy and x are read twice (once per role), which at these sizes the 256 MB
+// Infinity Cache serves; for wide batches the ring, which reads them once, is
+// the program to use.
+constexpr int kSmallBlock = 256, kSmallPacks = 4, kSmallLanes = kSmallBlock / kSmallPacks;
+constexpr int kSmallUnroll = 8;  // rows of a lane whose loads are issued together
+
+template <typename T, int VEC, bool LN>
+__global__ __launch_bounds__(kSmallBlock) void norm_bwd_small(
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
+    const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
+    T* __restrict__ dweight, T* __restrict__ dbias, int64_t rows, int hidden, int ncolwg) {
+  __shared__ float part[2][kSmallLanes][kSmallPacks * VEC];
+  __shared__ float red[2][kSmallBlock / kWave];
+  const int t = threadIdx.x;
+  if ((int)blockIdx.x < ncolwg) {
+    const int p = t % kSmallPacks, rl = t / kSmallPacks;
+    const int c0 = ((int)blockIdx.x * kSmallPacks + p) * VEC;
+    const bool live = c0 < hidden;
+    // Compensated (Kahan) sums per lane, then a pairwise tree over the 64 lanes: a
+    // lane's rows are summed in order with their rounding errors carried, so the
+    // result stays within a few units of the exact column sum even where the rows
+    // cancel (the ring's many short partial rows give the same by splitting).
+    float sw[VEC], sb[VEC], cw[VEC], cb[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { sw[i] = 0.f; sb[i] = 0.f; cw[i] = 0.f; cb[i] = 0.f; }
+    auto kahan = [](float& s, float& c, float v) {
+      const float y = v - c;
+      const float t2 = s + y;
+      c = (t2 - s) - y;
+      s = t2;
+    };
+    if (live) {
+      // kSmallUnroll rows per batch, all their loads issued before the sums (rows
+      // past the end load row 0 and are skipped)
+      for (int64_t r0 = rl; r0 < rows; r0 += (int64_t)kSmallLanes * kSmallUnroll) {
+        float g[kSmallUnroll][VEC], xv[kSmallUnroll][VEC], rs[kSmallUnroll], mu[kSmallUnroll];
+#pragma unroll
+        for (int u = 0; u < kSmallUnroll; ++u) {
+          const int64_t r = r0 + (int64_t)u * kSmallLanes;
+          const int64_t rc = r < rows ? r : 0;
+          load_f32<T, VEC>(dy + rc * hidden + c0, g[u]);
+          load_f32<T, VEC>(x + rc * hidden + c0, xv[u]);
+          rs[u] = rstd[rc];
+          mu[u] = LN ? mean[rc] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kSmallUnroll; ++u) {
+          if (r0 + (int64_t)u * kSmallLanes >= rows) break;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            kahan(sw[i], cw[i], g[u][i] * ((xv[u][i] - mu[u]) * rs[u]));
+            if (LN) kahan(sb[i], cb[i], g[u][i]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      part[0][rl][p * VEC + i] = sw[i] - cw[i];
+      if (LN) part[1][rl][p * VEC + i] = sb[i] - cb[i];
+    }
+    __syncthreads();
+    if (t < kSmallPacks * VEC) {
+      const int col = (int)blockIdx.x * kSmallPacks * VEC + t;
+      float a[kSmallLanes], b[kSmallLanes];
+#pragma unroll
+      for (int l = 0; l < kSmallLanes; ++l) {
+        a[l] = part[0][l][t];
+        b[l] = LN ? part[1][l][t] : 0.f;
+      }
+#pragma unroll
+      for (int w2 = kSmallLanes / 2; w2 >= 1; w2 >>= 1)
+#pragma unroll
+        for (int l = 0; l < w2; ++l) {
+          a[l] += a[l + w2];
+          if (LN) b[l] += b[l + w2];
+        }
+      if (col < hidden) {
+        dweight[col] = from_f32<T>(a[0]);
+        if (LN) dbias[col] = from_f32<T>(b[0]);
+      }
+    }
+    return;
+  }
+  const int64_t r = (int64_t)blockIdx.x - ncolwg;
+  const T* dyr = dy + r * hidden;
+  const T* xr = x + r * hidden;
+  const float rs = rstd[r], mu = LN ? mean[r] : 0.f;
+  // pass 1: sum(g) (LayerNorm) and sum(g * xhat), g = dy * w
+  float sa = 0.f, sg = 0.f;
+  for (int c = t * VEC; c < hidden; c += kSmallBlock * VEC) {
+    float g[VEC], xv[VEC], wv[VEC];
+    load_f32<T, VEC>(dyr + c, g);
+    load_f32<T, VEC>(xr + c, xv);
+    load_f32<T, VEC>(w + c, wv);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float gi = g[i] * wv[i];
+      sa = __builtin_fmaf(gi, (xv[i] - mu) * rs, sa);
+      if (LN) sg += gi;
+    }
+  }
+  sa = wave_reduce(sa, SumOp());
+  if (LN) sg = wave_reduce(sg, SumOp());
+  if ((t & (kWave - 1)) == 0) {
+    red[0][t / kWave] = sa;
+    red[1][t / kWave] = sg;
+  }
+  __syncthreads();
+  float ta = red[0][0], tg = red[1][0];
+#pragma unroll
+  for (int k = 1; k < kSmallBlock / kWave; ++k) {
+    ta += red[0][k];
+    tg += red[1][k];
+  }
+  const float inv_h = 1.0f / (float)hidden;
+  const float mgx = ta * inv_h, mg = LN ? tg * inv_h : 0.f;
+  // pass 2: dx = rstd * (g - mean(g) - xhat * mean(g * xhat))   (RMSNorm: no mean(g))
+  for (int c = t * VEC; c < hidden; c += kSmallBlock * VEC) {
+    float g[VEC], xv[VEC], wv[VEC], o[VEC];
+    load_f32<T, VEC>(dyr + c, g);
+    load_f32<T, VEC>(xr + c, xv);
+    load_f32<T, VEC>(w + c, wv);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float xh = (xv[i] - mu) * rs;
+      o[i] = (g[i] * wv[i] - mg - xh * mgx) * rs;
+    }
+    store_f32<T, VEC>(dx + r * hidden + c, o);
+  }
+}
+
+template <bool LN>
+static int norm_bwd_small_impl(const char* name, const void* dy, const void* x,
+                               const void* weight, const float* mean, const float* rstd,
+                               void* dx, void* dweight, void* dbias, int64_t rows,
+                               int64_t hidden, int dtype, void* stream) {
+  clear_error();
+  if (check_norm_dims(name, rows, hidden)) return 1;
+  if (!dweight || (LN && !dbias)) { set_error("%s: null dweight/dbias", name); return 1; }
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    const size_t es = dtype == EG_F32 ? 4 : 2;
+    if (int rc = zero_fill(dweight, (size_t)hidden * es, st, name)) return rc;
+    return LN ? zero_fill(dbias, (size_t)hidden * es, st, name) : 0;
+  }
+  if (!dy || !x || !weight || (LN && !mean) || !rstd || !dx) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  if (rows > 0x7fffffff - 65536) {
+    set_error("%s: rows=%lld exceeds the launch grid", name, (long long)rows);
+    return 1;
+  }
+  return EG_DISPATCH_FLOAT(dtype, name, [&] {
+    using T = scalar_t;
+    constexpr int V = 16 / sizeof(T);
+    const int h = (int)hidden;
+    auto go = [&](auto vc) {
+      constexpr int VC = decltype(vc)::value;
+      const int ncol = (h + kSmallPacks * VC - 1) / (kSmallPacks * VC);
+      EG_LAUNCH((norm_bwd_small<T, VC, LN>), dim3((unsigned)(ncol + rows)), dim3(kSmallBlock), 0,
+                st, (const T*)dy, (const T*)x, (const T*)weight, mean, rstd, (T*)dx, (T*)dweight,
+                (T*)dbias, rows, h, ncol);
+      return check_launch(name);
+    };
+    if (vec_ok<T>(h, {dy, x, weight, dx})) return go(std::integral_constant<int, V>{});
+    return go(std::integral_constant<int, 1>{});
+  });
+}
+
+extern "C" int eg_rmsnorm_bwd_small(const void* dy, const void* x, const void* weight,
+                                    const float* rstd, void* dx, void* dweight, int64_t rows,
+                                    int64_t hidden, int dtype, void* stream) {
+  return norm_bwd_small_impl<false>("eg_rmsnorm_bwd_small", dy, x, weight, nullptr, rstd, dx,
+                                    dweight, nullptr, rows, hidden, dtype, stream);
+}
+
+extern "C" int eg_layernorm_bwd_small(const void* dy, const void* x, const void* weight,
+                                      const float* mean, const float* rstd, void* dx,
+                                      void* dweight, void* dbias, int64_t rows, int64_t hidden,
+                                      int dtype, void* stream) {
+  return norm_bwd_small_impl<true>("eg_layernorm_bwd_small", dy, x, weight, mean, rstd, dx,
+                                   dweight, dbias, rows, hidden, dtype, stream);
+}
+
 // ------------------------------------------------- allocation-free backward
 // eg_rmsnorm_bwd_noalloc runs eg_rmsnorm_bwd's kernels with the partial rows in
 // `scratch`, a device-resident array of the library (one copy per GPU, held

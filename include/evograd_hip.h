@@ -97,6 +97,16 @@ int eg_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const floa
                    void* dx, void* dweight, void* workspace, int64_t rows, int64_t hidden,
                    int dtype, void* stream);
 
+/* The same backward as eg_rmsnorm_bwd (src/evograd/ops/level1/rmsnorm/__init__.py:
+ * 85-86) in one launch and with no workspace, for few rows (the reference's small
+ * regime, under 4096 tokens: src/evograd/opdecl/models.py:306): column workgroups
+ * sum dweight = sum_rows(dy * x * rstd) directly in a fixed order while row
+ * workgroups form dx. dy and x are read twice (served from the device's caches at
+ * these sizes); wide batches are faster on eg_rmsnorm_bwd. */
+int eg_rmsnorm_bwd_small(const void* dy, const void* x, const void* weight, const float* rstd,
+                         void* dx, void* dweight, int64_t rows, int64_t hidden, int dtype,
+                         void* stream);
+
 /* Size of the device-resident scratch array behind eg_rmsnorm_bwd_noalloc (16 MiB
  * per GPU: the [G, hidden] fp32 partial rows for hidden up to 8192). */
 #define EG_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
@@ -154,6 +164,13 @@ int eg_layernorm_bwd(const void* dy, const void* x, const void* weight, const fl
                      const float* rstd, void* dx, void* dweight, void* dbias,
                      void* workspace, int64_t rows, int64_t hidden, int dtype,
                      void* stream);
+
+/* eg_layernorm_bwd in one launch with no workspace, for few rows (as
+ * eg_rmsnorm_bwd_small): dweight = sum_rows(dy * xhat), dbias = sum_rows(dy) summed
+ * per column in a fixed order, dx per row. */
+int eg_layernorm_bwd_small(const void* dy, const void* x, const void* weight, const float* mean,
+                           const float* rstd, void* dx, void* dweight, void* dbias,
+                           int64_t rows, int64_t hidden, int dtype, void* stream);
 
 /* ----------------------------------------------------------------- swiglu
  * Replaces swiglu_forward_ref (src/evograd/ops/level1/swiglu/forward_ref.py:6-9):

@@ -63,6 +63,25 @@ def test_pair_file_loads_as_a_top_level_candidate(path, tmp_path):
         assert module == f"evograd_candidate_{path.stem}"
 
 
+def _extra_files():
+    from evograd_amd import DISPATCH_MODULES, SMALL_PROGRAMS
+
+    for table in (SMALL_PROGRAMS, DISPATCH_MODULES):
+        for op_name, mod in sorted(table.items()):
+            yield pytest.param(op_name, ROOT / (mod.replace(".", "/") + ".py"),
+                               id=mod.rsplit(".", 1)[1])
+
+
+@pytest.mark.parametrize("op_name,path", list(_extra_files()))
+def test_small_programs_and_dispatchers_load_as_candidates(op_name, path, tmp_path):
+    """The small-shape programs and the dispatchers over them load from their paths
+    like any candidate, with the repository off sys.path, and expose the pair."""
+    found = _run_isolated(LOAD_AND_LOOKUP.format(root=str(ROOT), path=str(path), ops=[op_name]),
+                          tmp_path)
+    fwd, bwd, _ = found[op_name]
+    assert fwd.endswith("forward_with_saved") and bwd.endswith("backward_from_saved")
+
+
 def test_every_declaration_has_a_pair_file():
     from evograd_amd.decls import OPS
 

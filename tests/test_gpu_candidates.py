@@ -35,9 +35,14 @@ def test_path_loaded_candidate_passes_the_gate(op_name):
 
 
 def test_emitted_dispatcher_over_hip_files_passes_the_gate(tmp_path):
+    """A dispatcher module written to disk over two different program files (the
+    small-shape program and the ring program), loaded by path as a candidate."""
+    from evograd_amd import SMALL_PROGRAMS
+
     op = decls.RMSNORM
     rms = _file_of("rmsnorm")
-    out = emit_dispatcher(op, rms, rms, 64.0, tmp_path / "dispatch_rmsnorm.py")
+    small_file = ROOT / (SMALL_PROGRAMS["rmsnorm"].replace(".", "/") + ".py")
+    out = emit_dispatcher(op, small_file, rms, 64.0, tmp_path / "dispatch_rmsnorm.py")
     module = load_module(out)
     small = [w for w in op.correctness if w.dims["rows"] < 64][:1]
     large = [w for w in op.correctness if w.dims["rows"] >= 64][:1]
