@@ -247,7 +247,8 @@ __device__ __forceinline__ V rd_tr(const uint16_t* lds, int r16, int dd0, int la
 // Copies rows [row0, row0 + ROWS) of a [nrows, D] slice into a swizzled LDS tile
 // with 16-byte buffer->LDS loads. Each lane's offset inside the tile is fixed;
 // the buffer resource starts at row0 and ends at the slice's last row, so rows
-// past the slice are never fetched (their LDS rows keep earlier, finite values).
+// past the slice are not fetched: their LDS rows are written with zeros (the
+// bounded-access rules in eg_common.hpp).
 template <int ROWS, int D, int NW>
 struct TileLoader {
   static constexpr int CPR = D / 8;

@@ -202,6 +202,14 @@ __device__ __forceinline__ void block_reduce2(float& a, float& b, float* lds) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Bounded buffer accesses on gfx950 (relied on by the kernels that use them):
+//  - a buffer load whose offset lies outside the resource's range returns zero;
+//  - a buffer->LDS load (buffer_load ... lds) outside the range writes zero into
+//    the lane's LDS slot, exactly as the register load returns zero (the products'
+//    ragged-k and odd-slice-count cases in tests/test_gpu_gemm.py hold only if it
+//    does);
+//  - a buffer store outside the range is dropped.
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ------------------------------------------------------------ launching

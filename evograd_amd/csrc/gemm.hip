@@ -249,7 +249,8 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   const int nk = part ? min(nk_all, kb + kt_per) : nk_all;
   // The k loop runs an even number of steps (two per iteration, one per buffer). A
   // slice at or past nk loads through an empty buffer range, which fills its LDS
-  // slots with zeros: the step past the range, when its length is odd, adds zeros.
+  // slots with zeros (the bounded-access rules in eg_common.hpp): the step past the
+  // range, when its length is odd, adds zeros.
   const int nk2 = kb + (nk - kb) + ((nk - kb) & 1);
 
   f32x16 acc[4][4];

@@ -212,8 +212,9 @@ __global__ __launch_bounds__(BLOCK) void softmax_bwd_loop(const T* __restrict__ 
 // registers, and converted to fp32 again in each pass; the empty asm statements keep
 // the compiler from hoisting fp32 copies of the register packs across the
 // reductions. All loads go through buffer resources bounded by the row's bytes, so
-// none sits under a branch: packs past the row read as zeros (registers) or leave
-// their LDS slot unwritten, and are masked in the reductions.
+// none sits under a branch: packs past the row read as zeros, in registers and in
+// LDS alike (the bounded-access rules in eg_common.hpp), and are masked in the
+// reductions.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -277,7 +278,7 @@ void softmax_fwd_lds(const T* __restrict__ x, T* __restrict__ y, int cols) {
     }
   };
   float m = -INFINITY;
-  // Packs past the row (zeros from the register loads, unwritten LDS slots) are
+  // Packs past the row (zeros from the register and the buffer->LDS loads) are
   // masked out of the max and the sum.
   pass([&](int it, const u32x4& p) {
     const bool in = (it * BLOCK + tid) * 8 < cols;
@@ -346,12 +347,9 @@ __global__ __launch_bounds__(BLOCK) void softmax_bwd_lds(const T* __restrict__ y
   for (int it = 0; it < RI; ++it)
     gr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                            rg, ((it + LITEMS) * BLOCK + tid) * 16, 0, kNtLoad));
-  // LDS slots past the row, which the bounded loads leave unwritten, hold zeros (the
-  // register loads return zeros there), so they add nothing to sum(dy * y).
-#pragma unroll
-  for (int it = 0; it < LITEMS; ++it)
-    if ((it * BLOCK + tid) * 8 >= cols)
-      *reinterpret_cast<u32x4*>(dys + (it * BLOCK + tid) * 8) = u32x4{0u, 0u, 0u, 0u};
+  // LDS slots past the row hold zeros written by the bounded buffer->LDS loads, and
+  // the register loads return zeros there too (eg_common.hpp), so they add nothing
+  // to sum(dy * y).
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own LDS slots only: no barrier
   auto gpack = [&](int it) -> u32x4 {
     return it < LITEMS ? *reinterpret_cast<const u32x4*>(dys + (it * BLOCK + tid) * 8)
