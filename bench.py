@@ -343,9 +343,16 @@ def gpu_op(name: str, steps: int, warmup: int, flush) -> dict:
         "saved_tensors": report["saved_tensors"],
         "kernels_us": kt,
     }
-    if base == LAYER:
-        out["saved"]["peak_scratch_note"] = ("forward and backward intermediates are "
-                                             "torch.empty buffers freed when each call returns")
+    if base == "fused_linear_cross_entropy":
+        # the forward's scratch (one chunk of dlogits and group statistics, the fp32
+        # dweight sum over chunks), freed when the forward returns
+        from evograd_amd import _lib
+        from evograd_amd.pairs._util import tag
+
+        d = w.dims
+        out["saved"]["peak_scratch_bytes"] = int(_lib.query(
+            "eg_flce_workspace_bytes", d["rows"], d["hidden"], d["vocab"], 0,
+            tag(inputs["x"].dtype)))
     phase, kname, occurrence = DOMINANT[name]
     kkey = find_kernel(kt, phase, kname, occurrence)
     k_us = kt[kkey]
