@@ -109,14 +109,16 @@ def mfma(counter_csv: str, stats_csv: str, filt: str = "", ghz: float = 2.4) -> 
 def traffic(fetch_csv: str, write_csv: str, kernel: str, key: str = "") -> dict:
     f, w = _counter_table(fetch_csv), _counter_table(write_csv)
 
-    def pick(table, sub, counter):
+    def pick(table, sub, counter, how=statistics.median):
         vals = [v for k, cs in table.items() if sub in k for v in cs.get(counter, [])]
         if not vals:
             raise SystemExit(f"no {counter} readings for kernels matching {sub!r}")
-        return statistics.median(vals)
+        return how(vals)
 
-    copy_fetch_kib = pick(f, COPY_KERNEL, "FETCH_SIZE")
-    copy_write_kib = pick(w, COPY_KERNEL, "WRITE_SIZE")
+    # the calibration copy is the largest kernel of its kind in the run (an input
+    # recipe may launch smaller ones of the same kind, e.g. weight scalings)
+    copy_fetch_kib = pick(f, COPY_KERNEL, "FETCH_SIZE", max)
+    copy_write_kib = pick(w, COPY_KERNEL, "WRITE_SIZE", max)
     fetch_scale = COPY_BYTES / (copy_fetch_kib * 1024.0)
     write_scale = COPY_BYTES / (copy_write_kib * 1024.0)
     kf = pick(f, kernel, "FETCH_SIZE") * 1024.0 * fetch_scale
