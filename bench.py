@@ -557,6 +557,64 @@ def cpu_model() -> str:
     return "unknown"
 
 
+# ------------------------------------------------------------ sustained rates
+PROBE_ITERS = 100000   # about 0.1 s per probe launch
+
+
+def sustained_rates(reps: int = 3) -> dict:
+    """The device's sustained rates in this run, beside the published peaks: bf16
+    MFMA from registers on random operands (eg_probe_mfma_bf16, one 256-thread
+    workgroup per CU, launches of about 0.1 s so power management settles), and an
+    HBM copy (torch's copy kernel over 1 GiB each way, larger than every cache)."""
+    import torch
+
+    from evograd_amd import _lib
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device="cuda").manual_seed(7)
+    operands = torch.randn(16384, device="cuda", generator=g).to(torch.bfloat16)  # 32 KiB
+    out = torch.empty(cus * 256, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def probe(iters):
+        _lib.call("eg_probe_mfma_bf16", operands.data_ptr(), out.data_ptr(), cus, iters, stream)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(ts)
+
+    probe(PROBE_ITERS // 10)
+    s = timed(lambda: probe(PROBE_ITERS))
+    if not torch.isfinite(out).all():
+        raise RuntimeError("MFMA probe produced non-finite checksums")
+    mfma_tflops = cus * 4 * PROBE_ITERS * 64 * 32768 / s / 1e12
+    n = 1 << 29  # bf16 elements: 1 GiB
+    src = torch.randn(n, device="cuda", generator=g, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    c = timed(lambda: dst.copy_(src))
+    copy_gbs = 2 * n * 2 / c / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {
+        "mfma_bf16_tflops": round(mfma_tflops, 1),
+        "mfma_frac_of_peak": round(mfma_tflops / BF16_PEAK_TFLOPS, 4),
+        "hbm_copy_gbs": round(copy_gbs, 1),
+        "hbm_copy_frac_of_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
+        "how": ("eg_probe_mfma_bf16: 64 MFMAs per wave per iteration from registers, random bf16 "
+                f"operands, {cus} workgroups x {PROBE_ITERS} iterations, median of {reps}; copy: "
+                f"torch copy_ of 1 GiB bf16, median of {reps}"),
+    }
+
+
 # ---------------------------------------------------------- profiling mode
 COPY_BYTES = 256 << 20
 
@@ -635,7 +693,8 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the token sweeps of the memory-bound operators")
     ap.add_argument("--profile", metavar="OP",
-                    help="rocprofv3 workload: STEPS x (flush, fwd, bwd) of OP plus copy calibration")
+                    help="rocprofv3 workload: STEPS x (flush, fwd, bwd) of OP plus copy calibration; "
+                         "'sustained' runs the MFMA probe and the HBM copy STEPS times")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every operator's work shards by rows, tokens or "
@@ -654,6 +713,9 @@ def main() -> int:
 
     _lib.load()
     torch.cuda.set_device(0)
+    if args.profile == "sustained":
+        print(json.dumps(sustained_rates(args.steps)), flush=True)
+        return 0
     if args.profile:
         print(json.dumps(profile_run(args.profile, args.steps)), flush=True)
         return 0
@@ -687,6 +749,18 @@ def main() -> int:
                 sweeps[name] = {"error": f"{type(e).__name__}: {e}"}
             log(f"sweep {name}: " + json.dumps({k: v.get("hbm_frac_full") if isinstance(v, dict)
                                                 else v for k, v in sweeps[name].items()}))
+
+    log("sustained rates ...")
+    try:
+        sustained = sustained_rates()
+    except Exception as e:
+        sustained = {"error": f"{type(e).__name__}: {e}"}
+    log("sustained rates: " + json.dumps({k: v for k, v in sustained.items() if k != "how"}))
+    if "mfma_bf16_tflops" in sustained:
+        for r in results.values():
+            if "mfma_frac_full" in r:
+                r["mfma_frac_full_of_sustained"] = round(
+                    r["mfma_frac_full"] * BF16_PEAK_TFLOPS / sustained["mfma_bf16_tflops"], 4)
 
     cpu = {}
     if not args.no_cpu:
@@ -742,6 +816,7 @@ def main() -> int:
         "cpu_baseline": ({k: v for k, v in cpu[HEADLINE].items() if k != "what"}
                          if HEADLINE in cpu and "value" in cpu[HEADLINE] else None),
         "cpu_model": cpu_model(),
+        "sustained": sustained,
         "ops": results,
         "sweeps": sweeps,
     }
@@ -749,6 +824,8 @@ def main() -> int:
     if traffic is not None:
         line["roofline"]["traffic"] = traffic.get("hbm_bytes_per_launch")
         line["roofline"]["traffic_source"] = "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+    if "hbm_copy_gbs" in sustained:
+        line["roofline"]["frac_of_sustained_copy"] = round(achieved / sustained["hbm_copy_gbs"], 4)
     if line["cpu_baseline"] is not None:
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 1)
     print(json.dumps(line), flush=True)

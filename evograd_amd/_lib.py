@@ -20,7 +20,7 @@ import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libevograd_hip.so")
 
 EG_F32, EG_F16, EG_BF16 = 0, 1, 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _DTYPE_TAG = {
     torch.float32: EG_F32,
@@ -58,6 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_attn_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "eg_attn_gqa_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "eg_attn_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
+    "eg_attn_gqa_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
     "eg_attn_gqa_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "eg_attn_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
     "eg_llama3_attn_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
@@ -79,6 +80,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_rmsnorm_bwd_small": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_layernorm_bwd_small": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_silu_mul": (_i32, [_p, _p, _p, _i64, _i32, _p]),
+    "eg_probe_mfma_bf16": (_i32, [_p, _p, _i32, _i32, _p]),
 }
 
 _lib = None

@@ -132,6 +132,15 @@ __device__ __forceinline__ void store_rows(uint16_t* __restrict__ row, const f32
   }
 }
 
+// The same rows as fp32 (16-byte stores), for a split walk's partial sums.
+__device__ __forceinline__ void store_rows_f32(float* __restrict__ row, const f32x16& c, int t,
+                                               int hh, float f) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    *reinterpret_cast<float4*>(row + 32 * t + 8 * g + 4 * hh) =
+        make_float4(c[4 * g + 0] * f, c[4 * g + 1] * f, c[4 * g + 2] * f, c[4 * g + 3] * f);
+}
+
 // RoPE on a query row held as MFMA operands (the decoder layer's q rotation,
 // src/evograd/ops/level3/llama3_decoder_layer/forward_ref.py:42-51, fused into the
 // forward's Q load): f[kk] holds columns 16kk + 8hh .. +7, so f[kk] and
@@ -507,7 +516,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, uint16_t* __restrict__ dk,
     uint16_t* __restrict__ dv, int S, float scale, float scale_log2, int BHkv, int group,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, int parts,
+    float* __restrict__ part) {
   using v8 = typename MM<T>::v8;
   constexpr int BK = 32 * NW;
   constexpr int KSTEPS = D / 16, DT = D / 32;
@@ -520,9 +530,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   __shared__ __align__(16) float Ls[2][BQ];
   __shared__ __align__(16) float Es[2][BQ];
 
-  int kvh, kb;
-  block_coords(BHkv, kvh, kb);  // kb = 0 (the longest walk) first
-  if (kvh >= BHkv) return;
+  // Workgroup (kv head, part of the walk, key block); with parts > 1 the walk
+  // below is cut into `parts` ranges of steps, each summed into its own fp32 slab
+  // of `part` (attn_dkdv_reduce_kernel adds the slabs in order). The parts of a
+  // kv head share its XCD when BHkv is a multiple of 8.
+  int vh, kb;
+  block_coords(BHkv * parts, vh, kb);  // kb = 0 (the longest walk) first
+  if (vh >= BHkv * parts) return;
+  const int kvh = vh % BHkv, pi = vh / BHkv;
   const int k0 = kb * BK;
   const int lane = threadIdx.x & 63, w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
@@ -564,6 +579,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   const int i_first = k0 / BQ;
   const int ntq = (S + BQ - 1) / BQ - i_first;
   const int nsteps = group * ntq;
+  const int per = (nsteps + parts - 1) / parts;
+  const int s_begin = min(nsteps, pi * per), s_end = min(nsteps, s_begin + per);
   const int wave_first_key = k0 + 32 * w;
   TileLoader<BQ, D, NW> ld;
   ld.init();
@@ -596,18 +613,18 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
     lv.init();
     lv.load(v + base, k0, S, Vk);
   }
-  if (nsteps > 0) {
-    const int64_t hb = (int64_t)qhead(0) * S * D;
-    ld.load(q + hb, qtile(0) * BQ, S, Qs0);
-    ld.load(dout + hb, qtile(0) * BQ, S, Ds0);
-    load_stats(0);
+  if (s_begin < s_end) {
+    const int64_t hb = (int64_t)qhead(s_begin) * S * D;
+    ld.load(q + hb, qtile(s_begin) * BQ, S, Qs0);
+    ld.load(dout + hb, qtile(s_begin) * BQ, S, Ds0);
+    load_stats(s_begin);
     store_stats(Ls[0], Es[0]);
   }
   auto step_fn = [&](auto bufc, int step) {
     constexpr int buf = decltype(bufc)::value;
     wait_loads();
     __syncthreads();
-    const bool more = step + 1 < nsteps;
+    const bool more = step + 1 < s_end;
     if (more) {
       const int64_t hb = (int64_t)qhead(step + 1) * S * D;
       ld.load(q + hb, qtile(step + 1) * BQ, S, buf ? Qs0 : Qs1);
@@ -720,9 +737,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
   };
   // Unrolled over the two buffers, so every LDS address is a register plus an
   // immediate and the buffers are distinct objects at compile time.
-  for (int step = 0; step < nsteps; step += 2) {
+  for (int step = s_begin; step < s_end; step += 2) {
     step_fn(std::integral_constant<int, 0>{}, step);
-    if (step + 1 < nsteps) step_fn(std::integral_constant<int, 1>{}, step + 1);
+    if (step + 1 < s_end) step_fn(std::integral_constant<int, 1>{}, step + 1);
   }
 
   if (key < S) {
@@ -735,12 +752,50 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dkdv_kernel(
       unrotate_rows<D>(dka, rope_cos + (int64_t)key * D, rope_sin + (int64_t)key * D, hh);
       fk = 1.0f;
     }
+    if (part) {  // this part's sums, scaled (and unrotated) like the direct store
+      const int64_t slab = (int64_t)BHkv * S * D;
+      float* pk = part + pi * slab + base + (int64_t)key * D;
+      float* pv = part + (parts + pi) * slab + base + (int64_t)key * D;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      store_rows<T>(dkp, dka[t], t, hh, fk);
-      store_rows<T>(dvp, dva[t], t, hh, 1.0f);
+      for (int t = 0; t < DT; ++t) {
+        store_rows_f32(pk, dka[t], t, hh, fk);
+        store_rows_f32(pv, dva[t], t, hh, 1.0f);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        store_rows<T>(dkp, dka[t], t, hh, fk);
+        store_rows<T>(dvp, dva[t], t, hh, 1.0f);
+      }
     }
   }
+}
+
+// dK, dV of a split walk: the parts' fp32 slabs ([2][parts][BHkv][S][D], dK slabs
+// first) added in part order and rounded once; 4 consecutive elements of each per
+// thread (D is a multiple of 4).
+template <typename T>
+__global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(const float* __restrict__ part,
+                                                               int parts, int64_t n,
+                                                               uint16_t* __restrict__ dk,
+                                                               uint16_t* __restrict__ dv) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  float4 a = *reinterpret_cast<const float4*>(part + i);
+  float4 b = *reinterpret_cast<const float4*>(part + parts * n + i);
+  for (int p = 1; p < parts; ++p) {
+    const float4 x = *reinterpret_cast<const float4*>(part + p * n + i);
+    const float4 y = *reinterpret_cast<const float4*>(part + (parts + p) * n + i);
+    a.x += x.x, a.y += x.y, a.z += x.z, a.w += x.w;
+    b.x += y.x, b.y += y.y, b.z += y.z, b.w += y.w;
+  }
+  uint2 u;
+  u.x = MM<T>::pack2(a.x, a.y);
+  u.y = MM<T>::pack2(a.z, a.w);
+  *reinterpret_cast<uint2*>(dk + i) = u;
+  u.x = MM<T>::pack2(b.x, b.y);
+  u.y = MM<T>::pack2(b.z, b.w);
+  *reinterpret_cast<uint2*>(dv + i) = u;
 }
 
 // ------------------------------------------------------------------- dQ
@@ -936,6 +991,28 @@ constexpr int kDkdvRows = 32;
 // workgroups of 256 keys are 3-4% slower).
 template <int D> constexpr int dkdv_waves() { return 4; }
 
+// Split walk of the dK/dV kernel: with fewer than kDkdvTarget workgroups (kv heads
+// x key blocks of 128 keys: small batches, few kv heads, short sequences), each key
+// block's walk over the query tiles of its group is cut into `parts` (at most
+// kDkdvMaxParts) whose fp32 sums go to workspace slabs, added in part order by
+// attn_dkdv_reduce_kernel. The choice depends on the shape only, so results are
+// the same on every run and device.
+constexpr int kDkdvTarget = 1024, kDkdvMaxParts = 8;
+int dkdv_parts(int64_t BHkv, int64_t S, int64_t D) {
+  if (D != 64 && D != 128) return 1;
+  const int64_t nkb = (S + 32 * dkdv_waves<128>() - 1) / (32 * dkdv_waves<128>());
+  const int64_t wgs = BHkv * nkb;
+  if (wgs <= 0 || wgs >= kDkdvTarget) return 1;
+  return (int)std::min<int64_t>(kDkdvMaxParts, (kDkdvTarget + wgs - 1) / wgs);
+}
+// Backward workspace after delta (fp32 [BH, S], rounded up to 256 bytes): the split
+// walk's slabs, 2 x parts x BHkv x S x D fp32 (none without a split).
+size_t attn_delta_bytes(int64_t BH, int64_t S) { return ((size_t)(BH * S) * 4 + 255) / 256 * 256; }
+size_t attn_part_bytes(int64_t BHkv, int64_t S, int64_t D) {
+  const int parts = dkdv_parts(BHkv, S, D);
+  return parts > 1 ? (size_t)2 * parts * BHkv * S * D * 4 : 0;
+}
+
 // The MFMA kernels take 16-bit tensors with head_dim 64 or 128; everything else
 // (fp32, other even head sizes up to 128) runs on the generic kernels
 // (attn_generic.hip).
@@ -992,6 +1069,8 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
                     const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t BH,
                     int64_t S, int group, float scale, hipStream_t st,
                     const float* rc = nullptr, const float* rs = nullptr) {
+  // The split walk's slabs follow delta in the workspace.
+  float* part = (float*)((char*)delta + attn_delta_bytes(BH, S));
   // dQ first: it also computes delta = rowsum(do * o) for its rows, which the
   // dK/dV kernel reads.
   constexpr int NQ = kDqWaves;
@@ -1004,11 +1083,18 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
   constexpr int NK = dkdv_waves<D>();
   const int nkb = (int)((S + 32 * NK - 1) / (32 * NK));
   const int64_t BHkv = BH / group;
-  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows, ROPE>), dim3(grid_for(BHkv, nkb)),
+  static_assert(NK == dkdv_waves<128>(), "dkdv_parts assumes one key-block width");
+  const int parts = dkdv_parts(BHkv, S, D);
+  EG_LAUNCH((attn_dkdv_kernel<T, D, NK, kDkdvRows, ROPE>), dim3(grid_for(BHkv * parts, nkb)),
             dim3(NK * 64), 0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
             (const uint16_t*)dout, lse, delta, (uint16_t*)dk, (uint16_t*)dv, (int)S, scale,
-            scale * kLog2e, (int)BHkv, group, rc, rs);
-  return check_launch("eg_attn_bwd(dkdv)");
+            scale * kLog2e, (int)BHkv, group, rc, rs, parts, parts > 1 ? part : nullptr);
+  if (int e = check_launch("eg_attn_bwd(dkdv)")) return e;
+  if (parts == 1) return 0;
+  const int64_t n = BHkv * S * D;
+  EG_LAUNCH((attn_dkdv_reduce_kernel<T>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st,
+            (const float*)part, parts, n, (uint16_t*)dk, (uint16_t*)dv);
+  return check_launch("eg_attn_bwd(dkdv reduce)");
 }
 
 // Explicit instantiations: hip-clang leaves some implicitly instantiated kernel
@@ -1021,7 +1107,7 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
   template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows, R>(            \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,        \
       const float*, uint16_t*, uint16_t*, int, float, float, int, int, const float*,           \
-      const float*);                                                                         \
+      const float*, int, float*);                                                            \
   template __global__ void attn_dq_kernel<T, D, kDqWaves, R>(                                \
       const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,     \
       const float*, float*, uint16_t*, int, float, float, int, int, int, const float*,         \
@@ -1047,11 +1133,15 @@ bool attn_aligned(std::initializer_list<const void*> ptrs) {
 
 using namespace eg;
 
+extern "C" size_t eg_attn_gqa_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                              int64_t seq, int64_t head_dim) {
+  if (batch <= 0 || heads <= 0 || seq <= 0 || kv_heads <= 0) return 0;
+  return attn_delta_bytes(batch * heads, seq) + attn_part_bytes(batch * kv_heads, seq, head_dim);
+}
+
 extern "C" size_t eg_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t seq,
                                           int64_t head_dim) {
-  (void)head_dim;
-  if (batch <= 0 || heads <= 0 || seq <= 0) return 0;
-  return (size_t)(batch * heads * seq) * sizeof(float);
+  return eg_attn_gqa_workspace_bytes(batch, heads, heads, seq, head_dim);
 }
 
 extern "C" int eg_attn_gqa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -1138,7 +1228,7 @@ extern "C" size_t eg_llama3_attn_workspace_bytes(int64_t batch, int64_t heads, i
                                                  int64_t seq, int64_t head_dim) {
   if (batch <= 0 || heads <= 0 || kv_heads <= 0 || seq <= 0 || head_dim <= 0) return 0;
   return llama3_ws_qr(batch, heads, seq, head_dim) + llama3_ws_kr(batch, kv_heads, seq, head_dim) +
-         (size_t)(batch * heads * seq) * sizeof(float);
+         attn_delta_bytes(batch * heads, seq) + attn_part_bytes(batch * kv_heads, seq, head_dim);
 }
 
 template <typename F>

@@ -92,7 +92,7 @@ extern "C" int eg_time_kernel_missed(void) {
   return missed;
 }
 
-extern "C" int eg_abi_version(void) { return 3; }
+extern "C" int eg_abi_version(void) { return 4; }
 
 extern "C" const char* eg_time_kernel_label(void) { return eg::g_label; }
 

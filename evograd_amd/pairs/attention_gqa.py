@@ -65,7 +65,7 @@ def causal_attention_gqa_backward_from_saved(do: torch.Tensor, saved):
     do = as_contiguous("do", do)
     B, H, S, D = q.shape
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = workspace(_lib.query("eg_attn_workspace_bytes", B, H, S, D), q.device)
+    ws = workspace(_lib.query("eg_attn_gqa_workspace_bytes", B, H, k.shape[1], S, D), q.device)
     _lib.call("eg_attn_gqa_bwd", _lib.ptr(do), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
               _lib.ptr(o), _lib.ptr(lse), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws),
               B, H, k.shape[1], S, D, 1.0 / math.sqrt(D), tag(q.dtype), _lib.stream_of(q))

@@ -323,7 +323,7 @@ def llama3_decoder_layer_backward_from_saved(dout, saved, eps: float = 1e-5):
     ops.split(do_, doh, s, s.H, s.q_out, 0)
     del do_
     dqh, dkh, dvh = torch.empty_like(qh), torch.empty_like(kh), torch.empty_like(vh)
-    ws = workspace(_lib.query("eg_attn_workspace_bytes", s.B, s.H, s.T, s.D), x.device)
+    ws = workspace(_lib.query("eg_attn_gqa_workspace_bytes", s.B, s.H, s.KVH, s.T, s.D), x.device)
     _lib.call("eg_attn_gqa_bwd", _lib.ptr(doh), _lib.ptr(qh), _lib.ptr(kh), _lib.ptr(vh),
               _lib.ptr(oh), _lib.ptr(lse), _lib.ptr(dqh), _lib.ptr(dkh), _lib.ptr(dvh),
               _lib.ptr(ws), s.B, s.H, s.KVH, s.T, s.D, 1.0 / math.sqrt(s.D), ops.tg, ops.st)

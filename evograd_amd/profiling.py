@@ -4,6 +4,7 @@
     python -m evograd_amd.profiling counters <prefix>_counter_collection.csv [FILTER]
     python -m evograd_amd.profiling traffic  FETCH.csv WRITE.csv KERNEL_SUBSTRING [KEY]
     python -m evograd_amd.profiling mfma     COUNTERS.csv KERNEL_STATS.csv [FILTER] [GHZ]
+    python -m evograd_amd.profiling clock    COUNTERS.csv [FILTER]
 
 ``traffic`` turns the FETCH_SIZE and WRITE_SIZE readings (KiB per dispatch,
 summed over the L2 channels) of one kernel into HBM bytes per launch, scaled by
@@ -106,6 +107,47 @@ def mfma(counter_csv: str, stats_csv: str, filt: str = "", ghz: float = 2.4) -> 
     return "\n".join(lines)
 
 
+def clock(counter_csv: str, filt: str = "", shader_engines: int = 32, simds: int = 1024,
+          nominal_ghz: float = 2.4) -> str:
+    """Effective engine clock and MFMA busy share per kernel, from one counter run
+    holding SQ_BUSY_CYCLES and SQ_VALU_MFMA_BUSY_CYCLES. SQ_BUSY_CYCLES is summed
+    over the shader engines (32 on an MI355X: the agent's Num_Shader_Banks), so
+    busy / engines / dispatch duration is the clock the kernel ran at;
+    SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x those cycles) is the share of cycles the
+    matrix cores were busy. A fraction of the published peak is the product of the
+    two: busy share x clock / nominal clock. Durations are the counter rows'
+    dispatch timestamps; the median over a kernel's dispatches is reported."""
+    per = collections.defaultdict(lambda: collections.defaultdict(dict))
+    span = {}
+    for r in csv.DictReader(open(counter_csv)):
+        k, d = r["Kernel_Name"], r["Dispatch_Id"]
+        cs = per[k][d]
+        cs[r["Counter_Name"]] = cs.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        span[(k, d)] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
+    lines = ["| kernel | dispatches | median us | clock GHz | MFMA busy % of cycles | "
+             f"fraction of peak at {nominal_ghz} GHz |", "|---|---:|---:|---:|---:|---:|"]
+    for k, ds in per.items():
+        if filt and filt not in k:
+            continue
+        rows = []
+        for d, cs in ds.items():
+            t = span[(k, d)]
+            busy, mfma = cs.get("SQ_BUSY_CYCLES"), cs.get("SQ_VALU_MFMA_BUSY_CYCLES")
+            if not busy or t <= 0:
+                continue
+            cyc = busy / shader_engines
+            share = (mfma or 0.0) / (simds * cyc)
+            rows.append((t, cyc / t / 1e9, share))
+        if not rows:
+            continue
+        t = statistics.median(r[0] for r in rows)
+        ghz = statistics.median(r[1] for r in rows)
+        share = statistics.median(r[2] for r in rows)
+        lines.append(f"| `{short_name(k)}` | {len(rows)} | {t * 1e6:.1f} | {ghz:.3f} | "
+                     f"{100 * share:.1f} | {100 * share * ghz / nominal_ghz:.1f}% |")
+    return "\n".join(lines)
+
+
 def traffic(fetch_csv: str, write_csv: str, kernel: str, key: str = "") -> dict:
     f, w = _counter_table(fetch_csv), _counter_table(write_csv)
 
@@ -151,6 +193,8 @@ def main(argv: list) -> int:
     elif cmd == "mfma":
         print(mfma(argv[1], argv[2], argv[3] if len(argv) > 3 else "",
                    float(argv[4]) if len(argv) > 4 else 2.4))
+    elif cmd == "clock":
+        print(clock(argv[1], argv[2] if len(argv) > 2 else ""))
     elif cmd == "traffic":
         print(json.dumps(traffic(argv[1], argv[2], argv[3], argv[4] if len(argv) > 4 else ""), indent=1))
     else:

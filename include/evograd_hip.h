@@ -224,8 +224,14 @@ int eg_attn_gqa_fwd(const void* q, const void* k, const void* v, void* o, float*
                     int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                     int64_t head_dim, float scale, int dtype, void* stream);
 
-/* Bytes of workspace eg_attn_bwd / eg_attn_gqa_bwd need: delta = rowsum(do * o),
- * fp32 [batch, heads, seq] (heads = query heads). */
+/* Bytes of workspace eg_attn_gqa_bwd needs: delta = rowsum(do * o), fp32 [batch,
+ * heads, seq] (heads = query heads), rounded up to 256 bytes; then, for shapes with
+ * fewer than 1024 (kv head, 128-key block) pairs, where the dK/dV walk over the
+ * query tiles is split into parts (at most 8, a choice of the shape alone), the
+ * parts' fp32 sums: 2 x parts x batch x kv_heads x seq x head_dim x 4 bytes.
+ * eg_attn_workspace_bytes (for eg_attn_bwd) is this with kv_heads = heads. */
+size_t eg_attn_gqa_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                   int64_t seq, int64_t head_dim);
 size_t eg_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t seq,
                                int64_t head_dim);
 
@@ -239,7 +245,7 @@ int eg_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
 /* Backward of eg_attn_gqa_fwd: dq [batch, heads, seq, head_dim]; dk, dv [batch,
  * kv_heads, seq, head_dim], each the sum over the heads/kv_heads query heads that
  * share the kv head (the gradient of the repeat_interleave), accumulated in fp32
- * in a fixed order. */
+ * in a fixed order. Workspace: eg_attn_gqa_workspace_bytes. */
 int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* v,
                     const void* o, const float* lse, void* dq, void* dk, void* dv,
                     void* workspace, int64_t batch, int64_t heads, int64_t kv_heads,
@@ -255,8 +261,9 @@ int eg_attn_gqa_bwd(const void* dout, const void* q, const void* k, const void* 
  * [batch, heads, seq] of the rotated scores. The backward takes the pre-rotation
  * q, k and rotates them again: the saved state holds no rotated copy. dq and dk
  * are the gradients of the pre-rotation q and k.
- * Workspace: the backward's holds q_r, k_r (dtype), then delta fp32 [batch, heads,
- * seq] (eg_llama3_attn_workspace_bytes); the forward's needs only batch * kv_heads
+ * Workspace: the backward's holds q_r, k_r (dtype), then what eg_attn_gqa_bwd's
+ * workspace holds (delta, and the split dK/dV walk's sums for shapes that split it)
+ * (eg_llama3_attn_workspace_bytes); the forward's needs only batch * kv_heads
  * * seq * head_dim elements of dtype (its rotated keys). */
 size_t eg_llama3_attn_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
                                       int64_t seq, int64_t head_dim);
@@ -404,6 +411,17 @@ int eg_add(const void* a, const void* b, void* c, int64_t n, int dtype, void* st
  * the MLP activation of forward_ref.py:115-116 (unlike the level-1 SwiGLU, which
  * rounds silu first). Its backward is eg_swiglu_bwd's formula. */
 int eg_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/* ---- measurement aid (no counterpart in the reference) ---------------------
+ * Sustained bf16 MFMA rate, for reading the roofline fractions of the MFMA-bound
+ * kernels (bench.py reports it beside the published peak): `workgroups` 256-thread
+ * workgroups (pass the CU count: one per CU, one wave per SIMD) each run `iters`
+ * iterations of 64 v_mfma_f32_32x32x16_bf16 per wave from registers, on operands
+ * taken from `operands` (32 KiB, 16-byte aligned, random bf16 values: the clock
+ * the device holds depends on how much the operand bits toggle). Work:
+ * workgroups x 4 x iters x 64 x 32768 FLOP. `out` receives workgroups x 256 floats
+ * (checksums that keep the work live). */
+int eg_probe_mfma_bf16(const void* operands, float* out, int workgroups, int iters, void* stream);
 
 #ifdef __cplusplus
 }

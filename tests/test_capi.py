@@ -86,6 +86,24 @@ def test_flce_scratch_grows_with_the_chunk_not_with_rows_times_vocab():
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_attention_workspace_holds_the_split_walk_only_when_split():
+    """delta (fp32 [batch, heads, seq], rounded up to 256 bytes), plus the split dK/dV
+    walk's fp32 slabs (2 x parts x batch x kv_heads x seq x head_dim) when fewer than
+    1024 (kv head, 128-key block) pairs exist: parts = min(8, ceil(1024 / pairs))."""
+    al = lambda n: (n + 255) // 256 * 256
+    q = lambda *a: _lib.query("eg_attn_gqa_workspace_bytes", *a)
+    assert q(4, 32, 8, 4096, 128) == al(4 * 32 * 4096 * 4)          # 1024 pairs: no split
+    assert q(1, 32, 8, 4096, 128) == al(32 * 4096 * 4) + 2 * 4 * 8 * 4096 * 128 * 4
+    assert q(1, 32, 8, 1024, 128) == al(32 * 1024 * 4) + 2 * 8 * 8 * 1024 * 128 * 4
+    assert q(2, 8, 2, 300, 64) == al(2 * 8 * 300 * 4) + 2 * 8 * 4 * 300 * 64 * 4
+    assert q(1, 4, 4, 64, 48) == al(4 * 64 * 4)                      # generic kernels
+    assert _lib.query("eg_attn_workspace_bytes", 4, 32, 4096, 128) == al(4 * 32 * 4096 * 4)
+    assert _lib.query("eg_attn_workspace_bytes", 1, 32, 4096, 128) == q(1, 32, 32, 4096, 128)
+    lq = _lib.query("eg_llama3_attn_workspace_bytes", 1, 32, 8, 1024, 128)
+    assert lq == 2 * (32 + 8) * 1024 * 128 + q(1, 32, 8, 1024, 128)
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
 def test_host_side_validation_errors_without_gpu():
     """Argument errors are reported before any launch (no device needed)."""
     with pytest.raises(RuntimeError, match="negative"):
@@ -106,6 +124,10 @@ def test_host_side_validation_errors_without_gpu():
     with pytest.raises(RuntimeError, match="more than the 16777216-byte scratch"):
         _lib.call("eg_rmsnorm_bwd_noalloc", 16, 16, 16, 16, 16, 16, 16384, 16384,
                   _lib.EG_BF16, None)
+    with pytest.raises(RuntimeError, match="null"):
+        _lib.call("eg_probe_mfma_bf16", None, None, 256, 1, None)
+    with pytest.raises(RuntimeError, match="workgroups"):
+        _lib.call("eg_probe_mfma_bf16", 16, 16, 0, 1, None)
     # empty inputs are a no-op, not an error
     _lib.call("eg_softmax_fwd", None, None, 0, 0, _lib.EG_F32, None)
     _lib.call("eg_cross_entropy_bwd", None, None, None, None, None, None, 0, 8, -100,

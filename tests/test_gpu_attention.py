@@ -112,6 +112,16 @@ def test_attention_gqa_backward_is_bitwise_deterministic():
     assert all(torch.equal(x, y) for x, y in zip(a, b))
 
 
+def test_attention_gqa_split_dkdv_walk():
+    """Few (kv head, key block) pairs: the dK/dV walk is cut into parts summed in
+    fp32 slabs (B=1, 8 kv heads, 8 key blocks: 8 parts), held to the oracle like
+    every other workload, and repeatable bitwise."""
+    w = Workload(dims=dict(B=1, H=32, KVH=8, S=1024, D=128), dtype="bfloat16")
+    _note("gqa split walk", w.dims)
+    rep = verify(GQA, pair_module("causal_attention_gqa"), device="cuda", workloads=(w,))
+    assert rep.ok, "\n".join(rep.failures())
+
+
 def test_attention_gqa_llama3_8b_config():
     w = GQA.benchmark[0]
     _note("gqa llama3_8b", w.dims)
