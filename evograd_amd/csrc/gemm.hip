@@ -47,6 +47,7 @@
 // per XCD, so the workgroups in flight on one XCD share B panels in its L2.
 #include "eg_common.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace eg {
@@ -178,14 +179,7 @@ template <> __device__ __forceinline__ void put<f16_t>(f16_t* p, float v) { *p =
 // m-fastest over all m tiles, 16 x 2 in flight: logits 4.38 -> 3.96 ms at
 // 4096 x 128256 x 4096).
 constexpr int kGroupM = 4;
-__device__ __forceinline__ void tile_of(int tiles_m, int tiles, int& tm, int& tn) {
-  const int i = blockIdx.x;
-  const int per = (tiles + 7) / 8;
-  const int t = (i % 8) * per + i / 8;
-  if (t >= tiles) {
-    tn = -1;
-    return;
-  }
+__device__ __forceinline__ void tile_decode(int t, int tiles_m, int tiles, int& tm, int& tn) {
   const int tiles_n = tiles / tiles_m;
   const int g = t / (kGroupM * tiles_n);
   const int gm = min(kGroupM, tiles_m - g * kGroupM);
@@ -193,6 +187,22 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles, int& tm, int& tn
   tm = g * kGroupM + r % gm;
   tn = r / gm;
 }
+// Workgroups [0, round8(head)) take tiles [0, head) whole, XCD-contiguously as
+// above. A split tail (tail > 0): workgroup head + j takes tile head + j % tail and
+// k part j / tail. Returns the tile order index t (-1: no tile) and the part.
+__device__ __forceinline__ int tile_index(int head, int tail, int& kpart) {
+  const int i = blockIdx.x;
+  kpart = -1;
+  if (tail > 0 && i >= head) {
+    const int j = i - head;
+    kpart = j / tail;
+    return head + j % tail;
+  }
+  const int per = (head + 7) / 8;
+  const int t = (i % 8) * per + i / 8;
+  return t < head ? t : -1;
+}
+constexpr int kTileElems = kBM * kBN;  // one fp32 partial tile of a split tail
 
 // Softmax epilogue of the logits product (SMX): target [M], per-group statistics
 // [M][nh2][2] and the target logits [M].
@@ -223,16 +233,18 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                  int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c,
                  SmxArgs smx, const void* R, int64_t ldr, int r_f32, int kt_per,
-                 float* __restrict__ part) {
+                 float* __restrict__ part, int head, int tail) {
   using v8 = typename GM<T>::v8;
   // Two separate buffers per operand, selected at compile time in the unrolled k
   // loop: the LDS reads of one buffer provably do not alias the loads in flight
   // into the other, so they need not wait for them.
   __shared__ __align__(16) uint16_t As0[kSliceElems], As1[kSliceElems];
   __shared__ __align__(16) uint16_t Bs0[kSliceElems], Bs1[kSliceElems];
+  int kpart;
+  const int t_idx = tile_index(head, tail, kpart);
+  if (t_idx < 0) return;
   int tm, tn;
-  tile_of(tiles_m, tiles, tm, tn);
-  if (tn < 0) return;
+  tile_decode(t_idx, tiles_m, tiles, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int lane = threadIdx.x & 63, w = gwave();
   const int wm = (w >> 1) * 128, wn = (w & 1) * 128;
@@ -242,11 +254,14 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   la.init(lda);
   lb.init(ldb);
   const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
-  // Split K (part != nullptr): workgroup row blockIdx.y takes k slices
-  // [kb, kb + kt_per) and writes its fp32 partial tile to part[blockIdx.y].
+  // Split K: with part != nullptr and no split tail, workgroup row blockIdx.y takes
+  // k slices [kb, kb + kt_per) and writes its fp32 partial tile to the [M][N] slab
+  // part[blockIdx.y]; a split tail's workgroup (kpart >= 0) takes slices of part
+  // kpart and writes a tile-major partial (splitk_tail_reduce_kernel sums them).
+  const bool partial = part && (tail == 0 || kpart >= 0);
   const int nk_all = (K + kBK - 1) / kBK;
-  const int kb = part ? (int)blockIdx.y * kt_per : 0;
-  const int nk = part ? min(nk_all, kb + kt_per) : nk_all;
+  const int kb = partial ? (tail ? kpart : (int)blockIdx.y) * kt_per : 0;
+  const int nk = partial ? min(nk_all, kb + kt_per) : nk_all;
   // The k loop runs an even number of steps (two per iteration, one per buffer). A
   // slice at or past nk loads through an empty buffer range, which fills its LDS
   // slots with zeros (the bounded-access rules in eg_common.hpp): the step past the
@@ -358,7 +373,23 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 
   // C tile (i, j): lane l holds row l%32, register r holds column 8(r/4) + 4(l/32) + r%4.
   const int hh = lane >> 5, l32 = lane & 31;
-  if (part) {
+  if (partial && tail) {
+    // a split tail's partial: tile-major [kpart][tail tile][256][256], whole tiles
+    // (rows and columns past M, N hold sums of zeros and are never read back)
+    float* pt = part + ((int64_t)kpart * tail + (t_idx - head)) * kTileElems;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(pt + (wm + 32 * i + l32) * kBN + wn + 32 * j + 8 * q + 4 * hh) =
+              f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                    acc[i][j][4 * q + 3]};
+    return;
+  }
+  if (partial) {
     // split-K partial: fp32 [M][N] slab of this k range, summed by splitk_reduce_kernel
     float* slab = part + (int64_t)blockIdx.y * M * N;
 #pragma unroll
@@ -608,6 +639,50 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
   store_f32<TC, V>(C + (int64_t)row * ldc + col, v);
 }
 
+// The split tail's tiles: parts summed in order, the residual added, one rounding.
+// Thread = 4 consecutive columns of one row of one tail tile.
+template <typename TC>
+__global__ __launch_bounds__(256) void splitk_tail_reduce_kernel(
+    const float* __restrict__ part, int parts, int head, int tail, int tiles_m, int tiles, int M,
+    int N, TC* C, int64_t ldc, const void* R, int64_t ldr, int r_f32, int vec_c) {
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e >= (int64_t)tail * kTileElems) return;
+  const int tt = (int)(e / kTileElems), rc = (int)(e % kTileElems);
+  const int r = rc / kBN, c = rc % kBN;
+  int tm, tn;
+  tile_decode(head + tt, tiles_m, tiles, tm, tn);
+  const int row = tm * kBM + r, col = tn * kBN + c;
+  if (row >= M || col >= N) return;
+  float v[4];
+  load_f32<float, 4>(part + e, v);
+  for (int p = 1; p < parts; ++p) {
+    float w[4];
+    load_f32<float, 4>(part + (int64_t)p * tail * kTileElems + e, w);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] += w[q];
+  }
+  TC* crow = C + (int64_t)row * ldc;
+  if (vec_c && col + 3 < N) {
+    if (R) {
+      float rr[4];
+      if (r_f32) load_f32<float, 4>((const float*)R + (int64_t)row * ldr + col, rr);
+      else load_f32<TC, 4>((const TC*)R + (int64_t)row * ldr + col, rr);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] += rr[q];
+    }
+    store_f32<TC, 4>(crow + col, v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (col + q >= N) break;
+      float x = v[q];
+      if (R) x += r_f32 ? ((const float*)R)[(int64_t)row * ldr + col + q]
+                        : to_f32(((const TC*)R)[(int64_t)row * ldr + col + q]);
+      put<TC>(crow + col + q, x);
+    }
+  }
+}
+
 }  // namespace
 
 // Split-K: when the output has fewer tiles than kSplitTarget (one per CU of an
@@ -627,10 +702,40 @@ int gemm_splits(int64_t M, int64_t N, int64_t K) {
   return (int)((nk + per - 1) / per);
 }
 
+// Split tail: a product of more than one wave of tiles (kSplitTarget workgroups per
+// wave) whose last wave is at most half full runs that wave's tiles in k parts,
+// min(kMaxTailParts, kSplitTarget / tail, slices / kMinSliceRun) of them, so that the
+// last wave fills the device (an 896-tile product: 3.5 waves -> 3 + 2 x 0.5); the
+// parts' fp32 tiles are summed in order by splitk_tail_reduce_kernel. Shape-only.
+constexpr int kMaxTailParts = 4;
+struct TailPlan {
+  int64_t head, tail;
+  int parts, kt_per;
+};
+TailPlan gemm_tail(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  const int64_t nk = (K + kBK - 1) / kBK;
+  TailPlan p{tiles, 0, 1, 0};
+  if (gemm_splits(M, N, K) > 1) return p;
+  const int64_t waves = (tiles + kSplitTarget - 1) / kSplitTarget;
+  const int64_t rem = tiles - (waves - 1) * kSplitTarget;
+  if (waves < 2 || rem > kSplitTarget / 2) return p;
+  const int64_t s = std::min<int64_t>({kMaxTailParts, kSplitTarget / rem, nk / kMinSliceRun});
+  if (s < 2) return p;
+  const int64_t per = (nk + s - 1) / s;
+  p.head = tiles - rem;
+  p.tail = rem;
+  p.kt_per = (int)per;
+  p.parts = (int)((nk + per - 1) / per);
+  return p;
+}
+
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int s = gemm_splits(M, N, K);
-  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+  if (s > 1) return (size_t)s * M * N * sizeof(float);
+  const TailPlan p = gemm_tail(M, N, K);
+  return p.tail ? (size_t)p.parts * p.tail * kTileElems * sizeof(float) : 0;
 }
 
 // C[M][N] = A B in fp32 accumulation; see the file comment for the layouts.
@@ -725,20 +830,30 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
   // 16-byte aligned base; otherwise the kernel stores element by element.
   const int vec_c = (ldc % 4 == 0) && aligned16(C) &&
                     (!R || ((ldr % 4 == 0) && aligned16(R)));
+  const bool ws_ok = ws && aligned16(ws) && ws_bytes >= gemm_workspace_bytes(M, N, K);
   int splits = gemm_splits(M, N, K);
-  if (splits > 1 && (!ws || ws_bytes < gemm_workspace_bytes(M, N, K) || !aligned16(ws)))
-    splits = 1;
+  if (splits > 1 && !ws_ok) splits = 1;
+  TailPlan tp = gemm_tail(M, N, K);
+  if (!ws_ok) tp = TailPlan{tiles, 0, 1, 0};
   const int nk = (int)((K + kBK - 1) / kBK);
-  const int kt_per = (nk + splits - 1) / splits;
+  const int kt_per = tp.tail ? tp.kt_per : (nk + splits - 1) / splits;
+  const unsigned grid_x = tp.tail ? (unsigned)(tp.head + tp.tail * tp.parts) : grid;
   auto go = [&](auto tag, auto ctag, auto akc, auto bkc) {
     using T = decltype(tag);
     using TC = decltype(ctag);
-    float* part = splits > 1 ? (float*)ws : nullptr;
+    float* part = (splits > 1 || tp.tail) ? (float*)ws : nullptr;
     EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>),
-              dim3(grid, (unsigned)splits), dim3(kThreads), 0, st, (const uint16_t*)A,
+              dim3(grid_x, (unsigned)splits), dim3(kThreads), 0, st, (const uint16_t*)A,
               (const uint16_t*)B, (TC*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows,
-              (int)tiles_m, (int)tiles, vec_c, SmxArgs{}, R, ldr, (int)r_f32, kt_per, part);
+              (int)tiles_m, (int)tiles, vec_c, SmxArgs{}, R, ldr, (int)r_f32, kt_per, part,
+              (int)tp.head, (int)tp.tail);
     if (int e = check_launch(name)) return e;
+    if (tp.tail) {
+      EG_LAUNCH((splitk_tail_reduce_kernel<TC>), dim3((unsigned)(tp.tail * (kTileElems / 1024))),
+                dim3(256), 0, st, (const float*)part, tp.parts, (int)tp.head, (int)tp.tail,
+                (int)tiles_m, (int)tiles, (int)M, (int)N, (TC*)C, ldc, R, ldr, (int)r_f32, vec_c);
+      return check_launch(name);
+    }
     if (splits == 1) return 0;
     const bool v4 = (N % 4 == 0) && vec_c;
     const int64_t n = M * N / (v4 ? 4 : 1);
@@ -800,7 +915,7 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M,
     EG_LAUNCH((gemm_kernel<T, true, true, T, true>), dim3(grid), dim3(kThreads), 0, st,
               (const uint16_t*)x, (const uint16_t*)w, (T*)e, (int)M, (int)N, (int)K, ldx, ldw,
               lde, M, N, (int)tiles_m, (int)tiles, vec_c, smx, (const void*)nullptr, (int64_t)0,
-              0, 0, (float*)nullptr);
+              0, 0, (float*)nullptr, (int)tiles, 0);
     return check_launch(name);
   };
   return dtype == EG_BF16 ? go(bf16_t{}) : go(f16_t{});

@@ -86,6 +86,25 @@ def test_flce_scratch_grows_with_the_chunk_not_with_rows_times_vocab():
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_gemm_workspace_split_k_and_split_tail():
+    """Split k (fewer than 128 tiles of 256 x 256): splits x M x N fp32. Split tail
+    (more than 256 tiles, the last wave of 256 at most half full): parts x tail tiles
+    of 256 x 256 fp32, parts = min(4, 256 / tail, slices / 4) rounded to whole slices."""
+    q = lambda m, n, k: _lib.query("eg_gemm_workspace_bytes", m, n, k, _lib.EG_BF16)
+    tile = 256 * 256 * 4
+    assert q(1024, 1024, 4096) == 16 * 1024 * 1024 * 4        # 16 tiles: 16 splits
+    assert q(4096, 4096, 4096) == 0                          # one full wave
+    assert q(8192, 8192, 8192) == 0                          # 4 full waves
+    assert q(4096, 14336, 4096) == 2 * 128 * tile            # 896 tiles: 128 in 2 parts
+    assert q(14336, 4096, 4096) == 2 * 128 * tile
+    assert q(2048, 14336, 4096) == 0                         # 448 tiles: last wave 3/4 full
+    assert q(128256, 4096, 4096) == 3 * 80 * tile            # 8016 tiles: 80 in 3 parts
+    assert q(4300, 4000, 704) == 2 * 16 * tile               # 272 tiles, 11 slices
+    assert q(4300, 4000, 448) == 0                           # 7 slices: no two runs of 4
+    assert _lib.query("eg_gemm_workspace_bytes", 4096, 14336, 4096, _lib.EG_F32) == 0
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
 def test_attention_workspace_holds_the_split_walk_only_when_split():
     """delta (fp32 [batch, heads, seq], rounded up to 256 bytes), plus the split dK/dV
     walk's fp32 slabs (2 x parts x batch x kv_heads x seq x head_dim) when fewer than

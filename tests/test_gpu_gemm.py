@@ -159,11 +159,19 @@ def test_gemm_residual_fp32_path():
 @pytest.mark.parametrize("M,N,K,akc,bkc", [(1024, 1024, 4096, True, True),
                                            (300, 700, 2048, True, False),
                                            (512, 256, 1000, False, False),
-                                           (1024, 4096, 14336, True, True)])
+                                           (1024, 4096, 14336, True, True),
+                                           # split tails: 272 tiles (the last 16 in 2 parts)
+                                           (4300, 4000, 704, True, True),
+                                           (4300, 4000, 704, True, False),
+                                           (4300, 4000, 704, False, False),
+                                           (4300, 4000, 704, False, True),
+                                           # 896 tiles: the last 128 in 2 parts
+                                           (4096, 14336, 1024, True, True)])
 def test_gemm_split_k_matches_unsplit_and_is_repeatable(cdt, M, N, K, akc, bkc):
-    """Few output tiles and a workspace: k splits into fp32 partials summed in a fixed
-    order, the residual added and c rounded once. Against the unsplit product: the
-    same sum in another order (fp32), and bitwise equal run to run."""
+    """Few output tiles (split k) or a last wave of tiles at most half full (split
+    tail), and a workspace: k parts into fp32 partials summed in a fixed order, the
+    residual added and c rounded once. Against the unsplit product: the same sum in
+    another order (fp32), and bitwise equal run to run."""
     print(f"\n[gpu-gemm] split-K {M}x{N}x{K} {cdt}", flush=True)
     need = _lib.query("eg_gemm_workspace_bytes", M, N, K, _lib.EG_BF16)
     assert need > 0
