@@ -187,8 +187,9 @@ DOMINANT = {
     "fused_linear_cross_entropy": ("fwd", "gemm_kernel", 5),
     # bf16 rows of 128256: the backward's y held in registers as raw packs
     "softmax@vocab": ("bwd", "softmax_bwd_lds", 0),
-    # the decoder layer's gate projection h2 Wg^T: its 5th product (after q, k, v, o)
-    **{f"{LAYER}@llama3_8b_T{t}": ("fwd", "gemm_kernel", 4) for t in (1024, 2048, 4096)},
+    # the decoder layer's gate and up projections, one product over the segmented
+    # weights [Wg; Wu]: its 3rd product (after [q | k | v] and o)
+    **{f"{LAYER}@llama3_8b_T{t}": ("fwd", "gemm_kernel", 2) for t in (1024, 2048, 4096)},
 }
 
 
@@ -208,8 +209,8 @@ def dominant_work(name: str, w, work: dict) -> float:
     if name in ("causal_attention", "causal_attention_gqa", "llama3_attention"):
         # dK/dV kernel: S, dP, dV, dK of the five products
         return work["bwd"] * 4 / 5
-    if name == LAYER:  # the gate projection h2 Wg^T
-        return 2.0 * d["B"] * d["T"] * d["hidden"] * d["intermediate"]
+    if name == LAYER:  # the gate and up projections as one product h2 [Wg; Wu]^T
+        return 2.0 * d["B"] * d["T"] * d["hidden"] * 2 * d["intermediate"]
     phase = DOMINANT[name][0]
     return work[phase]
 

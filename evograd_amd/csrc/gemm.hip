@@ -213,6 +213,68 @@ struct SmxArgs {
   int nh2;
 };
 
+// Operand segments: the product's operands may be concatenations, along one of
+// M, N or K, of up to kMaxSegs separate buffers that share a row stride (the
+// projections of one input by several weights, or their gradients, as one product).
+// Segment s covers [start[s], start[s + 1]) of that dimension; every start is a
+// multiple of the tile (256 along M or N, 64 along K), so a workgroup's tile (M, N)
+// or a k slice (K) lies in one segment. a/b/c[s] point at element (start[s]) of
+// the segmented dimension of each operand that the dimension indexes (null: that
+// operand is the single buffer passed as usual): along M, A (rows m of a k-contiguous
+// A, columns of a k-major one) and C (rows); along N, B and C (columns); along K,
+// A and B.
+constexpr int kMaxSegs = 4;
+enum SegDim { kSegNone = 0, kSegM = 1, kSegN = 2, kSegK = 3 };
+struct SegArgs {
+  int dim, n;
+  int start[kMaxSegs + 1];
+  const void* a[kMaxSegs];
+  const void* b[kMaxSegs];
+  void* c[kMaxSegs];
+};
+__device__ __forceinline__ int seg_of(const SegArgs& g, int idx) {
+  int s = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i) s += (i < g.n && idx >= g.start[i]) ? 1 : 0;
+  return s;
+}
+// Base, shift and element bound of one operand [rows][ld]: element (r, c) of the
+// product's view is at base + r * ld + c - shift, and bytes past `end` elements
+// (from base) read as zero.
+struct OpView {
+  const uint16_t* base;
+  int64_t shift, end;
+};
+template <bool KC>
+__device__ __forceinline__ OpView seg_view(const uint16_t* plain, int64_t rows, int64_t ld,
+                                           const SegArgs& g, const void* const* tab, bool along_k,
+                                           int idx) {
+  OpView v{plain, 0, rows * ld};
+  if (g.dim == kSegNone || (g.dim == kSegK) != along_k) return v;
+  const int s = seg_of(g, idx);
+  if (!tab[s]) return v;
+  const int64_t st = g.start[s], en = g.start[s + 1];
+  v.base = (const uint16_t*)tab[s];
+  // the segmented dimension runs along the operand's rows (k-contiguous operand
+  // segmented along M or N; k-major along K) or along its columns
+  const bool rows_seg = KC != along_k;
+  v.shift = rows_seg ? st * ld : st;
+  v.end = rows_seg ? (en - st) * ld : rows * ld;
+  return v;
+}
+
+// Address of C element (row, col) under the segments of C (see SegArgs).
+template <typename TC>
+__device__ __forceinline__ TC* c_at(TC* C, int64_t ldc, const SegArgs& g, int row, int col) {
+  if (g.dim == kSegM || g.dim == kSegN) {
+    const int sg = seg_of(g, g.dim == kSegM ? row : col);
+    if (g.c[sg])
+      return (TC*)g.c[sg] + ((int64_t)row * ldc + col -
+                             (g.dim == kSegM ? (int64_t)g.start[sg] * ldc : g.start[sg]));
+  }
+  return C + (int64_t)row * ldc + col;
+}
+
 // One accumulator value read out of its AGPR. The "a" operand keeps the
 // accumulators in AGPRs through the k loop when an epilogue feeds them to VALU
 // work (otherwise the allocator moves them to VGPRs and spills inside the loop).
@@ -233,7 +295,7 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                  int64_t a_rows, int64_t b_rows, int tiles_m, int tiles, int vec_c,
                  SmxArgs smx, const void* R, int64_t ldr, int r_f32, int kt_per,
-                 float* __restrict__ part, int head, int tail) {
+                 float* __restrict__ part, int head, int tail, SegArgs seg) {
   using v8 = typename GM<T>::v8;
   // Two separate buffers per operand, selected at compile time in the unrolled k
   // loop: the LDS reads of one buffer provably do not alias the loads in flight
@@ -253,7 +315,6 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   SliceLoader<BKC> lb;
   la.init(lda);
   lb.init(ldb);
-  const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
   // Split K: with part != nullptr and no split tail, workgroup row blockIdx.y takes
   // k slices [kb, kb + kt_per) and writes its fp32 partial tile to the [M][N] slab
   // part[blockIdx.y]; a split tail's workgroup (kpart >= 0) takes slices of part
@@ -306,15 +367,21 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  // Segmented operands (seg.dim): along M or N the tile's segment is fixed for the
+  // workgroup; along K each slice picks its segment.
+  const OpView va_t = seg_view<AKC>(A, a_rows, lda, seg, seg.a, false, m0);
+  const OpView vb_t = seg_view<BKC>(B, b_rows, ldb, seg, seg.b, false, n0);
   auto loadA = [&](int kt, uint16_t* as) {
     const int k0 = kt * kBK;
-    const int64_t oa = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
-    la.load(A + oa, kt < nk ? (a_end - oa) * 2 : 0, as);
+    const OpView va = seg.dim == kSegK ? seg_view<AKC>(A, a_rows, lda, seg, seg.a, true, k0) : va_t;
+    const int64_t oa = (AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0) - va.shift;
+    la.load(va.base + oa, kt < nk ? (va.end - oa) * 2 : 0, as);
   };
   auto loadB = [&](int kt, uint16_t* bs) {
     const int k0 = kt * kBK;
-    const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
-    lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
+    const OpView vb = seg.dim == kSegK ? seg_view<BKC>(B, b_rows, ldb, seg, seg.b, true, k0) : vb_t;
+    const int64_t ob = (BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0) - vb.shift;
+    lb.load(vb.base + ob, kt < nk ? (vb.end - ob) * 2 : 0, bs);
   };
   loadA(kb, As0);
   loadB(kb, Bs0);
@@ -507,11 +574,21 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     else rows_of(std::false_type{});
     return;
   }
+  // C of the tile's segment (along M: rows; along N: columns)
+  TC* cb = C;
+  int64_t cshift = 0;
+  if (seg.dim == kSegM || seg.dim == kSegN) {
+    const int sg = seg_of(seg, seg.dim == kSegM ? m0 : n0);
+    if (seg.c[sg]) {
+      cb = (TC*)seg.c[sg];
+      cshift = seg.dim == kSegM ? (int64_t)seg.start[sg] * ldc : seg.start[sg];
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = m0 + wm + 32 * i + l32;
     if (row >= M) continue;
-    TC* crow = C + (int64_t)row * ldc;
+    TC* crow = cb + ((int64_t)row * ldc - cshift);
     // residual row: of TC, or fp32 (r_f32: a running fp32 sum rounded into C)
     const TC* rrow = R ? (const TC*)R + (int64_t)row * ldr : nullptr;
     const float* rrow32 = R ? (const float*)R + (int64_t)row * ldr : nullptr;
@@ -616,7 +693,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 template <typename TC, int V>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(
     const float* __restrict__ part, int splits, int M, int N, TC* C, int64_t ldc, const void* R,
-    int64_t ldr, int r_f32) {
+    int64_t ldr, int r_f32, SegArgs seg) {
   const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
   const int64_t MN = (int64_t)M * N;
   if (idx >= MN) return;
@@ -636,7 +713,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
 #pragma unroll
     for (int e = 0; e < V; ++e) v[e] += r[e];
   }
-  store_f32<TC, V>(C + (int64_t)row * ldc + col, v);
+  store_f32<TC, V>(c_at(C, ldc, seg, row, col), v);
 }
 
 // The split tail's tiles: parts summed in order, the residual added, one rounding.
@@ -644,7 +721,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(
 template <typename TC>
 __global__ __launch_bounds__(256) void splitk_tail_reduce_kernel(
     const float* __restrict__ part, int parts, int head, int tail, int tiles_m, int tiles, int M,
-    int N, TC* C, int64_t ldc, const void* R, int64_t ldr, int r_f32, int vec_c) {
+    int N, TC* C, int64_t ldc, const void* R, int64_t ldr, int r_f32, int vec_c, SegArgs seg) {
   const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (e >= (int64_t)tail * kTileElems) return;
   const int tt = (int)(e / kTileElems), rc = (int)(e % kTileElems);
@@ -661,7 +738,7 @@ __global__ __launch_bounds__(256) void splitk_tail_reduce_kernel(
 #pragma unroll
     for (int q = 0; q < 4; ++q) v[q] += w[q];
   }
-  TC* crow = C + (int64_t)row * ldc;
+  TC* cp = c_at(C, ldc, seg, row, col);  // 4 columns of one tile: one segment
   if (vec_c && col + 3 < N) {
     if (R) {
       float rr[4];
@@ -670,7 +747,7 @@ __global__ __launch_bounds__(256) void splitk_tail_reduce_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] += rr[q];
     }
-    store_f32<TC, 4>(crow + col, v);
+    store_f32<TC, 4>(cp, v);
   } else {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -678,7 +755,7 @@ __global__ __launch_bounds__(256) void splitk_tail_reduce_kernel(
       float x = v[q];
       if (R) x += r_f32 ? ((const float*)R)[(int64_t)row * ldr + col + q]
                         : to_f32(((const TC*)R)[(int64_t)row * ldr + col + q]);
-      put<TC>(crow + col + q, x);
+      put<TC>(cp + q, x);
     }
   }
 }
@@ -741,10 +818,30 @@ size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 // C[M][N] = A B in fp32 accumulation; see the file comment for the layouts.
 // a_kc: A is [a_rows][lda] holding rows m (else rows k); b_kc: B is [b_rows][ldb]
 // holding rows n (else rows k). Rows at or past a_rows / b_rows read as zero.
+namespace {
+int gemm_impl(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+              int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
+              int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
+              const void* R, int64_t ldr, bool r_f32, void* ws, size_t ws_bytes,
+              const SegArgs& seg);
+}  // namespace
+
 int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
                 int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
                 const void* R, int64_t ldr, bool r_f32, void* ws, size_t ws_bytes) {
+  SegArgs none{};
+  none.dim = kSegNone;
+  return gemm_impl(A, B, C, M, N, K, lda, ldb, ldc, a_kc, b_kc, a_rows, b_rows, dtype, c_dtype, st,
+                   name, R, ldr, r_f32, ws, ws_bytes, none);
+}
+
+namespace {
+int gemm_impl(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+              int64_t lda, int64_t ldb, int64_t ldc, bool a_kc, bool b_kc, int64_t a_rows,
+              int64_t b_rows, int dtype, int c_dtype, hipStream_t st, const char* name,
+              const void* R, int64_t ldr, bool r_f32, void* ws, size_t ws_bytes,
+              const SegArgs& seg) {
   if (M <= 0 || N <= 0) return 0;
   if (K <= 0) {
     set_error("%s: K must be positive", name);
@@ -808,7 +905,17 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
               "elements and bases 16-byte aligned", name);
     return 1;
   }
-  if ((a_kc ? lda < K : lda < M) || (b_kc ? ldb < K : ldb < N) || ldc < N || (R && ldr < N)) {
+  // Row widths: a column-segmented operand's rows are one segment wide.
+  int64_t seg_max = 0;
+  for (int i = 0; seg.dim != kSegNone && i < seg.n; ++i)
+    seg_max = std::max<int64_t>(seg_max, seg.start[i + 1] - seg.start[i]);
+  const bool a_cols = (seg.dim == kSegK && a_kc) || (seg.dim == kSegM && !a_kc);
+  const bool b_cols = (seg.dim == kSegK && b_kc) || (seg.dim == kSegN && !b_kc);
+  const bool c_cols = seg.dim == kSegN && seg.c[0];
+  const int64_t a_w = a_cols && seg.a[0] ? seg_max : (a_kc ? K : M);
+  const int64_t b_w = b_cols && seg.b[0] ? seg_max : (b_kc ? K : N);
+  const int64_t c_w = c_cols ? seg_max : N;
+  if (lda < a_w || ldb < b_w || ldc < c_w || (R && ldr < N)) {
     set_error("%s: a leading dimension is smaller than its row", name);
     return 1;
   }
@@ -846,12 +953,13 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
               dim3(grid_x, (unsigned)splits), dim3(kThreads), 0, st, (const uint16_t*)A,
               (const uint16_t*)B, (TC*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows,
               (int)tiles_m, (int)tiles, vec_c, SmxArgs{}, R, ldr, (int)r_f32, kt_per, part,
-              (int)tp.head, (int)tp.tail);
+              (int)tp.head, (int)tp.tail, seg);
     if (int e = check_launch(name)) return e;
     if (tp.tail) {
       EG_LAUNCH((splitk_tail_reduce_kernel<TC>), dim3((unsigned)(tp.tail * (kTileElems / 1024))),
                 dim3(256), 0, st, (const float*)part, tp.parts, (int)tp.head, (int)tp.tail,
-                (int)tiles_m, (int)tiles, (int)M, (int)N, (TC*)C, ldc, R, ldr, (int)r_f32, vec_c);
+                (int)tiles_m, (int)tiles, (int)M, (int)N, (TC*)C, ldc, R, ldr, (int)r_f32, vec_c,
+                seg);
       return check_launch(name);
     }
     if (splits == 1) return 0;
@@ -860,10 +968,10 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     const unsigned rg = (unsigned)((n + 255) / 256);
     if (v4)
       EG_LAUNCH((splitk_reduce_kernel<TC, 4>), dim3(rg), dim3(256), 0, st, part, splits, (int)M,
-                (int)N, (TC*)C, ldc, R, ldr, (int)r_f32);
+                (int)N, (TC*)C, ldc, R, ldr, (int)r_f32, seg);
     else
       EG_LAUNCH((splitk_reduce_kernel<TC, 1>), dim3(rg), dim3(256), 0, st, part, splits, (int)M,
-                (int)N, (TC*)C, ldc, R, ldr, (int)r_f32);
+                (int)N, (TC*)C, ldc, R, ldr, (int)r_f32, seg);
     return check_launch(name);
   };
   auto layouts = [&](auto tag, auto ctag) {
@@ -878,6 +986,7 @@ int gemm_launch(const void* A, const void* B, void* C, int64_t M, int64_t N, int
     return c_dtype == EG_F32 ? layouts(bf16_t{}, float{}) : layouts(bf16_t{}, bf16_t{});
   return c_dtype == EG_F32 ? layouts(f16_t{}, float{}) : layouts(f16_t{}, f16_t{});
 }
+}  // namespace
 
 int64_t flce_groups(int64_t n) { return 2 * ((n + kBN - 1) / kBN); }
 
@@ -915,7 +1024,7 @@ int gemm_logits_softmax_launch(const void* x, const void* w, void* e, int64_t M,
     EG_LAUNCH((gemm_kernel<T, true, true, T, true>), dim3(grid), dim3(kThreads), 0, st,
               (const uint16_t*)x, (const uint16_t*)w, (T*)e, (int)M, (int)N, (int)K, ldx, ldw,
               lde, M, N, (int)tiles_m, (int)tiles, vec_c, smx, (const void*)nullptr, (int64_t)0,
-              0, 0, (float*)nullptr, (int)tiles, 0);
+              0, 0, (float*)nullptr, (int)tiles, 0, SegArgs{});
     return check_launch(name);
   };
   return dtype == EG_BF16 ? go(bf16_t{}) : go(f16_t{});
@@ -947,4 +1056,92 @@ extern "C" int eg_gemm(const void* a, const void* b, void* c, const void* r, int
   return gemm_launch(a, b, c, m, n, k, lda, ldb, ldc, akc, bkc, akc ? m : k, bkc ? n : k, dtype,
                      c_dtype, as_stream(stream), "eg_gemm", r, ldr, false, workspace,
                      workspace_bytes);
+}
+
+extern "C" int eg_gemm_segmented(const void* a, const void* b, void* c, int64_t m, int64_t n,
+                                 int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
+                                 int a_k_contiguous, int b_k_contiguous, int seg_dim, int nseg,
+                                 const int64_t* seg_sizes, const void* const* a_segs,
+                                 const void* const* b_segs, void* const* c_segs, int dtype,
+                                 int c_dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  clear_error();
+  const char* name = "eg_gemm_segmented";
+  if (m < 0 || n < 0 || k < 0) {
+    set_error("%s: negative size", name);
+    return 1;
+  }
+  if (seg_dim < kSegM || seg_dim > kSegK || nseg < 1 || nseg > kMaxSegs || !seg_sizes) {
+    set_error("%s: seg_dim must be 1 (M), 2 (N) or 3 (K), with 1 to %d segment sizes", name,
+              kMaxSegs);
+    return 1;
+  }
+  if (dtype != EG_BF16 && dtype != EG_F16) {
+    set_error("%s: operands must be bf16 or fp16", name);
+    return 1;
+  }
+  // the operands the segmented dimension indexes: M -> A, C; N -> B, C; K -> A, B
+  const bool a_ok = seg_dim != kSegN, b_ok = seg_dim != kSegM, c_ok = seg_dim != kSegK;
+  if ((a_segs && !a_ok) || (b_segs && !b_ok) || (c_segs && !c_ok) ||
+      (!a_segs && !b_segs && !c_segs)) {
+    set_error("%s: segment pointers given for an operand the dimension does not index, or "
+              "for none", name);
+    return 1;
+  }
+  const bool akc = a_k_contiguous != 0, bkc = b_k_contiguous != 0;
+  const int64_t extent = seg_dim == kSegM ? m : seg_dim == kSegN ? n : k;
+  const int64_t unit = seg_dim == kSegK ? kBK : kBM;
+  SegArgs g{};
+  g.dim = seg_dim;
+  g.n = nseg;
+  int64_t at = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (seg_sizes[i] <= 0 || (i + 1 < nseg && seg_sizes[i] % unit)) {
+      set_error("%s: segment sizes must be positive and, except the last, multiples of %lld",
+                name, (long long)unit);
+      return 1;
+    }
+    g.start[i] = (int)at;
+    at += seg_sizes[i];
+    if (at > 0x7fffffff) {
+      set_error("%s: size out of range", name);
+      return 1;
+    }
+  }
+  for (int i = nseg; i <= kMaxSegs; ++i) g.start[i] = (int)at;
+  if (at != extent) {
+    set_error("%s: segment sizes add up to %lld, the segmented dimension is %lld", name,
+              (long long)at, (long long)extent);
+    return 1;
+  }
+  if (seg_dim == kSegK && (akc || bkc) && k % kBK) {
+    set_error("%s: segments along K with a k-contiguous operand need K %% 64 == 0", name);
+    return 1;
+  }
+  for (int i = 0; i < nseg; ++i) {
+    g.a[i] = a_segs ? a_segs[i] : nullptr;
+    g.b[i] = b_segs ? b_segs[i] : nullptr;
+    g.c[i] = c_segs ? c_segs[i] : nullptr;
+    if ((a_segs && !g.a[i]) || (b_segs && !g.b[i]) || (c_segs && !g.c[i])) {
+      set_error("%s: null segment pointer", name);
+      return 1;
+    }
+    if ((g.a[i] && !aligned16(g.a[i])) || (g.b[i] && !aligned16(g.b[i])) ||
+        (g.c[i] && !aligned16(g.c[i]))) {
+      set_error("%s: segment pointers must be 16-byte aligned", name);
+      return 1;
+    }
+  }
+  // a segmented operand's plain pointer stands for its first segment
+  const void* pa = a_segs ? a_segs[0] : a;
+  const void* pb = b_segs ? b_segs[0] : b;
+  void* pc = c_segs ? c_segs[0] : c;
+  if (m > 0 && n > 0 && (!pa || !pb || !pc)) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  if (m == 0 || n == 0) return 0;
+  return gemm_impl(pa, pb, pc, m, n, k, lda, ldb, ldc, akc, bkc, akc ? m : k, bkc ? n : k, dtype,
+                   c_dtype, as_stream(stream), name, nullptr, 0, false, workspace,
+                   workspace_bytes, g);
 }

@@ -47,6 +47,7 @@ if not __package__:
     if _ROOT not in _sys.path:
         _sys.path.insert(0, _ROOT)
 
+import ctypes
 import math
 
 import torch
@@ -81,6 +82,11 @@ class _Shape:
         # row strides: k-contiguous 16-bit operands of a product need k % 64 == 0
         self.Ip = _pad64(self.inter) if wide else self.inter
         self.kvp = _pad64(self.kv_out) if wide else self.kv_out
+        # 16-bit widths in whole 256-wide tiles: the projections that share an input
+        # (q, k, v; gate, up) run as one product over their concatenated weights
+        self.qkv = self.q_out + 2 * self.kv_out
+        self.fuse_qkv = wide and self.q_out % 256 == 0 and self.kv_out % 256 == 0
+        self.fuse_mlp = wide and self.inter % 256 == 0
         if wide and self.hidden % 64:
             raise ValueError(f"llama3_decoder_layer: 16-bit inputs need hidden % 64 == 0, got "
                              f"{self.hidden}")
@@ -143,6 +149,19 @@ class _Ops:
                   ldb, ldc, ldr, int(akc), int(bkc), self.tg, self.tg, _lib.ptr(ws), nbytes,
                   self.st)
 
+    def gemm_seg(self, a, b, c, m, n, k, lda, ldb, ldc, akc, bkc, dim, sizes, a_segs=None,
+                 b_segs=None, c_segs=None):
+        """eg_gemm_segmented: operands concatenated from separate buffers along dim
+        (1 = M, 2 = N, 3 = K), segment extents `sizes`."""
+        nbytes = _lib.query("eg_gemm_workspace_bytes", m, n, k, self.tg)
+        ws = workspace(nbytes, self.dev) if nbytes else None
+        n_seg = len(sizes)
+        arr = lambda ts: (ctypes.c_void_p * n_seg)(*[t.data_ptr() for t in ts]) if ts else None
+        _lib.call("eg_gemm_segmented", _lib.ptr(a), _lib.ptr(b), _lib.ptr(c), m, n, k, lda, ldb,
+                  ldc, int(akc), int(bkc), dim, n_seg, (ctypes.c_int64 * n_seg)(*sizes),
+                  arr(a_segs), arr(b_segs), arr(c_segs), self.tg, self.tg, _lib.ptr(ws), nbytes,
+                  self.st)
+
     def linear(self, h, w, out, m, n, k, ldh, ldo, r=None):
         """out[m, :n] = r + h[m, :k] w^T, w [n, k] (F.linear)."""
         self.gemm(h, w, out, m, n, k, ldh, w.shape[1], ldo, True, True, r, ldo if r is not None
@@ -184,24 +203,41 @@ class _Ops:
 
 
 def _qkv_heads(ops, s, h1, wq, wk, wv, cos, sin):
-    """q, k, v projections of h1, rotated (q, k) and split into [B, heads, T, D]."""
-    q = ops.empty(s.M, s.q_out)
-    k = ops.empty(s.M, s.kv_out)
-    v = ops.empty(s.M, s.kv_out)
-    ops.linear(h1, wq, q, s.M, s.q_out, s.hidden, s.hidden, s.q_out)
-    ops.linear(h1, wk, k, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
-    ops.linear(h1, wv, v, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
+    """q, k, v projections of h1, rotated (q, k) and split into [B, heads, T, D]. With
+    the widths whole tiles, one product [q | k | v] = h1 [Wq; Wk; Wv]^T (the weights
+    as segments along N) into one [M, q_out + 2 kv_out] buffer."""
     qh = ops.empty(s.B, s.H, s.T, s.D)
     kh = ops.empty(s.B, s.KVH, s.T, s.D)
     vh = ops.empty(s.B, s.KVH, s.T, s.D)
-    ops.split(q, qh, s, s.H, s.q_out, 1, cos, sin)
-    ops.split(k, kh, s, s.KVH, s.kv_out, 1, cos, sin)
-    ops.split(v, vh, s, s.KVH, s.kv_out, 0)
+    if s.fuse_qkv:
+        qkv = ops.empty(s.M, s.qkv)
+        ops.gemm_seg(h1, None, qkv, s.M, s.qkv, s.hidden, s.hidden, s.hidden, s.qkv, True, True,
+                     2, [s.q_out, s.kv_out, s.kv_out], b_segs=[wq, wk, wv])
+        q, k, v = qkv, qkv[:, s.q_out:], qkv[:, s.q_out + s.kv_out:]
+        ldq = ldk = s.qkv
+    else:
+        q = ops.empty(s.M, s.q_out)
+        k = ops.empty(s.M, s.kv_out)
+        v = ops.empty(s.M, s.kv_out)
+        ops.linear(h1, wq, q, s.M, s.q_out, s.hidden, s.hidden, s.q_out)
+        ops.linear(h1, wk, k, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
+        ops.linear(h1, wv, v, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
+        ldq, ldk = s.q_out, s.kv_out
+    ops.split(q, qh, s, s.H, ldq, 1, cos, sin)
+    ops.split(k, kh, s, s.KVH, ldk, 1, cos, sin)
+    ops.split(v, vh, s, s.KVH, ldk, 0)
     return qh, kh, vh
 
 
 def _mlp_in(ops, s, h2, wg, wu):
-    """gate, up = h2 Wg^T, h2 Wu^T as [M, Ip] rows (padding columns zero)."""
+    """gate, up = h2 Wg^T, h2 Wu^T as [M, Ip] rows (padding columns zero). With whole
+    tiles, one product with [Wg; Wu] as segments along N and the two outputs as the
+    segments of C: gate and up are the two halves of one [2, M, Ip] buffer."""
+    if s.fuse_mlp:
+        gu = ops.empty(2, s.M, s.Ip)
+        ops.gemm_seg(h2, None, None, s.M, 2 * s.inter, s.hidden, s.hidden, s.hidden, s.Ip, True,
+                     True, 2, [s.inter, s.inter], b_segs=[wg, wu], c_segs=[gu[0], gu[1]])
+        return gu[0], gu[1]
     gate = ops.padded(s.M, s.inter, s.Ip)
     up = ops.padded(s.M, s.inter, s.Ip)
     ops.linear(h2, wg, gate, s.M, s.inter, s.hidden, s.hidden, s.Ip)
@@ -294,12 +330,22 @@ def llama3_decoder_layer_backward_from_saved(dout, saved, eps: float = 1e-5):
     dgate, dup = gate, up
     del d_act
     dh2 = ops.empty(M, hidden)
-    ops.linear_dinput(dgate, wg, dh2, M, s.inter, hidden, s.Ip, hidden)
-    ops.linear_dinput(dup, wu, dh2, M, s.inter, hidden, s.Ip, hidden, r=dh2)
-    d_wg = ops.empty(s.inter, hidden)
-    d_wu = ops.empty(s.inter, hidden)
-    ops.linear_dweight(dgate, h2, d_wg, M, s.inter, hidden, s.Ip, hidden)
-    ops.linear_dweight(dup, h2, d_wu, M, s.inter, hidden, s.Ip, hidden)
+    if s.fuse_mlp:
+        # dh2 = [dgate | dup] [Wg; Wu] (segments along K); [dWg; dWu] = [dgate | dup]^T h2
+        # (A's columns in two segments along M) into one buffer, returned as two views
+        ops.gemm_seg(None, None, dh2, M, hidden, 2 * s.inter, s.Ip, hidden, hidden, True, False,
+                     3, [s.inter, s.inter], a_segs=[dgate, dup], b_segs=[wg, wu])
+        d_wgu = ops.empty(2 * s.inter, hidden)
+        ops.gemm_seg(None, h2, d_wgu, 2 * s.inter, hidden, M, s.Ip, hidden, hidden, False, False,
+                     1, [s.inter, s.inter], a_segs=[dgate, dup])
+        d_wg, d_wu = d_wgu[:s.inter], d_wgu[s.inter:]
+    else:
+        ops.linear_dinput(dgate, wg, dh2, M, s.inter, hidden, s.Ip, hidden)
+        ops.linear_dinput(dup, wu, dh2, M, s.inter, hidden, s.Ip, hidden, r=dh2)
+        d_wg = ops.empty(s.inter, hidden)
+        d_wu = ops.empty(s.inter, hidden)
+        ops.linear_dweight(dgate, h2, d_wg, M, s.inter, hidden, s.Ip, hidden)
+        ops.linear_dweight(dup, h2, d_wu, M, s.inter, hidden, s.Ip, hidden)
     del dgate, dup, gate, up, h2
     # h2 = rmsnorm(x1); dx1 = dout (residual) + the norm's input gradient
     dx1 = ops.empty(M, hidden)
@@ -329,24 +375,42 @@ def llama3_decoder_layer_backward_from_saved(dout, saved, eps: float = 1e-5):
               _lib.ptr(ws), s.B, s.H, s.KVH, s.T, s.D, 1.0 / math.sqrt(s.D), ops.tg, ops.st)
     del qh, kh, vh, oh, doh, ws
     # back to token rows; the rotation's transpose takes dq, dk to the pre-rotation q, k
-    dq = ops.empty(M, s.q_out)
-    dk = ops.padded(M, s.kv_out, s.kvp)
-    dv = ops.padded(M, s.kv_out, s.kvp)
-    ops.merge(dqh, dq, s, s.H, s.q_out, 2, cos, sin)
-    ops.merge(dkh, dk, s, s.KVH, s.kvp, 2, cos, sin)
-    ops.merge(dvh, dv, s, s.KVH, s.kvp, 0)
-    del dqh, dkh, dvh
     dh1 = ops.empty(M, hidden)
-    ops.linear_dinput(dq, wq, dh1, M, s.q_out, hidden, s.q_out, hidden)
-    ops.linear_dinput(dk, wk, dh1, M, s.kv_out, hidden, s.kvp, hidden, r=dh1)
-    ops.linear_dinput(dv, wv, dh1, M, s.kv_out, hidden, s.kvp, hidden, r=dh1)
-    d_wq = ops.empty(s.q_out, hidden)
-    d_wk = ops.empty(s.kv_out, hidden)
-    d_wv = ops.empty(s.kv_out, hidden)
-    ops.linear_dweight(dq, h1, d_wq, M, s.q_out, hidden, s.q_out, hidden)
-    ops.linear_dweight(dk, h1, d_wk, M, s.kv_out, hidden, s.kvp, hidden)
-    ops.linear_dweight(dv, h1, d_wv, M, s.kv_out, hidden, s.kvp, hidden)
-    del dq, dk, dv, h1
+    if s.fuse_qkv:
+        # [dq | dk | dv] in one [M, q_out + 2 kv_out] buffer; dh1 = [dq | dk | dv] [Wq; Wk;
+        # Wv] (the weights as segments along K); [dWq; dWk; dWv] = [dq | dk | dv]^T h1 in
+        # one buffer, returned as three views
+        dqkv = ops.empty(M, s.qkv)
+        ops.merge(dqh, dqkv, s, s.H, s.qkv, 2, cos, sin)
+        ops.merge(dkh, dqkv[:, s.q_out:], s, s.KVH, s.qkv, 2, cos, sin)
+        ops.merge(dvh, dqkv[:, s.q_out + s.kv_out:], s, s.KVH, s.qkv, 0)
+        del dqh, dkh, dvh
+        ops.gemm_seg(dqkv, None, dh1, M, hidden, s.qkv, s.qkv, hidden, hidden, True, False, 3,
+                     [s.q_out, s.kv_out, s.kv_out], b_segs=[wq, wk, wv])
+        d_wqkv = ops.empty(s.qkv, hidden)
+        ops.linear_dweight(dqkv, h1, d_wqkv, M, s.qkv, hidden, s.qkv, hidden)
+        d_wq = d_wqkv[:s.q_out]
+        d_wk = d_wqkv[s.q_out:s.q_out + s.kv_out]
+        d_wv = d_wqkv[s.q_out + s.kv_out:]
+        del dqkv, h1
+    else:
+        dq = ops.empty(M, s.q_out)
+        dk = ops.padded(M, s.kv_out, s.kvp)
+        dv = ops.padded(M, s.kv_out, s.kvp)
+        ops.merge(dqh, dq, s, s.H, s.q_out, 2, cos, sin)
+        ops.merge(dkh, dk, s, s.KVH, s.kvp, 2, cos, sin)
+        ops.merge(dvh, dv, s, s.KVH, s.kvp, 0)
+        del dqh, dkh, dvh
+        ops.linear_dinput(dq, wq, dh1, M, s.q_out, hidden, s.q_out, hidden)
+        ops.linear_dinput(dk, wk, dh1, M, s.kv_out, hidden, s.kvp, hidden, r=dh1)
+        ops.linear_dinput(dv, wv, dh1, M, s.kv_out, hidden, s.kvp, hidden, r=dh1)
+        d_wq = ops.empty(s.q_out, hidden)
+        d_wk = ops.empty(s.kv_out, hidden)
+        d_wv = ops.empty(s.kv_out, hidden)
+        ops.linear_dweight(dq, h1, d_wq, M, s.q_out, hidden, s.q_out, hidden)
+        ops.linear_dweight(dk, h1, d_wk, M, s.kv_out, hidden, s.kvp, hidden)
+        ops.linear_dweight(dv, h1, d_wv, M, s.kv_out, hidden, s.kvp, hidden)
+        del dq, dk, dv, h1
     # h1 = rmsnorm(x); dx = dx1 (residual) + the norm's input gradient
     dx = ops.empty(M, hidden)
     d_win = torch.empty_like(w_in)

@@ -373,12 +373,31 @@ int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int6
  * workgroups when `workspace` holds at least eg_gemm_workspace_bytes(m, n, k, dtype)
  * bytes (else, or with workspace NULL, they run unsplit): each k range writes an
  * fp32 partial, and a second pass sums them in a fixed order, adds r and rounds c
- * once. The split depends on the shape only, so results are bitwise repeatable. */
+ * once. So do the tiles of a last wave that is at most half full (more than 256
+ * tiles). The split depends on the shape only, so results are bitwise repeatable. */
 size_t eg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int dtype);
 int eg_gemm(const void* a, const void* b, void* c, const void* r, int64_t m, int64_t n,
             int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int64_t ldr, int a_k_contiguous,
             int b_k_contiguous, int dtype, int c_dtype, void* workspace, size_t workspace_bytes,
             void* stream);
+
+/* eg_gemm over operands that are concatenations of up to 4 buffers along one
+ * dimension (no counterpart call in the reference; it runs several of the decoder
+ * layer's F.linear calls of forward_ref.py:89-91 and :115-116, and their gradients,
+ * as one product): seg_dim 1 (M), 2 (N) or 3 (K); seg_sizes[i] is segment i's extent
+ * along it (all but the last a multiple of 256 for M and N, of 64 for K; they add up
+ * to m, n or k). a_segs, b_segs, c_segs (arrays of nseg pointers, or NULL for an
+ * operand that is the single buffer a, b or c) point at the first element of each
+ * segment of the operands the dimension indexes: along M, rows of A (columns of a
+ * k-major A) and rows of C; along N, B's rows (columns of a k-major B) and C's
+ * columns; along K, A and B. Segments of one operand share its row stride. No
+ * residual; workspace as for eg_gemm (eg_gemm_workspace_bytes of the whole shape). */
+int eg_gemm_segmented(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                      int64_t lda, int64_t ldb, int64_t ldc, int a_k_contiguous,
+                      int b_k_contiguous, int seg_dim, int nseg, const int64_t* seg_sizes,
+                      const void* const* a_segs, const void* const* b_segs, void* const* c_segs,
+                      int dtype, int c_dtype, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /* ---------------------------------------------- decoder layer: layout, adds
  * The steps of the Llama-3 decoder layer

@@ -1,6 +1,7 @@
 """The C-ABI library builds, loads and exports exactly what include/evograd_hip.h
 declares; the Python binding declares the same set. No kernel is launched."""
 
+import ctypes
 import os
 import re
 
@@ -151,6 +152,25 @@ def test_host_side_validation_errors_without_gpu():
     _lib.call("eg_softmax_fwd", None, None, 0, 0, _lib.EG_F32, None)
     _lib.call("eg_cross_entropy_bwd", None, None, None, None, None, None, 0, 8, -100,
               _lib.EG_F32, None)
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_gemm_segmented_refuses_bad_segments_on_the_host():
+    """Segment checks run on the host before any launch (no device needed)."""
+    p = 1 << 20  # never dereferenced: the checks run before any launch
+    segs = (ctypes.c_void_p * 2)(p, p)
+    def call(dim, sizes, m, n, k, a_segs=None, b_segs=segs, c_segs=None):
+        return _lib.call("eg_gemm_segmented", p, p, p, m, n, k, 1024, 1024, 1024, 1, 1, dim,
+                         len(sizes), (ctypes.c_int64 * len(sizes))(*sizes), a_segs, b_segs,
+                         c_segs, _lib.EG_BF16, _lib.EG_BF16, None, 0, None)
+    with pytest.raises(RuntimeError, match="multiples of 256"):
+        call(2, [200, 56], 256, 256, 64)
+    with pytest.raises(RuntimeError, match="add up"):
+        call(2, [256, 256], 256, 600, 64)
+    with pytest.raises(RuntimeError, match="does not index"):
+        call(1, [256, 256], 512, 256, 64)          # B segments along M
+    with pytest.raises(RuntimeError, match="seg_dim"):
+        call(4, [256, 256], 256, 512, 64)
 
 
 def test_pairs_refuse_cpu_tensors():

@@ -51,6 +51,21 @@ def test_layer_llama3_8b_widths(w):
     torch.cuda.empty_cache()
 
 
+def test_layer_fused_projections_at_whole_tile_widths():
+    """Widths in whole 256-wide tiles (16-bit): q/k/v and gate/up run as single
+    products over segmented weights (eg_gemm_segmented), and their gradients too;
+    held to the same gate as every other workload (the small workloads above take
+    the separate products)."""
+    from evograd_amd.opdecl import Workload
+
+    w = Workload(dims=dict(B=1, T=256, hidden=512, head_dim=64, q_out=512, kv_out=256,
+                           intermediate=768), dtype="bfloat16")
+    _note("fused", w.dims)
+    rep = verify(OP, pair_module(OP.name), device="cuda", workloads=(w,))
+    torch.cuda.synchronize()
+    assert rep.ok, "\n".join(rep.failures())
+
+
 def _run(inp, mod):
     args = [inp.get(a.name, getattr(a, "default", None)) for a in OP.args]
     out, saved = mod.llama3_decoder_layer_forward_with_saved(*args)

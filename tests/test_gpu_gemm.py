@@ -4,6 +4,7 @@ N and k-major K, padded strides, fp32 / bf16 / fp16 outputs, and the fp32 path.
 Bound: the fp32 result within fp32 accumulation rounding of the exact product of
 the (exactly representable) 16-bit inputs; a 16-bit result within one rounding."""
 
+import ctypes
 import sys
 
 import pytest
@@ -202,3 +203,91 @@ def test_gemm_split_k_matches_unsplit_and_is_repeatable(cdt, M, N, K, akc, bkc):
               need - 1, st)
     torch.cuda.synchronize()
     assert torch.equal(c, outs[2])
+
+
+# ------------------------------------------------------------- segmented operands
+def _pieces(stored, along_rows, sizes, ld):
+    """Split a stored [rows][cols] matrix into separate buffers of row stride ld,
+    along its rows or its columns."""
+    out, at = [], 0
+    for n in sizes:
+        part = stored[at:at + n] if along_rows else stored[:, at:at + n]
+        buf = torch.zeros(part.shape[0], ld, device="cuda", dtype=stored.dtype)
+        buf[:, :part.shape[1]] = part
+        out.append(buf)
+        at += n
+    return out
+
+
+SEG_CASES = [
+    # dim, sizes, (M, N, K) with the segmented extent from sizes
+    (1, [256, 512, 100], (None, 300, 384)),
+    (2, [256, 256, 300], (300, None, 384)),
+    (2, [256, 256, 300], (300, None, 2048)),          # split k, C in segments
+    (2, [2048, 2048], (4352, None, 512)),             # split tail (272 tiles), C in segments
+    (3, [128, 64, 192], (300, 400, None)),
+    (3, [4096, 1024, 1024], (256, 512, None)),        # the decoder layer's q/k/v gradient
+]
+
+
+def _seg_cases():
+    for dim, sizes, mnk in SEG_CASES:
+        for akc, bkc in LAYOUTS:
+            yield pytest.param(dim, sizes, mnk, akc, bkc,
+                               id=f"d{dim}-{'-'.join(map(str, sizes))}-{mnk}-a{int(akc)}b{int(bkc)}")
+
+
+@pytest.mark.parametrize("dim,sizes,mnk,akc,bkc", list(_seg_cases()))
+def test_gemm_segmented_is_the_concatenated_product_bitwise(dim, sizes, mnk, akc, bkc):
+    """eg_gemm_segmented on operands cut into separate buffers along M, N or K gives
+    the bits eg_gemm gives on the concatenated operands (same tiles, same k order,
+    same split plan), for every layout; C in segments along M or N."""
+    M, N, K = (sum(sizes) if v is None else v for v in mnk)
+    print(f"\n[gpu-gemm] segmented dim={dim} sizes={sizes} {M}x{N}x{K} a{int(akc)} b{int(bkc)}",
+          flush=True)
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, torch.bfloat16, M * 3 + N + K + dim)
+    st = torch.cuda.current_stream().cuda_stream
+    need = _lib.query("eg_gemm_workspace_bytes", M, N, K, _lib.EG_BF16)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    ldc = _r8(N)
+    want = torch.full((M, ldc), float("nan"), device="cuda", dtype=torch.bfloat16)
+    _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), want.data_ptr(), None, M, N, K, lda, ldb,
+              ldc, 0, int(akc), int(bkc), _lib.EG_BF16, _lib.EG_BF16, ws.data_ptr(), need, st)
+    # the operands the dimension indexes, cut into segments sharing one row stride
+    a_segs = b_segs = c_segs = None
+    seg_ld = _r8(max(sizes))
+    if dim in (1, 3):  # A: rows m (k-contiguous) / columns m (k-major), or k
+        a_rows = (dim == 1) == akc
+        a_segs = _pieces(a[:, :(K if akc else M)], a_rows, sizes, lda if a_rows else seg_ld)
+        seg_lda = lda if a_rows else seg_ld
+    else:
+        seg_lda = lda
+    if dim in (2, 3):  # B: rows n (k-contiguous) / columns n, or k
+        b_rows = (dim == 2) == bkc
+        b_segs = _pieces(b[:, :(K if bkc else N)], b_rows, sizes, ldb if b_rows else seg_ld)
+        seg_ldb = ldb if b_rows else seg_ld
+    else:
+        seg_ldb = ldb
+    seg_ldc = ldc
+    if dim in (1, 2):
+        seg_ldc = ldc if dim == 1 else seg_ld
+        c_segs = [torch.full((n if dim == 1 else M, seg_ldc), float("nan"), device="cuda",
+                             dtype=torch.bfloat16) for n in sizes]
+    arr = lambda ts: (ctypes.c_void_p * len(sizes))(*[t.data_ptr() for t in ts]) if ts else None
+    c = None if c_segs else torch.full((M, ldc), float("nan"), device="cuda",
+                                       dtype=torch.bfloat16)
+    _lib.call("eg_gemm_segmented", None if a_segs else a.data_ptr(),
+              None if b_segs else b.data_ptr(), None if c_segs else c.data_ptr(), M, N, K,
+              seg_lda, seg_ldb, seg_ldc, int(akc), int(bkc), dim, len(sizes),
+              (ctypes.c_int64 * len(sizes))(*sizes), arr(a_segs), arr(b_segs), arr(c_segs),
+              _lib.EG_BF16, _lib.EG_BF16, ws.data_ptr(), need, st)
+    if c_segs:
+        got = torch.cat([t[:, :(N if dim == 1 else n)] for t, n in zip(c_segs, sizes)],
+                        dim=0 if dim == 1 else 1)
+    else:
+        got = c[:, :N]
+    torch.cuda.synchronize()
+    assert torch.equal(got, want[:, :N])
+    ref = A.double() @ B.double()
+    assert ((got.double() - ref).abs() <= 2.0 ** -8 * ref.abs() + 4e-6 * K).all()
+
