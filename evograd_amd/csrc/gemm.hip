@@ -371,15 +371,46 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   // workgroup; along K each slice picks its segment.
   const OpView va_t = seg_view<AKC>(A, a_rows, lda, seg, seg.a, false, m0);
   const OpView vb_t = seg_view<BKC>(B, b_rows, ldb, seg, seg.b, false, n0);
+  // Along K, the segment bases and starts are read once, here, so that each slice
+  // selects among values already in registers (an indexed read of the argument
+  // table inside the loop is a scalar memory load, and waiting for it also waits
+  // for the LDS reads in flight).
+  const bool kseg = seg.dim == kSegK;
+  const int ks1 = kseg && seg.n > 1 ? seg.start[1] : 0x7fffffff;
+  const int ks2 = kseg && seg.n > 2 ? seg.start[2] : 0x7fffffff;
+  const int ks3 = kseg && seg.n > 3 ? seg.start[3] : 0x7fffffff;
+  const uint16_t* ka[kMaxSegs];
+  const uint16_t* kbp[kMaxSegs];
+#pragma unroll
+  for (int i = 0; i < kMaxSegs; ++i) {
+    ka[i] = kseg && seg.a[i] ? (const uint16_t*)seg.a[i] : A;
+    kbp[i] = kseg && seg.b[i] ? (const uint16_t*)seg.b[i] : B;
+  }
+  const bool ka_seg = kseg && seg.a[0], kb_seg = kseg && seg.b[0];
+  // element view of a k slice of a K-segmented operand: rows k (k-major) or columns
+  auto kview = [&](auto kcc, const uint16_t* const* tab, bool segd, int64_t rows, int64_t ld,
+                   int k0, OpView plain) {
+    constexpr bool KC = decltype(kcc)::value;
+    if (!segd) return plain;
+    const int si = (k0 >= ks1) + (k0 >= ks2) + (k0 >= ks3);
+    const uint16_t* b = si == 0 ? tab[0] : si == 1 ? tab[1] : si == 2 ? tab[2] : tab[3];
+    const int st = si == 0 ? 0 : si == 1 ? ks1 : si == 2 ? ks2 : ks3;
+    const int en = si == 0 ? min(ks1, K) : si == 1 ? min(ks2, K) : si == 2 ? min(ks3, K) : K;
+    OpView v;
+    v.base = b;
+    v.shift = KC ? st : (int64_t)st * ld;
+    v.end = KC ? rows * ld : (int64_t)(en - st) * ld;
+    return v;
+  };
   auto loadA = [&](int kt, uint16_t* as) {
     const int k0 = kt * kBK;
-    const OpView va = seg.dim == kSegK ? seg_view<AKC>(A, a_rows, lda, seg, seg.a, true, k0) : va_t;
+    const OpView va = kview(std::integral_constant<bool, AKC>{}, ka, ka_seg, a_rows, lda, k0, va_t);
     const int64_t oa = (AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0) - va.shift;
     la.load(va.base + oa, kt < nk ? (va.end - oa) * 2 : 0, as);
   };
   auto loadB = [&](int kt, uint16_t* bs) {
     const int k0 = kt * kBK;
-    const OpView vb = seg.dim == kSegK ? seg_view<BKC>(B, b_rows, ldb, seg, seg.b, true, k0) : vb_t;
+    const OpView vb = kview(std::integral_constant<bool, BKC>{}, kbp, kb_seg, b_rows, ldb, k0, vb_t);
     const int64_t ob = (BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0) - vb.shift;
     lb.load(vb.base + ob, kt < nk ? (vb.end - ob) * 2 : 0, bs);
   };
