@@ -289,7 +289,7 @@ __device__ __forceinline__ float acc_read(float x) {
 // substep 1 suits the product with both operands K-major, substep 0 the others.
 template <bool AKC, bool BKC> struct LoadSpread { static constexpr int b_substep = !AKC && !BKC ? 1 : 0; };
 
-template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false>
+template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false, bool SEG = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -367,6 +367,18 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  // Plain operands: the slice's buffer range runs to the end of the matrix.
+  const int64_t a_end = a_rows * lda, b_end = b_rows * ldb;
+  auto loadA_plain = [&](int kt, uint16_t* as) {
+    const int k0 = kt * kBK;
+    const int64_t oa = AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0;
+    la.load(A + oa, kt < nk ? (a_end - oa) * 2 : 0, as);
+  };
+  auto loadB_plain = [&](int kt, uint16_t* bs) {
+    const int k0 = kt * kBK;
+    const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
+    lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
+  };
   // Segmented operands (seg.dim): along M or N the tile's segment is fixed for the
   // workgroup; along K each slice picks its segment.
   const OpView va_t = seg_view<AKC>(A, a_rows, lda, seg, seg.a, false, m0);
@@ -402,17 +414,27 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     v.end = KC ? rows * ld : (int64_t)(en - st) * ld;
     return v;
   };
-  auto loadA = [&](int kt, uint16_t* as) {
+  auto loadA_seg = [&](int kt, uint16_t* as) {
     const int k0 = kt * kBK;
     const OpView va = kview(std::integral_constant<bool, AKC>{}, ka, ka_seg, a_rows, lda, k0, va_t);
     const int64_t oa = (AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0) - va.shift;
     la.load(va.base + oa, kt < nk ? (va.end - oa) * 2 : 0, as);
   };
-  auto loadB = [&](int kt, uint16_t* bs) {
+  auto loadB_seg = [&](int kt, uint16_t* bs) {
     const int k0 = kt * kBK;
     const OpView vb = kview(std::integral_constant<bool, BKC>{}, kbp, kb_seg, b_rows, ldb, k0, vb_t);
     const int64_t ob = (BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0) - vb.shift;
     lb.load(vb.base + ob, kt < nk ? (vb.end - ob) * 2 : 0, bs);
+  };
+  // The segmented form is a separate instantiation (SEG): its per-slice selection
+  // costs the plain products 7-19% when compiled into the same kernel.
+  auto loadA = [&](int kt, uint16_t* as) {
+    if constexpr (SEG) loadA_seg(kt, as);
+    else loadA_plain(kt, as);
+  };
+  auto loadB = [&](int kt, uint16_t* bs) {
+    if constexpr (SEG) loadB_seg(kt, bs);
+    else loadB_plain(kt, bs);
   };
   loadA(kb, As0);
   loadB(kb, Bs0);
@@ -608,7 +630,7 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   // C of the tile's segment (along M: rows; along N: columns)
   TC* cb = C;
   int64_t cshift = 0;
-  if (seg.dim == kSegM || seg.dim == kSegN) {
+  if (SEG && (seg.dim == kSegM || seg.dim == kSegN)) {
     const int sg = seg_of(seg, seg.dim == kSegM ? m0 : n0);
     if (seg.c[sg]) {
       cb = (TC*)seg.c[sg];
@@ -979,12 +1001,25 @@ int gemm_impl(const void* A, const void* B, void* C, int64_t M, int64_t N, int64
   auto go = [&](auto tag, auto ctag, auto akc, auto bkc) {
     using T = decltype(tag);
     using TC = decltype(ctag);
+    constexpr bool AK = decltype(akc)::value, BK = decltype(bkc)::value;
     float* part = (splits > 1 || tp.tail) ? (float*)ws : nullptr;
-    EG_LAUNCH((gemm_kernel<T, decltype(akc)::value, decltype(bkc)::value, TC>),
-              dim3(grid_x, (unsigned)splits), dim3(kThreads), 0, st, (const uint16_t*)A,
-              (const uint16_t*)B, (TC*)C, (int)M, (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows,
-              (int)tiles_m, (int)tiles, vec_c, SmxArgs{}, R, ldr, (int)r_f32, kt_per, part,
-              (int)tp.head, (int)tp.tail, seg);
+    if (seg.dim != kSegNone) {
+      // segmented products: 16-bit C only (one more instantiation per layout)
+      if constexpr (std::is_same<T, TC>::value) {
+        EG_LAUNCH((gemm_kernel<T, AK, BK, TC, false, true>), dim3(grid_x, (unsigned)splits),
+                  dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
+                  (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c,
+                  SmxArgs{}, R, ldr, (int)r_f32, kt_per, part, (int)tp.head, (int)tp.tail, seg);
+      } else {
+        set_error("%s: segmented products write C in the operands' dtype", name);
+        return 1;
+      }
+    } else {
+      EG_LAUNCH((gemm_kernel<T, AK, BK, TC>), dim3(grid_x, (unsigned)splits), dim3(kThreads), 0,
+                st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M, (int)N, (int)K, lda,
+                ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c, SmxArgs{}, R, ldr,
+                (int)r_f32, kt_per, part, (int)tp.head, (int)tp.tail, seg);
+    }
     if (int e = check_launch(name)) return e;
     if (tp.tail) {
       EG_LAUNCH((splitk_tail_reduce_kernel<TC>), dim3((unsigned)(tp.tail * (kTileElems / 1024))),
