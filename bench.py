@@ -29,8 +29,13 @@ T in {1024, 2048, 4096} at Llama-3-8B widths, with its MFMA fraction over the
 layer's model FLOPs. ``sweeps`` holds the memory-bound operators over the
 reference's token sweeps (src/evograd/opdecl/models.py:286, :293).
 
+Each operator with an eager spelling also reports ``gpu_eager_full_us``: the reference's
+eager forward (torch operators) plus torch autograd on the same GPU and inputs, and
+``speedup_vs_gpu_eager``. ``sustained`` holds the device's sustained MFMA and copy rates
+measured in the same run.
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--ops a,b] [--no-cpu]
-                       [--no-sweep]
+                       [--no-sweep] [--no-eager]
 """
 
 from __future__ import annotations
@@ -558,6 +563,114 @@ def cpu_model() -> str:
     return "unknown"
 
 
+# ------------------------------------------------------ eager torch on this GPU
+# The reference's eager spellings of each forward (its runtime forwards where it
+# declares one), written here with torch's own operators, run through torch
+# autograd on the same GPU and inputs: what a user of the reference gets without
+# these kernels. Attention goes through F.scaled_dot_product_attention limited to
+# its flash and memory-efficient backends (never the math backend's batched
+# products); the decoder layer and the RoPE -> attention pair are not timed.
+EAGER_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "fused_add_rms_norm",
+             "causal_attention", "causal_attention_gqa", "cross_entropy",
+             "fused_linear_cross_entropy", "softmax@vocab")
+
+
+def _eager_forward(name: str):
+    import torch
+    import torch.nn.functional as F
+
+    def rotate_half(x):
+        h = x.shape[-1] // 2
+        return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+    def sdpa(q, k, v):
+        return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+
+    def gqa(q, k, v):
+        r = q.shape[1] // k.shape[1]
+        if r > 1:
+            k, v = k.repeat_interleave(r, dim=1), v.repeat_interleave(r, dim=1)
+        return sdpa(q, k, v)
+
+    return {
+        # softmax/forward_ref.py:6-7
+        "softmax": lambda x: torch.softmax(x.float(), dim=-1).to(x.dtype),
+        # rmsnorm/forward_ref.py:24-34, layernorm/forward_ref.py:26-42 (runtime forwards)
+        "rmsnorm": lambda x, w, eps: F.rms_norm(x, (x.shape[-1],), weight=w, eps=eps),
+        "layernorm": lambda x, w, b, eps: F.layer_norm(x, (x.shape[-1],), weight=w, bias=b,
+                                                       eps=eps),
+        # swiglu/forward_ref.py:6-9
+        "swiglu": lambda a, b: F.silu(a.float()).to(a.dtype) * b,
+        # rope/forward_ref.py:28-47
+        "rope": lambda x, c, s: (x.float() * c[None, None].float()
+                                 + rotate_half(x.float()) * s[None, None].float()).to(x.dtype),
+        # fused_add_rms_norm/forward_ref.py:19-34
+        "fused_add_rms_norm": lambda x, r, w, eps: F.rms_norm(x + r, (x.shape[-1],), weight=w,
+                                                              eps=eps),
+        # llama3_decoder_layer/forward_ref.py:101-107
+        "causal_attention": sdpa,
+        "causal_attention_gqa": gqa,
+        # cross_entropy/forward_ref.py:6-12
+        "cross_entropy": lambda lg, t: F.cross_entropy(lg.float(), t).to(lg.dtype),
+        # fused_linear_cross_entropy/forward_ref.py:23-35
+        "fused_linear_cross_entropy": lambda x, w, t: F.cross_entropy(
+            torch.matmul(x.float(), w.float().t()), t),
+    }[name]
+
+
+def gpu_eager(name: str, steps: int, warmup: int, flush) -> dict:
+    """Full step (forward + autograd backward) of the eager spelling on this GPU,
+    timed like the pairs: cache flush, events around each step, median."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from evograd_amd import decls
+    from evograd_amd.inputs import make_case_inputs
+
+    base, label = split_name(name)
+    op = decls.get_op(base)
+    w = bench_workload(op, label)
+    inputs = make_case_inputs(op, w, "cuda")
+    fwd = _eager_forward(base)
+    args, leaves = [], []
+    for a in op.args:
+        v = inputs.get(a.name, getattr(a, "default", None))
+        if isinstance(a, decls.Active):
+            v = v.detach().requires_grad_(True)
+            leaves.append(v)
+        args.append(v)
+    dy = inputs[op.upstream_grad_name]
+
+    def step():
+        for lf in leaves:
+            lf.grad = None
+        fwd(*args).backward(dy)
+
+    scale, note = 1.0, ""
+    if base == "rope":  # q of the joint q/k workload; its k heads are the same computation
+        scale = (w.dims["n_heads"] + int(w.extra["k_heads"])) / w.dims["n_heads"]
+        note = f"q timed, scaled x{scale:g} for the k heads"
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(steps):
+            flush()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            step()
+            e1.record()
+            e1.synchronize()
+            samples.append(e0.elapsed_time(e1) * 1e3)
+    del inputs, args, leaves, dy
+    torch.cuda.empty_cache()
+    out = {"full_us": round(statistics.median(samples) * scale, 2)}
+    if note:
+        out["note"] = note
+    return out
+
+
 # ------------------------------------------------------------ sustained rates
 PROBE_ITERS = 100000   # about 0.1 s per probe launch
 
@@ -693,6 +806,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the token sweeps of the memory-bound operators")
+    ap.add_argument("--no-eager", action="store_true",
+                    help="skip the eager torch baseline on the GPU")
     ap.add_argument("--profile", metavar="OP",
                     help="rocprofv3 workload: STEPS x (flush, fwd, bwd) of OP plus copy calibration; "
                          "'sustained' runs the MFMA probe and the HBM copy STEPS times")
@@ -751,6 +866,21 @@ def main() -> int:
             log(f"sweep {name}: " + json.dumps({k: v.get("hbm_frac_full") if isinstance(v, dict)
                                                 else v for k, v in sweeps[name].items()}))
 
+    if not args.no_eager:
+        for name in ops:
+            if name not in EAGER_OPS or "full_us" not in results.get(name, {}):
+                continue
+            log(f"gpu eager {name} ...")
+            try:
+                eg = gpu_eager(name, max(5, args.steps // 2), 2, flush)
+                results[name]["gpu_eager_full_us"] = eg["full_us"]
+                results[name]["speedup_vs_gpu_eager"] = round(eg["full_us"] / results[name]["full_us"], 3)
+                if "note" in eg:
+                    results[name]["gpu_eager_note"] = eg["note"]
+            except Exception as e:
+                results[name]["gpu_eager_error"] = f"{type(e).__name__}: {e}"
+            log(f"gpu eager {name}: " + json.dumps({k: v for k, v in results[name].items()
+                                                     if k.startswith(("gpu_eager", "speedup_vs_gpu"))}))
     log("sustained rates ...")
     try:
         sustained = sustained_rates()
