@@ -493,20 +493,55 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 
   // C tile (i, j): lane l holds row l%32, register r holds column 8(r/4) + 4(l/32) + r%4.
   const int hh = lane >> 5, l32 = lane & 31;
+  // A whole tile of fp32 values (a partial, or an fp32 C without residual) at
+  // dst[r * ld + c], 0 <= r, c < 256, 16-byte aligned rows: staged in LDS in two
+  // halves of 128 rows (128 KB each, all of the slice buffers) and written one
+  // 1 KB row per wave instruction. Written from the accumulator layout directly,
+  // each instruction would touch 32 rows 16 bytes at a time (measured: 8192 x 8192
+  // fp32 C at k = 1024, 241 -> 178 us). LDS rows: 64 16-byte chunks, chunk index
+  // XOR row % 32, so both the accumulator-layout writes and the row reads hit
+  // every bank once.
+  auto store_tile_f32 = [&](float* dst, int64_t ld) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    auto quarter = [&](int qi) {  // 32 fp32 rows each
+      return reinterpret_cast<float*>(qi == 0 ? As0 : qi == 1 ? As1 : qi == 2 ? Bs0 : Bs1);
+    };
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      __syncthreads();  // the last slices (first half) or the previous half are consumed
+      if (wm == half * 128) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float* lrow = quarter(i) + l32 * kBN;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int chunk = (wn + 32 * j + 8 * q + 4 * hh) >> 2;
+              *reinterpret_cast<f32x4*>(lrow + ((chunk ^ l32) << 2)) =
+                  f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]};
+            }
+        }
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int it = 0; it < 32; ++it) {  // wave w writes rows 32 w .. +31 of the half
+        const f32x4 x =
+            *reinterpret_cast<const f32x4*>(quarter(w) + it * kBN + ((lane ^ it) << 2));
+        *reinterpret_cast<f32x4*>(dst + (int64_t)(half * 128 + 32 * w + it) * ld + 4 * lane) = x;
+      }
+    }
+  };
   if (partial && tail) {
     // a split tail's partial: tile-major [kpart][tail tile][256][256], whole tiles
     // (rows and columns past M, N hold sums of zeros and are never read back)
-    float* pt = part + ((int64_t)kpart * tail + (t_idx - head)) * kTileElems;
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<f32x4*>(pt + (wm + 32 * i + l32) * kBN + wn + 32 * j + 8 * q + 4 * hh) =
-              f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                    acc[i][j][4 * q + 3]};
+    store_tile_f32(part + ((int64_t)kpart * tail + (t_idx - head)) * kTileElems, kBN);
+    return;
+  }
+  if (partial && (N & 3) == 0 && m0 + kBM <= M && n0 + kBN <= N) {
+    // split-K partial of a whole tile
+    store_tile_f32(part + (int64_t)blockIdx.y * M * N + (int64_t)m0 * N + n0, N);
     return;
   }
   if (partial) {
@@ -635,6 +670,70 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     if (seg.c[sg]) {
       cb = (TC*)seg.c[sg];
       cshift = seg.dim == kSegM ? (int64_t)seg.start[sg] * ldc : seg.start[sg];
+    }
+  }
+  if constexpr (std::is_same<TC, float>::value) {
+    if (!R && vec_c && m0 + kBM <= M && n0 + kBN <= N) {
+      store_tile_f32(cb + ((int64_t)m0 * ldc - cshift) + n0, ldc);
+      return;
+    }
+  } else {
+    // A whole 16-bit tile is staged in LDS and written as whole 512-byte row
+    // segments (16 bytes per lane, 2 rows per wave instruction): stored from the
+    // accumulator layout directly, each instruction would touch 32 rows 16 bytes at
+    // a time (8192 x 8192 at k = 1024: 187 -> 155 us). A residual is read and added
+    // in the accumulator layout before the one rounding (R may be C: every lane has
+    // read its elements of R before the barrier that precedes the row writes). LDS
+    // rows: 32 16-byte chunks, chunk index XOR row % 32, so that both the
+    // accumulator-layout writes and the row reads hit every bank once.
+    if (vec_c && (ldc & 7) == 0 && m0 + kBM <= M && n0 + kBN <= N) {
+      typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+      auto quarter = [&](int qi) {  // 64 tile rows each
+        return qi == 0 ? As0 : qi == 1 ? As1 : qi == 2 ? Bs0 : Bs1;
+      };
+      auto bits = [](TC x) {
+        uint16_t u;
+        __builtin_memcpy(&u, &x, 2);
+        return (unsigned)u;
+      };
+      __syncthreads();  // every wave is done with the last slices
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = wm + 32 * i + l32;
+        uint16_t* lrow = quarter((wm >> 6) + (i >> 1)) + (r & 63) * kBN;
+        const TC* rrow = R ? (const TC*)R + (int64_t)(m0 + r) * ldr : nullptr;
+        const float* rrow32 = R ? (const float*)R + (int64_t)(m0 + r) * ldr : nullptr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int chunk = (wn + 32 * j + 8 * q) >> 3;
+            float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                          acc[i][j][4 * q + 3]};
+            if (R) {
+              const int col = n0 + wn + 32 * j + 8 * q + 4 * hh;
+              float r4[4];
+              if (r_f32) load_f32<float, 4>(rrow32 + col, r4);
+              else load_f32<TC, 4>(rrow + col, r4);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] += r4[e];
+            }
+            *reinterpret_cast<u32x2*>(lrow + ((chunk ^ (r & 31)) << 3) + 4 * hh) =
+                u32x2{bits(from_f32<TC>(v[0])) | (bits(from_f32<TC>(v[1])) << 16),
+                      bits(from_f32<TC>(v[2])) | (bits(from_f32<TC>(v[3])) << 16)};
+          }
+      }
+      __syncthreads();
+      const int chunk = lane & 31;
+#pragma unroll 4
+      for (int it = 0; it < 32; ++it) {
+        const int r = 64 * w + 2 * it + hh;  // this wave's 64 rows: quarter w
+        const u32x4 v = *reinterpret_cast<const u32x4*>(quarter(w) + (r & 63) * kBN +
+                                                        ((chunk ^ (r & 31)) << 3));
+        *reinterpret_cast<u32x4*>(cb + ((int64_t)(m0 + r) * ldc - cshift) + n0 + 8 * chunk) = v;
+      }
+      return;
     }
   }
 #pragma unroll
