@@ -289,7 +289,7 @@ __device__ __forceinline__ float acc_read(float x) {
 // substep 1 suits the product with both operands K-major, substep 0 the others.
 template <bool AKC, bool BKC> struct LoadSpread { static constexpr int b_substep = !AKC && !BKC ? 1 : 0; };
 
-template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false, bool SEG = false>
+template <typename T, bool AKC, bool BKC, typename TC, bool SMX = false, int SEG = 0>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                  TC* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -379,61 +379,60 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const int64_t ob = BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0;
     lb.load(B + ob, kt < nk ? (b_end - ob) * 2 : 0, bs);
   };
-  // Segmented operands (seg.dim): along M or N the tile's segment is fixed for the
-  // workgroup; along K each slice picks its segment.
-  const OpView va_t = seg_view<AKC>(A, a_rows, lda, seg, seg.a, false, m0);
-  const OpView vb_t = seg_view<BKC>(B, b_rows, ldb, seg, seg.b, false, n0);
-  // Along K, the segment bases and starts are read once, here, so that each slice
-  // selects among values already in registers (an indexed read of the argument
-  // table inside the loop is a scalar memory load, and waiting for it also waits
-  // for the LDS reads in flight).
-  const bool kseg = seg.dim == kSegK;
-  const int ks1 = kseg && seg.n > 1 ? seg.start[1] : 0x7fffffff;
-  const int ks2 = kseg && seg.n > 2 ? seg.start[2] : 0x7fffffff;
-  const int ks3 = kseg && seg.n > 3 ? seg.start[3] : 0x7fffffff;
-  const uint16_t* ka[kMaxSegs];
-  const uint16_t* kbp[kMaxSegs];
-#pragma unroll
-  for (int i = 0; i < kMaxSegs; ++i) {
-    ka[i] = kseg && seg.a[i] ? (const uint16_t*)seg.a[i] : A;
-    kbp[i] = kseg && seg.b[i] ? (const uint16_t*)seg.b[i] : B;
+  // Segmented operands (SEG = 1: along M or N, the tile's segment is fixed for the
+  // workgroup; SEG = 2: along K, each operand keeps a running view that advances when
+  // a slice crosses into the next segment: slices are loaded in increasing k, and the
+  // argument table is read only on a crossing, so the loop holds no indexed argument
+  // read, whose scalar-memory wait would also wait for the LDS reads in flight).
+  OpView va = seg_view<AKC>(A, a_rows, lda, seg, seg.a, false, m0);
+  OpView vb = seg_view<BKC>(B, b_rows, ldb, seg, seg.b, false, n0);
+  int sa = 0, sb = 0, next_a = 0x7fffffff, next_b = 0x7fffffff;
+  if constexpr (SEG == 2) {
+    auto first = [&](auto kcc, const void* t0, int64_t rows, int64_t ld, OpView& v, int& nx) {
+      constexpr bool KC = decltype(kcc)::value;
+      if (!t0) return;  // this operand is the plain buffer
+      v.base = (const uint16_t*)t0;
+      v.shift = 0;
+      v.end = KC ? rows * ld : (int64_t)seg.start[1] * ld;
+      nx = seg.n > 1 ? seg.start[1] : 0x7fffffff;
+    };
+    first(std::integral_constant<bool, AKC>{}, seg.a[0], a_rows, lda, va, next_a);
+    first(std::integral_constant<bool, BKC>{}, seg.b[0], b_rows, ldb, vb, next_b);
   }
-  const bool ka_seg = kseg && seg.a[0], kb_seg = kseg && seg.b[0];
-  // element view of a k slice of a K-segmented operand: rows k (k-major) or columns
-  auto kview = [&](auto kcc, const uint16_t* const* tab, bool segd, int64_t rows, int64_t ld,
-                   int k0, OpView plain) {
+  auto advance = [&](auto kcc, const void* const* tab, int64_t rows, int64_t ld, int k0,
+                     OpView& v, int& si, int& nx) {
     constexpr bool KC = decltype(kcc)::value;
-    if (!segd) return plain;
-    const int si = (k0 >= ks1) + (k0 >= ks2) + (k0 >= ks3);
-    const uint16_t* b = si == 0 ? tab[0] : si == 1 ? tab[1] : si == 2 ? tab[2] : tab[3];
-    const int st = si == 0 ? 0 : si == 1 ? ks1 : si == 2 ? ks2 : ks3;
-    const int en = si == 0 ? min(ks1, K) : si == 1 ? min(ks2, K) : si == 2 ? min(ks3, K) : K;
-    OpView v;
-    v.base = b;
-    v.shift = KC ? st : (int64_t)st * ld;
-    v.end = KC ? rows * ld : (int64_t)(en - st) * ld;
-    return v;
+    while (k0 >= nx) {  // uniform and rare: at most kMaxSegs - 1 times per operand
+      ++si;
+      const int64_t st = seg.start[si], en = seg.start[si + 1];
+      v.base = (const uint16_t*)tab[si];
+      v.shift = KC ? st : st * ld;
+      v.end = KC ? rows * ld : (en - st) * ld;
+      nx = si + 1 < seg.n ? seg.start[si + 1] : 0x7fffffff;
+    }
   };
   auto loadA_seg = [&](int kt, uint16_t* as) {
     const int k0 = kt * kBK;
-    const OpView va = kview(std::integral_constant<bool, AKC>{}, ka, ka_seg, a_rows, lda, k0, va_t);
+    if constexpr (SEG == 2)
+      advance(std::integral_constant<bool, AKC>{}, seg.a, a_rows, lda, k0, va, sa, next_a);
     const int64_t oa = (AKC ? (int64_t)m0 * lda + k0 : (int64_t)k0 * lda + m0) - va.shift;
     la.load(va.base + oa, kt < nk ? (va.end - oa) * 2 : 0, as);
   };
   auto loadB_seg = [&](int kt, uint16_t* bs) {
     const int k0 = kt * kBK;
-    const OpView vb = kview(std::integral_constant<bool, BKC>{}, kbp, kb_seg, b_rows, ldb, k0, vb_t);
+    if constexpr (SEG == 2)
+      advance(std::integral_constant<bool, BKC>{}, seg.b, b_rows, ldb, k0, vb, sb, next_b);
     const int64_t ob = (BKC ? (int64_t)n0 * ldb + k0 : (int64_t)k0 * ldb + n0) - vb.shift;
     lb.load(vb.base + ob, kt < nk ? (vb.end - ob) * 2 : 0, bs);
   };
   // The segmented form is a separate instantiation (SEG): its per-slice selection
   // costs the plain products 7-19% when compiled into the same kernel.
   auto loadA = [&](int kt, uint16_t* as) {
-    if constexpr (SEG) loadA_seg(kt, as);
+    if constexpr (SEG != 0) loadA_seg(kt, as);
     else loadA_plain(kt, as);
   };
   auto loadB = [&](int kt, uint16_t* bs) {
-    if constexpr (SEG) loadB_seg(kt, bs);
+    if constexpr (SEG != 0) loadB_seg(kt, bs);
     else loadB_plain(kt, bs);
   };
   loadA(kb, As0);
@@ -665,7 +664,7 @@ void gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
   // C of the tile's segment (along M: rows; along N: columns)
   TC* cb = C;
   int64_t cshift = 0;
-  if (SEG && (seg.dim == kSegM || seg.dim == kSegN)) {
+  if (SEG == 1) {
     const int sg = seg_of(seg, seg.dim == kSegM ? m0 : n0);
     if (seg.c[sg]) {
       cb = (TC*)seg.c[sg];
@@ -1105,10 +1104,16 @@ int gemm_impl(const void* A, const void* B, void* C, int64_t M, int64_t N, int64
     if (seg.dim != kSegNone) {
       // segmented products: 16-bit C only (one more instantiation per layout)
       if constexpr (std::is_same<T, TC>::value) {
-        EG_LAUNCH((gemm_kernel<T, AK, BK, TC, false, true>), dim3(grid_x, (unsigned)splits),
-                  dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
-                  (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c,
-                  SmxArgs{}, R, ldr, (int)r_f32, kt_per, part, (int)tp.head, (int)tp.tail, seg);
+        if (seg.dim == kSegK)
+          EG_LAUNCH((gemm_kernel<T, AK, BK, TC, false, 2>), dim3(grid_x, (unsigned)splits),
+                    dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
+                    (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c,
+                    SmxArgs{}, R, ldr, (int)r_f32, kt_per, part, (int)tp.head, (int)tp.tail, seg);
+        else
+          EG_LAUNCH((gemm_kernel<T, AK, BK, TC, false, 1>), dim3(grid_x, (unsigned)splits),
+                    dim3(kThreads), 0, st, (const uint16_t*)A, (const uint16_t*)B, (TC*)C, (int)M,
+                    (int)N, (int)K, lda, ldb, ldc, a_rows, b_rows, (int)tiles_m, (int)tiles, vec_c,
+                    SmxArgs{}, R, ldr, (int)r_f32, kt_per, part, (int)tp.head, (int)tp.tail, seg);
       } else {
         set_error("%s: segmented products write C in the operands' dtype", name);
         return 1;

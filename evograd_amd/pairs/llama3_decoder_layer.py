@@ -87,6 +87,14 @@ class _Shape:
         self.qkv = self.q_out + 2 * self.kv_out
         self.fuse_qkv = wide and self.q_out % 256 == 0 and self.kv_out % 256 == 0
         self.fuse_mlp = wide and self.inter % 256 == 0
+        # the input gradients as one product with the weights as segments along K, or
+        # as separate products accumulating through the residual operand. q/k/v: one
+        # product at every T (measured T = 1024 / 2048 / 4096: -51 / -59 / -69 us per
+        # backward). gate/up: one product only while dh2 has fewer output tiles than
+        # half the CUs, where the products split k and one split beats two (T = 1024:
+        # -17 us; T = 2048 / 4096: +40 / +20 us, one long product against two)
+        self.kseg_qkv = self.fuse_qkv
+        self.kseg_mlp = self.fuse_mlp and (self.M + 255) // 256 * ((self.hidden + 255) // 256) < 128
         if wide and self.hidden % 64:
             raise ValueError(f"llama3_decoder_layer: 16-bit inputs need hidden % 64 == 0, got "
                              f"{self.hidden}")
@@ -333,8 +341,12 @@ def llama3_decoder_layer_backward_from_saved(dout, saved, eps: float = 1e-5):
     if s.fuse_mlp:
         # dh2 = [dgate | dup] [Wg; Wu] (segments along K); [dWg; dWu] = [dgate | dup]^T h2
         # (A's columns in two segments along M) into one buffer, returned as two views
-        ops.gemm_seg(None, None, dh2, M, hidden, 2 * s.inter, s.Ip, hidden, hidden, True, False,
-                     3, [s.inter, s.inter], a_segs=[dgate, dup], b_segs=[wg, wu])
+        if s.kseg_mlp:
+            ops.gemm_seg(None, None, dh2, M, hidden, 2 * s.inter, s.Ip, hidden, hidden, True,
+                         False, 3, [s.inter, s.inter], a_segs=[dgate, dup], b_segs=[wg, wu])
+        else:
+            ops.linear_dinput(dgate, wg, dh2, M, s.inter, hidden, s.Ip, hidden)
+            ops.linear_dinput(dup, wu, dh2, M, s.inter, hidden, s.Ip, hidden, r=dh2)
         d_wgu = ops.empty(2 * s.inter, hidden)
         ops.gemm_seg(None, h2, d_wgu, 2 * s.inter, hidden, M, s.Ip, hidden, hidden, False, False,
                      1, [s.inter, s.inter], a_segs=[dgate, dup])
@@ -385,8 +397,15 @@ def llama3_decoder_layer_backward_from_saved(dout, saved, eps: float = 1e-5):
         ops.merge(dkh, dqkv[:, s.q_out:], s, s.KVH, s.qkv, 2, cos, sin)
         ops.merge(dvh, dqkv[:, s.q_out + s.kv_out:], s, s.KVH, s.qkv, 0)
         del dqh, dkh, dvh
-        ops.gemm_seg(dqkv, None, dh1, M, hidden, s.qkv, s.qkv, hidden, hidden, True, False, 3,
-                     [s.q_out, s.kv_out, s.kv_out], b_segs=[wq, wk, wv])
+        if s.kseg_qkv:
+            ops.gemm_seg(dqkv, None, dh1, M, hidden, s.qkv, s.qkv, hidden, hidden, True, False,
+                         3, [s.q_out, s.kv_out, s.kv_out], b_segs=[wq, wk, wv])
+        else:
+            ops.linear_dinput(dqkv, wq, dh1, M, s.q_out, hidden, s.qkv, hidden)
+            ops.linear_dinput(dqkv[:, s.q_out:], wk, dh1, M, s.kv_out, hidden, s.qkv, hidden,
+                              r=dh1)
+            ops.linear_dinput(dqkv[:, s.q_out + s.kv_out:], wv, dh1, M, s.kv_out, hidden, s.qkv,
+                              hidden, r=dh1)
         d_wqkv = ops.empty(s.qkv, hidden)
         ops.linear_dweight(dqkv, h1, d_wqkv, M, s.qkv, hidden, s.qkv, hidden)
         d_wq = d_wqkv[:s.q_out]
