@@ -913,16 +913,16 @@ __global__ __launch_bounds__(256) void splitk_tail_reduce_kernel(
 
 }  // namespace
 
-// Split-K: when the output has fewer tiles than kSplitTarget (one per CU of an
-// MI355X; a constant, so the summation order depends on the shape only) and the
-// caller's workspace holds the fp32 partials, K is cut into `splits` ranges of
-// whole 64-deep slices, at least kMinSliceRun each.
+// Split-K: when the output has at most half as many tiles as kSplitTarget (one per
+// CU of an MI355X; a constant, so the summation order depends on the shape only)
+// and the caller's workspace holds the fp32 partials, K is cut into `splits` ranges
+// of whole 64-deep slices, at least kMinSliceRun each.
 constexpr int kSplitTarget = 256, kMaxSplits = 16, kMinSliceRun = 4;
 
 int gemm_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   const int64_t nk = (K + kBK - 1) / kBK;
-  if (tiles >= kSplitTarget / 2) return 1;
+  if (tiles > kSplitTarget / 2) return 1;  // 128 tiles: 2 splits fill the 256 CUs
   int64_t s = std::min<int64_t>(kMaxSplits, kSplitTarget / tiles);
   s = std::min<int64_t>(s, nk / kMinSliceRun);
   if (s < 2) return 1;

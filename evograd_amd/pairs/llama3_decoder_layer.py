@@ -90,11 +90,11 @@ class _Shape:
         # the input gradients as one product with the weights as segments along K, or
         # as separate products accumulating through the residual operand. q/k/v: one
         # product at every T (measured T = 1024 / 2048 / 4096: -51 / -59 / -69 us per
-        # backward). gate/up: one product only while dh2 has fewer output tiles than
-        # half the CUs, where the products split k and one split beats two (T = 1024:
-        # -17 us; T = 2048 / 4096: +40 / +20 us, one long product against two)
+        # backward). gate/up: one product only while dh2 has at most 128 output tiles
+        # (half the CUs), where the products split k and one split product beats two
+        # (T = 1024: -17 us; at T = 4096, 256 tiles, one long product against two: +20 us)
         self.kseg_qkv = self.fuse_qkv
-        self.kseg_mlp = self.fuse_mlp and (self.M + 255) // 256 * ((self.hidden + 255) // 256) < 128
+        self.kseg_mlp = self.fuse_mlp and (self.M + 255) // 256 * ((self.hidden + 255) // 256) <= 128
         if wide and self.hidden % 64:
             raise ValueError(f"llama3_decoder_layer: 16-bit inputs need hidden % 64 == 0, got "
                              f"{self.hidden}")

@@ -369,11 +369,11 @@ int eg_scale_copy(const void* src, int src_dtype, void* dst, int dst_dtype, int6
  * other operand is k-major, a row stride of at least k rounded up to 64 whose columns
  * past k hold finite values (zeros); strides are multiples of 8 elements and a, b are
  * 16-byte aligned.
- * Products with fewer output tiles (256 x 256) than an MI355X has CUs split k over
- * workgroups when `workspace` holds at least eg_gemm_workspace_bytes(m, n, k, dtype)
- * bytes (else, or with workspace NULL, they run unsplit): each k range writes an
- * fp32 partial, and a second pass sums them in a fixed order, adds r and rounds c
- * once. So do the tiles of a last wave that is at most half full (more than 256
+ * Products with at most half as many output tiles (256 x 256) as an MI355X has CUs
+ * split k over workgroups when `workspace` holds at least
+ * eg_gemm_workspace_bytes(m, n, k, dtype) bytes (else, or with workspace NULL, they
+ * run unsplit): each k range writes an fp32 partial, and a second pass sums them in
+ * a fixed order, adds r and rounds c once. So do the tiles of a last wave that is at most half full (more than 256
  * tiles). The split depends on the shape only, so results are bitwise repeatable. */
 size_t eg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int dtype);
 int eg_gemm(const void* a, const void* b, void* c, const void* r, int64_t m, int64_t n,

@@ -88,7 +88,7 @@ def test_flce_scratch_grows_with_the_chunk_not_with_rows_times_vocab():
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
 def test_gemm_workspace_split_k_and_split_tail():
-    """Split k (fewer than 128 tiles of 256 x 256): splits x M x N fp32. Split tail
+    """Split k (at most 128 tiles of 256 x 256): splits x M x N fp32. Split tail
     (more than 256 tiles, the last wave of 256 at most half full): parts x tail tiles
     of 256 x 256 fp32, parts = min(4, 256 / tail, slices / 4) rounded to whole slices."""
     q = lambda m, n, k: _lib.query("eg_gemm_workspace_bytes", m, n, k, _lib.EG_BF16)
@@ -99,6 +99,7 @@ def test_gemm_workspace_split_k_and_split_tail():
     assert q(4096, 14336, 4096) == 2 * 128 * tile            # 896 tiles: 128 in 2 parts
     assert q(14336, 4096, 4096) == 2 * 128 * tile
     assert q(2048, 14336, 4096) == 0                         # 448 tiles: last wave 3/4 full
+    assert q(2048, 4096, 14336) == 2 * 2048 * 4096 * 4       # 128 tiles: 2 splits
     assert q(128256, 4096, 4096) == 3 * 80 * tile            # 8016 tiles: 80 in 3 parts
     assert q(4300, 4000, 704) == 2 * 16 * tile               # 272 tiles, 11 slices
     assert q(4300, 4000, 448) == 0                           # 7 slices: no two runs of 4
