@@ -678,7 +678,10 @@ PROBE_ITERS = 100000   # about 0.1 s per probe launch
 def sustained_rates(reps: int = 3) -> dict:
     """The device's sustained rates in this run, beside the published peaks: bf16
     MFMA from registers on random operands (eg_probe_mfma_bf16, one 256-thread
-    workgroup per CU, launches of about 0.1 s so power management settles), and an
+    workgroup per CU, launches of about 0.1 s so power management settles), the same
+    work as v_mfma_f32_16x16x32_bf16 at two waves per SIMD, the 32 x 32 x 16 work fed
+    by one 1 KiB LDS operand read per MFMA (the attention kernels' operand traffic),
+    without and with one exponential per MFMA (eg_probe_mfma_mix kinds 1-3), and an
     HBM copy (torch's copy kernel over 1 GiB each way, larger than every cache)."""
     import torch
 
@@ -687,11 +690,15 @@ def sustained_rates(reps: int = 3) -> dict:
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     g = torch.Generator(device="cuda").manual_seed(7)
     operands = torch.randn(16384, device="cuda", generator=g).to(torch.bfloat16)  # 32 KiB
-    out = torch.empty(cus * 256, device="cuda")
+    out = torch.empty(2 * cus * 256, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
 
     def probe(iters):
         _lib.call("eg_probe_mfma_bf16", operands.data_ptr(), out.data_ptr(), cus, iters, stream)
+
+    def mix(kind, iters):
+        _lib.call("eg_probe_mfma_mix", kind, operands.data_ptr(), out.data_ptr(), 2 * cus, iters,
+                  stream)
 
     def timed(fn):
         fn()
@@ -708,9 +715,17 @@ def sustained_rates(reps: int = 3) -> dict:
 
     probe(PROBE_ITERS // 10)
     s = timed(lambda: probe(PROBE_ITERS))
-    if not torch.isfinite(out).all():
+    if not torch.isfinite(out[: cus * 256]).all():
         raise RuntimeError("MFMA probe produced non-finite checksums")
     mfma_tflops = cus * 4 * PROBE_ITERS * 64 * 32768 / s / 1e12
+    kinds = {}
+    for kind, key in ((1, "mfma16_bf16_tflops"), (2, "mfma_lds_operand_tflops"),
+                      (3, "mfma_lds_operand_exp_tflops")):
+        it = PROBE_ITERS // 2
+        t = timed(lambda: mix(kind, it))
+        if not torch.isfinite(out).all():
+            raise RuntimeError(f"MFMA probe kind {kind} produced non-finite checksums")
+        kinds[key] = round(2 * cus * 4 * it * 64 * 32768 / t / 1e12, 1)
     n = 1 << 29  # bf16 elements: 1 GiB
     src = torch.randn(n, device="cuda", generator=g, dtype=torch.bfloat16)
     dst = torch.empty_like(src)
@@ -718,15 +733,24 @@ def sustained_rates(reps: int = 3) -> dict:
     copy_gbs = 2 * n * 2 / c / 1e9
     del src, dst
     torch.cuda.empty_cache()
-    return {
+    res = {
         "mfma_bf16_tflops": round(mfma_tflops, 1),
         "mfma_frac_of_peak": round(mfma_tflops / BF16_PEAK_TFLOPS, 4),
+    }
+    for key, v in kinds.items():
+        res[key] = v
+        res[key.replace("_tflops", "_frac_of_peak")] = round(v / BF16_PEAK_TFLOPS, 4)
+    res.update({
         "hbm_copy_gbs": round(copy_gbs, 1),
         "hbm_copy_frac_of_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
-        "how": ("eg_probe_mfma_bf16: 64 MFMAs per wave per iteration from registers, random bf16 "
-                f"operands, {cus} workgroups x {PROBE_ITERS} iterations, median of {reps}; copy: "
-                f"torch copy_ of 1 GiB bf16, median of {reps}"),
-    }
+        "how": ("eg_probe_mfma_bf16: 64 v_mfma_f32_32x32x16_bf16 per wave per iteration from "
+                f"registers, random bf16 operands, {cus} workgroups x {PROBE_ITERS} iterations; "
+                "eg_probe_mfma_mix kinds 1-3 (the same FLOPs as 16x16x32 from registers; as "
+                "32x32x16 each fed one 1 KiB ds_read_b128; the latter plus one exp per MFMA), "
+                f"{2 * cus} workgroups (two waves per SIMD) x {PROBE_ITERS // 2} iterations; "
+                f"medians of {reps}; copy: torch copy_ of 1 GiB bf16, median of {reps}"),
+    })
+    return res
 
 
 # ---------------------------------------------------------- profiling mode

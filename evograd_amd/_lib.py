@@ -81,6 +81,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_layernorm_bwd_small": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_silu_mul": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "eg_probe_mfma_bf16": (_i32, [_p, _p, _i32, _i32, _p]),
+    "eg_probe_mfma_mix": (_i32, [_i32, _p, _p, _i32, _i32, _p]),
     "eg_gemm_segmented": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
                                  _i32, _p, _p, _p, _p, _i32, _i32, _p, _size, _p]),
 }

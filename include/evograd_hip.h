@@ -442,6 +442,21 @@ int eg_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtyp
  * (checksums that keep the work live). */
 int eg_probe_mfma_bf16(const void* operands, float* out, int workgroups, int iters, void* stream);
 
+/* Measurement aid (no counterpart in the reference): the same 64 x 32768 FLOP per
+ * wave and iteration as eg_probe_mfma_bf16, in one of four loops, for the ceilings
+ * bench.py reports beside the MFMA-bound kernels' fractions:
+ *   kind 0: eg_probe_mfma_bf16's loop (32 x 32 x 16 from registers, one wave per
+ *           SIMD: pass the CU count as `workgroups`);
+ *   kind 1: 128 v_mfma_f32_16x16x32_bf16 from registers (pass twice the CU count:
+ *           two waves per SIMD);
+ *   kind 2: 64 v_mfma_f32_32x32x16_bf16 each fed one ds_read_b128 of the operands
+ *           staged in LDS, 1 KiB per wave and MFMA as in the attention kernels
+ *           (twice the CU count);
+ *   kind 3: kind 2 plus one v_exp_f32 per MFMA (the softmax's exponentials).
+ * Operands, out and the checksums as for eg_probe_mfma_bf16. */
+int eg_probe_mfma_mix(int kind, const void* operands, float* out, int workgroups, int iters,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

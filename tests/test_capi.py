@@ -149,6 +149,10 @@ def test_host_side_validation_errors_without_gpu():
         _lib.call("eg_probe_mfma_bf16", None, None, 256, 1, None)
     with pytest.raises(RuntimeError, match="workgroups"):
         _lib.call("eg_probe_mfma_bf16", 16, 16, 0, 1, None)
+    with pytest.raises(RuntimeError, match="kind must be"):
+        _lib.call("eg_probe_mfma_mix", 4, 16, 16, 256, 1, None)
+    with pytest.raises(RuntimeError, match="workgroups"):
+        _lib.call("eg_probe_mfma_mix", 1, 16, 16, 0, 1, None)
     # empty inputs are a no-op, not an error
     _lib.call("eg_softmax_fwd", None, None, 0, 0, _lib.EG_F32, None)
     _lib.call("eg_cross_entropy_bwd", None, None, None, None, None, None, 0, 8, -100,
