@@ -236,196 +236,3 @@ def test_small_norm_program_gate_and_repeatability(name):
     b = bwd(inp["dy"], saved, eps=inp["eps"])
     torch.cuda.synchronize()
     assert all(torch.equal(p, q) for p, q in zip(a, b))
-
-"""Parity of the HIP pairs with the autograd oracle on the GPU.
-
-Every case runs the reference's gate (restated in oracle/verify.py): identical
-seeded inputs, the oracle's forward and gradients, then shape, dtype and
-allclose on the output and every gradient at this build's tolerances
-(fp32 1e-5/1e-5, fp16 1e-2/1e-2, bf16 2e-2/2e-2; see evograd_amd/decls.py).
-The benchmark-size cases run the same gate at full size plus size-independent
-properties (bitwise determinism of the two-stage reductions, in-place backward,
-joint q/k RoPE == two single launches).
-"""
-
-import sys
-
-import pytest
-import torch
-
-from evograd_amd import decls, pair_module
-from evograd_amd.inputs import make_case_inputs
-from oracle.oracle import oracle
-from oracle.verify import verify
-
-pytestmark = pytest.mark.gpu
-
-MEMORY_BOUND = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "fused_add_rms_norm",
-                "cross_entropy")
-
-
-def _cases(names):
-    for name in names:
-        for w in decls.get_op(name).correctness:
-            yield pytest.param(name, w, id=f"{name}-{w.key()}")
-
-
-def _run(name, w):
-    print(f"\n[gpu-parity] {name} {w.dims} {w.dtype} {w.label}", flush=True)
-    sys.stdout.flush()
-    rep = verify(decls.get_op(name), pair_module(name), device="cuda", workloads=(w,))
-    torch.cuda.synchronize()
-    assert rep.ok, "\n".join(rep.failures())
-    return rep
-
-
-@pytest.mark.parametrize("name,w", list(_cases(MEMORY_BOUND)))
-def test_memory_bound_correctness_workloads(name, w):
-    _run(name, w)
-
-
-@pytest.mark.parametrize("name", MEMORY_BOUND)
-def test_memory_bound_baseline_config(name):
-    for w in decls.get_op(name).benchmark:
-        _run(name, w)
-        torch.cuda.empty_cache()
-
-
-def test_rmsnorm_backward_is_bitwise_deterministic():
-    op = decls.RMSNORM
-    w = op.benchmark[0]
-    inp = make_case_inputs(op, w, "cuda")
-    mod = pair_module("rmsnorm")
-    _, saved = mod.rmsnorm_forward_with_saved(inp["x"], inp["weight"], inp["eps"])
-    a = mod.rmsnorm_backward_from_saved(inp["dy"], saved, eps=inp["eps"])
-    b = mod.rmsnorm_backward_from_saved(inp["dy"], saved, eps=inp["eps"])
-    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
-
-
-def test_layernorm_backward_is_bitwise_deterministic():
-    op = decls.LAYERNORM
-    inp = make_case_inputs(op, op.correctness[-3], "cuda")
-    mod = pair_module("layernorm")
-    _, saved = mod.layernorm_forward_with_saved(inp["x"], inp["weight"], inp["bias"], inp["eps"])
-    a = mod.layernorm_backward_from_saved(inp["dy"], saved)
-    b = mod.layernorm_backward_from_saved(inp["dy"], saved)
-    assert all(torch.equal(x, y) for x, y in zip(a, b))
-
-
-def test_swiglu_inplace_backward_matches():
-    mod = pair_module("swiglu")
-    op = decls.SWIGLU
-    w = op.correctness[-1]
-    inp = make_case_inputs(op, w, "cuda")
-    _, saved = mod.swiglu_forward_with_saved(inp["a"], inp["b"])
-    ref = mod.swiglu_backward_from_saved(inp["dc"], saved)
-    a2, b2 = inp["a"].clone(), inp["b"].clone()
-    mod.INPLACE_BACKWARD = True
-    try:
-        da, db = mod.swiglu_backward_from_saved(inp["dc"], (a2, b2))
-    finally:
-        mod.INPLACE_BACKWARD = False
-    assert da.data_ptr() == a2.data_ptr() and db.data_ptr() == b2.data_ptr()
-    assert torch.equal(da, ref[0]) and torch.equal(db, ref[1])
-
-
-def test_rope_joint_qk_equals_single_launches_and_oracle():
-    mod = pair_module("rope")
-    w = decls.ROPE.benchmark[0]
-    inp = make_case_inputs(decls.ROPE, w, "cuda")
-    q = inp["x"]
-    torch.manual_seed(1234)
-    k = torch.randn((q.shape[0], w.extra["k_heads"], q.shape[2], q.shape[3]), device="cuda",
-                    dtype=q.dtype)
-    (qo, ko), saved = mod.rope_qk_forward_with_saved(q, k, inp["cos"], inp["sin"])
-    qo1, _ = mod.rope_forward_with_saved(q, inp["cos"], inp["sin"])
-    ko1, _ = mod.rope_forward_with_saved(k, inp["cos"], inp["sin"])
-    assert torch.equal(qo, qo1) and torch.equal(ko, ko1)
-    dq, dk = mod.rope_qk_backward_from_saved((inp["dy"], k), saved)
-    assert torch.equal(dq, mod.rope_backward_from_saved(inp["dy"], saved))
-    yk, gk = oracle(decls.ROPE, {"x": k, "cos": inp["cos"], "sin": inp["sin"], "dy": k})
-    assert torch.allclose(ko.float(), yk.float(), atol=2e-2, rtol=2e-2)
-    assert torch.allclose(dk.float(), gk["dx"].float(), atol=2e-2, rtol=2e-2)
-    # the rotation is orthogonal: per (i, i + half) pair the norm is preserved
-    half = q.shape[-1] // 2
-    n_in = q.float()[..., :half] ** 2 + q.float()[..., half:] ** 2
-    n_out = qo.float()[..., :half] ** 2 + qo.float()[..., half:] ** 2
-    assert torch.allclose(n_in, n_out, rtol=2e-2, atol=2e-2)
-
-
-def test_rope_joint_qk_partial_head_groups():
-    """Heads are served in groups of four: q with 6 heads (a full and a partial group)
-    and k with 2 (one partial group) in one joint launch equal two single launches and
-    the oracle."""
-    mod = pair_module("rope")
-    g = torch.Generator(device="cpu").manual_seed(99)
-    q = torch.randn((2, 6, 33, 128), generator=g).to("cuda", torch.bfloat16)
-    k = torch.randn((2, 2, 33, 128), generator=g).to("cuda", torch.bfloat16)
-    pos = torch.arange(33, dtype=torch.float32)[:, None]
-    inv = 10000.0 ** (-torch.arange(0, 64, dtype=torch.float32) / 64)
-    ang = torch.cat([pos * inv, pos * inv], dim=-1)
-    cos, sin = ang.cos().cuda(), ang.sin().cuda()
-    print("\n[gpu-parity] rope joint q[2,6,33,128] k[2,2,33,128] bf16", flush=True)
-    (qo, ko), saved = mod.rope_qk_forward_with_saved(q, k, cos, sin)
-    assert torch.equal(qo, mod.rope_forward_with_saved(q, cos, sin)[0])
-    assert torch.equal(ko, mod.rope_forward_with_saved(k, cos, sin)[0])
-    for x, y in ((q, qo), (k, ko)):
-        yr, _ = oracle(decls.ROPE, {"x": x, "cos": cos, "sin": sin, "dy": x})
-        assert torch.allclose(y.float(), yr.float(), atol=2e-2, rtol=2e-2)
-    dq, dk = mod.rope_qk_backward_from_saved((q, k), saved)
-    _, gq = oracle(decls.ROPE, {"x": q, "cos": cos, "sin": sin, "dy": q})
-    _, gk = oracle(decls.ROPE, {"x": k, "cos": cos, "sin": sin, "dy": k})
-    assert torch.allclose(dq.float(), gq["dx"].float(), atol=2e-2, rtol=2e-2)
-    assert torch.allclose(dk.float(), gk["dx"].float(), atol=2e-2, rtol=2e-2)
-    # the same pair as an autograd node (the benchmark's autograd-bound step)
-    ql, kl = q.detach().requires_grad_(True), k.detach().requires_grad_(True)
-    qa, ka = mod.RopeQK.apply(ql, kl, cos, sin)
-    assert torch.equal(qa, qo) and torch.equal(ka, ko)
-    torch.autograd.backward((qa, ka), (q, k))
-    assert torch.equal(ql.grad, dq) and torch.equal(kl.grad, dk)
-
-
-def test_fused_add_rms_norm_backward_deterministic_and_grads_not_aliased():
-    """Bitwise-repeatable backward at the Llama-3-8B size; through the autograd
-    binding x.grad and r.grad hold equal values in separate storage (the pair
-    returns the single gradient through s for both slots)."""
-    from evograd_amd.bind import bind
-
-    op = decls.FUSED_ADD_RMS_NORM
-    w = op.benchmark[0]
-    print(f"\n[gpu-parity] fused_add_rms_norm determinism {w.dims}", flush=True)
-    inp = make_case_inputs(op, w, "cuda")
-    mod = pair_module("fused_add_rms_norm")
-    _, saved = mod.fused_add_rms_norm_forward_with_saved(inp["x"], inp["r"], inp["weight"],
-                                                         inp["eps"])
-    a = mod.fused_add_rms_norm_backward_from_saved(inp["dout"], saved, eps=inp["eps"])
-    b = mod.fused_add_rms_norm_backward_from_saved(inp["dout"], saved, eps=inp["eps"])
-    assert all(torch.equal(p, q) for p, q in zip(a, b))
-    small = make_case_inputs(op, decls.FUSED_ADD_RMS_NORM.correctness[-1], "cuda")
-    leaves = [small[n].detach().requires_grad_(True) for n in ("x", "r", "weight")]
-    y = bind(op, mod)(*leaves, small["eps"])
-    y.backward(small["dout"])
-    gx, gr = leaves[0].grad, leaves[1].grad
-    assert torch.equal(gx, gr)
-    assert gx.untyped_storage().data_ptr() != gr.untyped_storage().data_ptr()
-
-
-def test_shape_dispatch_routes_hip_programs():
-    """The wire format with HIP programs on both routes: the dispatched pair passes
-    the gate below and above the declaration's 4096-row split, and the saved state
-    carries the route tag."""
-    from evograd_amd.dispatch import ShapeDispatch
-    from evograd_amd.opdecl import Workload
-
-    op = decls.RMSNORM
-    hip = pair_module("rmsnorm")
-    pair = ShapeDispatch(op, hip, hip)
-    small = Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16")
-    large = Workload(dims=dict(rows=4096, hidden=4096), dtype="bfloat16")
-    print("\n[gpu-parity] dispatch rmsnorm", small.dims, large.dims, flush=True)
-    for w, route in ((small, 0), (large, 1)):
-        rep = verify(op, pair, device="cuda", workloads=(w,))
-        assert rep.ok, "\n".join(rep.failures())
-        inp = make_case_inputs(op, w, "cuda")
-        _, saved = pair.rmsnorm_forward_with_saved(inp["x"], inp["weight"], inp["eps"])
-        assert saved[0] == route
