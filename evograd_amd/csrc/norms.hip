@@ -395,7 +395,7 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_fwd_row(const T* __restrict__ x
   }
 #pragma unroll
   for (int rr = 0; rr < RPW; ++rr)
-    if (threadIdx.x == rr && row0 + rr < rows) rstd_out[row0 + rr] = rs[rr];
+    if ((int)threadIdx.x == rr && row0 + rr < rows) rstd_out[row0 + rr] = rs[rr];
 }
 
 // LayerNorm forward, one wave per row (rows of ITEMS x 64 lanes x VEC elements):
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(BLOCK) void layernorm_fwd_row(const T* __restrict__
   }
 #pragma unroll
   for (int rr = 0; rr < RPW; ++rr)
-    if (threadIdx.x == rr && row0 + rr < rows) {
+    if ((int)threadIdx.x == rr && row0 + rr < rows) {
       rstd_out[row0 + rr] = rs[rr];
       mean_out[row0 + rr] = mean[rr];
     }
