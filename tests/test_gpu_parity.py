@@ -52,6 +52,29 @@ def test_memory_bound_baseline_config(name):
         torch.cuda.empty_cache()
 
 
+# Row widths at the edges of the softmax kernels' row configurations: 16-byte packs per
+# row (npack) at each boundary of the register-row choices (64 .. 8192 packs of 512-1024
+# threads), the 16-bit LDS-row path above 8192 packs and the two-read loop past it; ragged
+# widths (a partial last pack) between them.
+_SOFTMAX_EDGES = (64, 65, 128, 129, 256, 257, 512, 513, 1000, 1024, 1025, 2048, 2049, 4096,
+                  4097, 8192, 8193)
+
+
+def _softmax_edge_cases():
+    from evograd_amd.opdecl import Workload
+
+    for dtype, vec in (("float32", 4), ("bfloat16", 8), ("float16", 8)):
+        for npack in _SOFTMAX_EDGES:
+            for cols in (npack * vec, npack * vec - 3):
+                yield pytest.param(Workload(dims=dict(rows=3, cols=cols), dtype=dtype),
+                                   id=f"{dtype}-{cols}")
+
+
+@pytest.mark.parametrize("w", list(_softmax_edge_cases()))
+def test_softmax_row_configuration_edges(w):
+    _run("softmax", w)
+
+
 def test_rmsnorm_backward_is_bitwise_deterministic():
     op = decls.RMSNORM
     w = op.benchmark[0]
