@@ -75,6 +75,34 @@ def test_softmax_row_configuration_edges(w):
     _run("softmax", w)
 
 
+# Row widths at the edges of the norm kernels' configurations: the one-wave forwards
+# (1, 2 and 4 packs per lane), the two-row forward, and the rings of 1024 threads with 2, 4
+# and 8 packs per thread (hidden up to 65536 bf16 / 32768 fp32), whole and ragged, at a few
+# rows and at more rows than the backward ring has workgroups.
+_NORM_EDGES = (("bfloat16", 512), ("bfloat16", 1024), ("bfloat16", 2048), ("bfloat16", 8200),
+               ("bfloat16", 16384), ("bfloat16", 16392), ("bfloat16", 32768), ("bfloat16", 65536),
+               ("float16", 12288), ("float32", 1024), ("float32", 8192), ("float32", 16384),
+               ("float32", 32768), ("float32", 8191))
+
+
+def _norm_edge_cases():
+    from evograd_amd.opdecl import Workload
+
+    for name in ("rmsnorm", "layernorm", "fused_add_rms_norm"):
+        width = "cols" if name == "fused_add_rms_norm" else "hidden"
+        for dtype, hidden in _NORM_EDGES:
+            for rows in (3, 600):
+                if rows * hidden > (1 << 22):
+                    continue
+                yield pytest.param(name, Workload(dims={"rows": rows, width: hidden}, dtype=dtype),
+                                   id=f"{name}-{dtype}-{rows}x{hidden}")
+
+
+@pytest.mark.parametrize("name,w", list(_norm_edge_cases()))
+def test_norm_width_edges(name, w):
+    _run(name, w)
+
+
 def test_rmsnorm_backward_is_bitwise_deterministic():
     op = decls.RMSNORM
     w = op.benchmark[0]
