@@ -984,6 +984,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dq_kernel(
 // serving 256 rows (interleaved at [4, 32, 4096, 128]: 590-597 us with 4 waves,
 // 565-571 us with 8). dQ keeps 4 waves (8: 3.5% slower).
 constexpr int kFwdWaves = 8;
+// Forward grids of fewer than two 8-wave workgroups per CU (few heads or short
+// sequences: the decoder layer's B = 1, 32 heads at T <= 2048) take 4-wave workgroups
+// instead, twice as many of them; the rows each wave computes are the same, so the
+// results are identical.
+constexpr int kFwdSmallWaves = 4, kFwdFullGrid = 512;
 constexpr int kDqWaves = 4;
 constexpr int kDkdvRows = 32;
 // dK/dV workgroup width: 4 waves (128 keys), one per SIMD, so that two workgroups
@@ -1053,12 +1058,18 @@ template <typename T, int D, bool ROPE = false>
 int attn_fwd_launch(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
                     int64_t S, int group, float scale, hipStream_t st,
                     const float* rc = nullptr, const float* rs = nullptr) {
-  constexpr int NW = kFwdWaves;
-  const int nqb = (int)((S + 32 * NW - 1) / (32 * NW));
-  EG_LAUNCH((attn_fwd_kernel<T, D, NW, ROPE>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
-            (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, (int)S,
-            scale * kLog2e, nqb, (int)BH, group, rc, rs);
-  return check_launch("eg_attn_fwd");
+  auto go = [&](auto nwc) {
+    constexpr int NW = decltype(nwc)::value;
+    const int nqb = (int)((S + 32 * NW - 1) / (32 * NW));
+    EG_LAUNCH((attn_fwd_kernel<T, D, NW, ROPE>), dim3(grid_for(BH, nqb)), dim3(NW * 64), 0, st,
+              (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
+              (int)S, scale * kLog2e, nqb, (int)BH, group, rc, rs);
+    return check_launch("eg_attn_fwd");
+  };
+  const int nqb_full = (int)((S + 32 * kFwdWaves - 1) / (32 * kFwdWaves));
+  if (grid_for(BH, nqb_full) < (unsigned)kFwdFullGrid)
+    return go(std::integral_constant<int, kFwdSmallWaves>{});
+  return go(std::integral_constant<int, kFwdWaves>{});
 }
 
 // BH counts query heads (x batch); the key/value tensors hold BH / group heads.
@@ -1102,6 +1113,9 @@ int attn_bwd_launch(const void* dout, const void* q, const void* k, const void* 
 // every kernel here makes the stubs certain.
 #define EG_ATTN_INSTANTIATE(T, D, R)                                                         \
   template __global__ void attn_fwd_kernel<T, D, kFwdWaves, R>(                              \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, float, int,   \
+      int, int, const float*, const float*);                                                 \
+  template __global__ void attn_fwd_kernel<T, D, kFwdSmallWaves, R>(                         \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, float, int,   \
       int, int, const float*, const float*);                                                 \
   template __global__ void attn_dkdv_kernel<T, D, dkdv_waves<D>(), kDkdvRows, R>(            \
