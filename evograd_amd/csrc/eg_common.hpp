@@ -238,7 +238,7 @@ void set_timed_label(const char* kernel_expr);
 // safe inside a captured graph). Returns 0 or an error code.
 int zero_fill(void* p, size_t bytes, hipStream_t st, const char* what);
 
-// The MFMA product behind eg_gemm (gemm.hip): c[m][n] = sum_k a(m, k) b(k, n) with
+// The MFMA product behind eg_gemm (gemm_kernel.hpp, launched by gemm.hip): c[m][n] = sum_k a(m, k) b(k, n) with
 // fp32 accumulation. a_kc: a is [a_rows][lda] holding rows m, else rows k; b_kc:
 // b is [b_rows][ldb] holding rows n, else rows k; rows at or past a_rows / b_rows
 // read as zero. bf16/fp16 operands need k % 64 == 0 for a k-contiguous operand.
@@ -254,7 +254,7 @@ int gemm_launch(const void* a, const void* b, void* c, int64_t m, int64_t n, int
                 void* ws = nullptr, size_t ws_bytes = 0);
 
 // The logits product of the fused linear cross entropy with its softmax terms
-// formed in the epilogue (gemm.hip), 16-bit operands only: for logits = x w^T
+// formed in the epilogue (gemm_kernel.hpp), 16-bit operands only: for logits = x w^T
 // (x [m][ldx] and w [n][ldw] both k-contiguous, k % 64 == 0) it writes, per
 // 128-column group h of a row (columns 128h .. 128h + 127),
 //   e[row][col] = exp(logit - mx_h) in the operand dtype (ld lde),

@@ -381,7 +381,7 @@ extern "C" int eg_cross_entropy_bwd(const void* dloss, const void* logits,
 // forward_ref.py:23-35; gradients declared at fused_linear_cross_entropy/
 // __init__.py:91-152) in one launch sequence. The gradient is formed in the
 // forward (the backward only receives the scalar dloss): per row chunk,
-//   16-bit inputs: the logits product x_c W^T (MFMA, gemm.hip) with the softmax
+//   16-bit inputs: the logits product x_c W^T (MFMA, gemm_kernel.hpp) with the softmax
 //   epilogue writes exp(logit - group max) into the dlogits rows, the group
 //   statistics and the target logits -> flce_fixup_kernel forms lse, the row
 //   losses and unit dlogits = softmax - onehot in place (one chunk of all rows by
