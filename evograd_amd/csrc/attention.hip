@@ -33,7 +33,8 @@
 // transpose read in 4 distinct 64-byte quarters (conflict-free at D = 128).
 //
 // Kernels (all deterministic, no atomics):
-//   attn_fwd:   workgroup = 8 waves x 32 query rows; double-buffered 64-key K and
+//   attn_fwd:   workgroup = 8 waves x 32 query rows (4 waves on grids of fewer than
+//               512 8-wave workgroups); double-buffered 64-key K and
 //               V tiles; online softmax in the log2 domain against a running
 //               reference max, refreshed only when a P term could exceed 2^8 (a
 //               lane's sum of P terms bounds each term, so no per-tile max is
