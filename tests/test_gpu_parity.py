@@ -103,6 +103,34 @@ def test_norm_width_edges(name, w):
     _run(name, w)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_softmax_vocab_rows_with_masked_entries(dtype):
+    """Rows of -inf entries on the on-chip (LDS) row path, as a causal or padding mask
+    gives them: a row whose first half is -inf, a row with -inf scattered through it,
+    a finite row, and a row of -inf only (NaN, as torch gives). Forward and backward
+    against torch's autograd in fp32, cast back."""
+    mod = pair_module("softmax")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    rows, cols = 4, 100000
+    x = torch.randn(rows, cols, device="cuda", generator=g).to(dtype)
+    x[0, : cols // 2] = float("-inf")
+    x[1, ::7] = float("-inf")
+    x[3] = float("-inf")
+    dy = torch.randn(rows, cols, device="cuda", generator=g).to(dtype)
+    print(f"\n[gpu-parity] softmax masked rows {dtype}", flush=True)
+    y, saved = mod.softmax_forward_with_saved(x)
+    dx = mod.softmax_backward_from_saved(dy, saved)
+    dx = dx[0] if isinstance(dx, tuple) else dx
+    xr = x.float().requires_grad_(True)
+    yr = torch.softmax(xr, -1)
+    (dxr,) = torch.autograd.grad(yr, xr, dy.float())
+    torch.cuda.synchronize()
+    assert torch.isnan(y[3]).all() and torch.isnan(yr[3]).all()
+    torch.testing.assert_close(y[:3].float(), yr[:3].to(dtype).float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(dx[:3].float(), dxr[:3].to(dtype).float(), atol=2e-2, rtol=2e-2)
+    assert (y[0, : cols // 2] == 0).all() and (y[1, ::7] == 0).all()
+
+
 def test_rmsnorm_backward_is_bitwise_deterministic():
     op = decls.RMSNORM
     w = op.benchmark[0]
