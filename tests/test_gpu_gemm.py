@@ -64,12 +64,13 @@ def _cases():
             yield pytest.param(M, N, K, akc, bkc, id=f"{M}x{N}x{K}-a{'k' if akc else 'm'}-b{'k' if bkc else 'n'}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N,K,akc,bkc", list(_cases()))
-def test_gemm_bf16_fp32_out(M, N, K, akc, bkc):
-    print(f"\n[gpu-gemm] bf16 {M}x{N}x{K} akc={akc} bkc={bkc}", flush=True)
+def test_gemm_16bit_operands_fp32_out(M, N, K, akc, bkc, dtype):
+    print(f"\n[gpu-gemm] {dtype} {M}x{N}x{K} akc={akc} bkc={bkc}", flush=True)
     sys.stdout.flush()
-    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, torch.bfloat16, M + 7 * N + K)
-    c = _run(a, b, M, N, K, lda, ldb, akc, bkc, torch.bfloat16, torch.float32)
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, dtype, M + 7 * N + K)
+    c = _run(a, b, M, N, K, lda, ldb, akc, bkc, dtype, torch.float32)
     ref = A.double() @ B.double()
     err = (c[:, :N].double() - ref).abs().max().item()
     # fp32 accumulation of K products of magnitude ~1: a few ulps of sqrt(K)
@@ -237,22 +238,24 @@ def _seg_cases():
                                id=f"d{dim}-{'-'.join(map(str, sizes))}-{mnk}-a{int(akc)}b{int(bkc)}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("dim,sizes,mnk,akc,bkc", list(_seg_cases()))
-def test_gemm_segmented_is_the_concatenated_product_bitwise(dim, sizes, mnk, akc, bkc):
+def test_gemm_segmented_is_the_concatenated_product_bitwise(dim, sizes, mnk, akc, bkc, dtype):
     """eg_gemm_segmented on operands cut into separate buffers along M, N or K gives
     the bits eg_gemm gives on the concatenated operands (same tiles, same k order,
     same split plan), for every layout; C in segments along M or N."""
     M, N, K = (sum(sizes) if v is None else v for v in mnk)
-    print(f"\n[gpu-gemm] segmented dim={dim} sizes={sizes} {M}x{N}x{K} a{int(akc)} b{int(bkc)}",
+    print(f"\n[gpu-gemm] segmented {dtype} dim={dim} sizes={sizes} {M}x{N}x{K} a{int(akc)} b{int(bkc)}",
           flush=True)
-    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, torch.bfloat16, M * 3 + N + K + dim)
+    A, B, a, b, lda, ldb = _operands(M, N, K, akc, bkc, dtype, M * 3 + N + K + dim)
     st = torch.cuda.current_stream().cuda_stream
-    need = _lib.query("eg_gemm_workspace_bytes", M, N, K, _lib.EG_BF16)
+    tg = _lib.dtype_tag(dtype)
+    need = _lib.query("eg_gemm_workspace_bytes", M, N, K, tg)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     ldc = _r8(N)
-    want = torch.full((M, ldc), float("nan"), device="cuda", dtype=torch.bfloat16)
+    want = torch.full((M, ldc), float("nan"), device="cuda", dtype=dtype)
     _lib.call("eg_gemm", a.data_ptr(), b.data_ptr(), want.data_ptr(), None, M, N, K, lda, ldb,
-              ldc, 0, int(akc), int(bkc), _lib.EG_BF16, _lib.EG_BF16, ws.data_ptr(), need, st)
+              ldc, 0, int(akc), int(bkc), tg, tg, ws.data_ptr(), need, st)
     # the operands the dimension indexes, cut into segments sharing one row stride
     a_segs = b_segs = c_segs = None
     seg_ld = _r8(max(sizes))
@@ -272,15 +275,14 @@ def test_gemm_segmented_is_the_concatenated_product_bitwise(dim, sizes, mnk, akc
     if dim in (1, 2):
         seg_ldc = ldc if dim == 1 else seg_ld
         c_segs = [torch.full((n if dim == 1 else M, seg_ldc), float("nan"), device="cuda",
-                             dtype=torch.bfloat16) for n in sizes]
+                             dtype=dtype) for n in sizes]
     arr = lambda ts: (ctypes.c_void_p * len(sizes))(*[t.data_ptr() for t in ts]) if ts else None
-    c = None if c_segs else torch.full((M, ldc), float("nan"), device="cuda",
-                                       dtype=torch.bfloat16)
+    c = None if c_segs else torch.full((M, ldc), float("nan"), device="cuda", dtype=dtype)
     _lib.call("eg_gemm_segmented", None if a_segs else a.data_ptr(),
               None if b_segs else b.data_ptr(), None if c_segs else c.data_ptr(), M, N, K,
               seg_lda, seg_ldb, seg_ldc, int(akc), int(bkc), dim, len(sizes),
               (ctypes.c_int64 * len(sizes))(*sizes), arr(a_segs), arr(b_segs), arr(c_segs),
-              _lib.EG_BF16, _lib.EG_BF16, ws.data_ptr(), need, st)
+              tg, tg, ws.data_ptr(), need, st)
     if c_segs:
         got = torch.cat([t[:, :(N if dim == 1 else n)] for t, n in zip(c_segs, sizes)],
                         dim=0 if dim == 1 else 1)
@@ -289,5 +291,6 @@ def test_gemm_segmented_is_the_concatenated_product_bitwise(dim, sizes, mnk, akc
     torch.cuda.synchronize()
     assert torch.equal(got, want[:, :N])
     ref = A.double() @ B.double()
-    assert ((got.double() - ref).abs() <= 2.0 ** -8 * ref.abs() + 4e-6 * K).all()
+    ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    assert ((got.double() - ref).abs() <= ulp * ref.abs() + 4e-6 * K).all()
 
