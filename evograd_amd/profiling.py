@@ -24,6 +24,7 @@ import sys
 
 COPY_KERNEL = "MulFunctor<float>"
 COPY_BYTES = 256 << 20
+COPY_GRID = COPY_BYTES // 16  # threads of the calibration copy: 4 floats per thread
 
 
 def short_name(name: str) -> str:
@@ -58,10 +59,13 @@ def stats(path: str, filt: str = "") -> str:
     return "\n".join(lines)
 
 
-def _counter_table(path: str):
-    """kernel name -> counter -> list of per-dispatch values."""
+def _counter_table(path: str, grid: int = 0):
+    """kernel name -> counter -> list of per-dispatch values (only dispatches of
+    `grid` threads when it is given)."""
     per = collections.defaultdict(lambda: collections.defaultdict(dict))
     for r in csv.DictReader(open(path)):
+        if grid and int(r["Grid_Size"]) != grid:
+            continue
         per[r["Kernel_Name"]][r["Counter_Name"]][r["Dispatch_Id"]] = (
             per[r["Kernel_Name"]][r["Counter_Name"]].get(r["Dispatch_Id"], 0.0)
             + float(r["Counter_Value"])
@@ -157,10 +161,12 @@ def traffic(fetch_csv: str, write_csv: str, kernel: str, key: str = "") -> dict:
             raise SystemExit(f"no {counter} readings for kernels matching {sub!r}")
         return how(vals)
 
-    # the calibration copy is the largest kernel of its kind in the run (an input
-    # recipe may launch smaller ones of the same kind, e.g. weight scalings)
-    copy_fetch_kib = pick(f, COPY_KERNEL, "FETCH_SIZE", max)
-    copy_write_kib = pick(w, COPY_KERNEL, "WRITE_SIZE", max)
+    # the calibration copy is told from other kernels of its kind (an input recipe
+    # may scale its tensors with the same kernel, smaller or larger) by its grid:
+    # torch's vectorized float kernel runs one thread per 4 elements
+    cf, cw = _counter_table(fetch_csv, COPY_GRID), _counter_table(write_csv, COPY_GRID)
+    copy_fetch_kib = pick(cf, COPY_KERNEL, "FETCH_SIZE")
+    copy_write_kib = pick(cw, COPY_KERNEL, "WRITE_SIZE")
     fetch_scale = COPY_BYTES / (copy_fetch_kib * 1024.0)
     write_scale = COPY_BYTES / (copy_write_kib * 1024.0)
     kf = pick(f, kernel, "FETCH_SIZE") * 1024.0 * fetch_scale

@@ -173,16 +173,18 @@ def _torch_ref32(x, wt, target):
     return loss.detach(), gx, gw
 
 
-def test_flce_target_out_of_range_gives_nan_row():
+@pytest.mark.parametrize("vocab", [1000, 8200])
+def test_flce_target_out_of_range_gives_nan_row(vocab):
     """A target outside [0, vocab) that is not ignore_index: the loss is NaN (torch
-    raises there) and so is that row's gradient; the other rows of dx stay finite."""
+    raises there) and so is that row's gradient; the other rows of dx stay finite
+    (the loop over each row, and the flat pass over wide rows)."""
     mod = pair_module("fused_linear_cross_entropy")
-    _note("bad target")
+    _note("bad target", vocab)
     g = torch.Generator(device="cuda").manual_seed(11)
     x = torch.randn(40, 128, device="cuda", dtype=torch.bfloat16, generator=g)
-    wt = torch.randn(1000, 128, device="cuda", dtype=torch.bfloat16, generator=g)
-    target = torch.randint(0, 1000, (40,), device="cuda", generator=g)
-    target[7] = 1000
+    wt = torch.randn(vocab, 128, device="cuda", dtype=torch.bfloat16, generator=g)
+    target = torch.randint(0, vocab, (40,), device="cuda", generator=g)
+    target[7] = vocab
     loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(x, wt, target)
     dx, _ = mod.fused_linear_cross_entropy_backward_from_saved(
         torch.ones((), device="cuda", dtype=torch.float32), saved)
@@ -224,3 +226,38 @@ def test_flce_vocab_past_the_fused_limit_takes_the_fp32_path():
     assert bool(((dw.float() - 2.0 * rgw).abs() <= bound_w + 1e-12).all())
     del wt, dw, rgw, dl, bound_w, logits
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("vocab", [8184, 8192, 8200, 131080])
+def test_flce_fixup_row_width_edges(vocab):
+    """The fix-up takes rows of whole 8-column packs from 8192 columns on as one flat
+    pass over the chunk (a workgroup's 1024 packs may span two rows) and loops over
+    each narrower row: the last width of the loop, the first of the flat pass (rows
+    of exactly one workgroup), one where workgroups span rows, and a wide padded one,
+    with targets in the first and last columns, an ignored row and a target in the
+    last 128-column group, agree with torch."""
+    mod = pair_module("fused_linear_cross_entropy")
+    _note("fix-up width", vocab)
+    g = torch.Generator(device="cuda").manual_seed(13)
+    x = torch.randn(6, 64, device="cuda", dtype=torch.bfloat16, generator=g)
+    wt = (0.25 * torch.randn(vocab, 64, device="cuda", generator=g)).bfloat16()
+    target = torch.tensor([0, vocab - 1, -100, vocab - 100, vocab // 2, 12345 % vocab],
+                          device="cuda")
+    loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(x, wt, target)
+    dloss = torch.full((), 1.5, device="cuda", dtype=torch.float32)
+    dx, dw = mod.fused_linear_cross_entropy_backward_from_saved(dloss, saved)
+    ref_loss, rgx, rgw = _torch_ref32(x, wt, target)
+    torch.cuda.synchronize()
+    assert abs(float(loss) - float(ref_loss)) <= 1e-4 * abs(float(ref_loss))
+    # each entry within 2^-6 of the sum of the absolute terms of its dot product (the
+    # unit gradient rounded to bf16, the results rounded twice more)
+    logits = x.float() @ wt.float().t()
+    dl = torch.softmax(logits, dim=1)
+    keep = target != -100
+    dl[keep, target[keep]] -= 1.0
+    dl = dl * keep[:, None] * (1.5 / float(keep.sum()))
+    bound_x = 2.0 ** -6 * (dl.abs() @ wt.float().abs())
+    bound_w = 2.0 ** -6 * (dl.abs().t() @ x.float().abs())
+    assert bool(((dx.float() - 1.5 * rgx).abs() <= bound_x + 1e-12).all())
+    assert bool(((dw.float() - 1.5 * rgw).abs() <= bound_w + 1e-12).all())
+    assert torch.equal(dx[2], torch.zeros_like(dx[2]))  # the ignored row
