@@ -50,9 +50,13 @@ def _close(a, ref, rel):
     return float((err - bound).max()) <= 0, float(err.max())
 
 
-def test_flce_chunked_equals_single_chunk_and_fp64():
+@pytest.mark.parametrize("vocab", [4096, 8200])
+def test_flce_chunked_equals_single_chunk_and_fp64(vocab):
+    """Five chunks of 64 rows (the last one ragged) against one chunk and fp64: the
+    per-row fix-up loop (4096 columns) and the flat fix-up pass over each chunk (8200
+    columns, padded rows)."""
     mod = pair_module("fused_linear_cross_entropy")
-    w = Workload(dims=dict(rows=300, hidden=256, vocab=4096), dtype="bfloat16",
+    w = Workload(dims=dict(rows=300, hidden=256, vocab=vocab), dtype="bfloat16",
                  extra={"ignore_every": 7})
     _note("chunking", w.dims)
     inp = make_case_inputs(OP, w, "cuda")
@@ -60,9 +64,9 @@ def test_flce_chunked_equals_single_chunk_and_fp64():
     one_loss, one_saved = mod.fused_linear_cross_entropy_forward_with_saved(*args)
     one = mod.fused_linear_cross_entropy_backward_from_saved(inp["dloss"], one_saved)
     old = mod.CHUNK_ELEMS
-    mod.CHUNK_ELEMS = 64 * 4096  # 64-row chunks: 5 chunks, the last one ragged
+    mod.CHUNK_ELEMS = 64 * vocab  # 64-row chunks: 5 chunks, the last one ragged
     try:
-        assert mod.chunk_rows(300, 4096) == 64
+        assert mod.chunk_rows(300, vocab) == 64
         many_loss, many_saved = mod.fused_linear_cross_entropy_forward_with_saved(*args)
         many = mod.fused_linear_cross_entropy_backward_from_saved(inp["dloss"], many_saved)
     finally:
@@ -83,7 +87,7 @@ def test_flce_chunked_equals_single_chunk_and_fp64():
     ok, e = _close(many[1], one[1].double(), 2.0 ** -6)
     assert ok, f"chunked dweight differs from one chunk by {e:.3g}"
     # saved state: the two gradients and one count, nothing rows x vocab
-    assert [tuple(t.shape) for t in many_saved] == [(300, 256), (4096, 256), (1,)]
+    assert [tuple(t.shape) for t in many_saved] == [(300, 256), (vocab, 256), (1,)]
 
 
 @pytest.mark.parametrize("dtype,hidden", [("bfloat16", 100), ("float16", 200)])
