@@ -78,3 +78,28 @@ def test_llama3_attention_llama3_8b_config():
     rep = verify(OP, pair_module("llama3_attention"), device="cuda", workloads=(w,))
     torch.cuda.empty_cache()
     assert rep.ok, "\n".join(rep.failures())
+
+
+def test_llama3_attention_tables_in_the_tensors_dtype():
+    """Tables in x's dtype (as the reference decoder layer passes them,
+    llama3_decoder_layer/__init__.py:122-123): the pair rotates with fp32 copies of
+    them, so o and the gradients equal those of the same tables given in fp32, bit
+    for bit, and the saved state holds the two fp32 copies as new storage."""
+    w = Workload(dims=dict(B=1, H=8, KVH=2, S=200, D=128), dtype="bfloat16")
+    _note("bf16 tables", w.dims)
+    inp = make_case_inputs(OP, w, "cuda")
+    mod = pair_module("llama3_attention")
+    cos16, sin16 = inp["cos"].bfloat16(), inp["sin"].bfloat16()
+    args = (inp["q"], inp["k"], inp["v"])
+    o16, s16 = mod.llama3_attention_forward_with_saved(*args, cos16, sin16)
+    o32, s32 = mod.llama3_attention_forward_with_saved(*args, cos16.float(), sin16.float())
+    g16 = mod.llama3_attention_backward_from_saved(inp["do"], s16)
+    g32 = mod.llama3_attention_backward_from_saved(inp["do"], s32)
+    torch.cuda.synchronize()
+    assert torch.equal(o16, o32)
+    assert all(torch.equal(a, b) for a, b in zip(g16, g32))
+    rep = saved_state_report(s16, {"q": inp["q"], "k": inp["k"], "v": inp["v"], "cos": cos16,
+                                   "sin": sin16})
+    S, D = w.dims["S"], w.dims["D"]
+    assert rep["new_storage_bytes"] == (o16.numel() * o16.element_size() + 8 * S * 4
+                                        + 2 * S * D * 4)
