@@ -232,8 +232,10 @@ def test_flce_vocab_past_the_fused_limit_takes_the_fp32_path():
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("vocab", [8184, 8192, 8200, 131080])
-def test_flce_fixup_row_width_edges(vocab):
+@pytest.mark.parametrize("vocab,dtype", [(8184, torch.bfloat16), (8192, torch.bfloat16),
+                                         (8200, torch.bfloat16), (8200, torch.float16),
+                                         (131080, torch.bfloat16)])
+def test_flce_fixup_row_width_edges(vocab, dtype):
     """The fix-up takes rows of whole 8-column packs from 8192 columns on as one flat
     pass over the chunk (a workgroup's 1024 packs may span two rows) and loops over
     each narrower row: the last width of the loop, the first of the flat pass (rows
@@ -241,10 +243,10 @@ def test_flce_fixup_row_width_edges(vocab):
     with targets in the first and last columns, an ignored row and a target in the
     last 128-column group, agree with torch."""
     mod = pair_module("fused_linear_cross_entropy")
-    _note("fix-up width", vocab)
+    _note("fix-up width", vocab, dtype)
     g = torch.Generator(device="cuda").manual_seed(13)
-    x = torch.randn(6, 64, device="cuda", dtype=torch.bfloat16, generator=g)
-    wt = (0.25 * torch.randn(vocab, 64, device="cuda", generator=g)).bfloat16()
+    x = torch.randn(6, 64, device="cuda", generator=g).to(dtype)
+    wt = (0.25 * torch.randn(vocab, 64, device="cuda", generator=g)).to(dtype)
     target = torch.tensor([0, vocab - 1, -100, vocab - 100, vocab // 2, 12345 % vocab],
                           device="cuda")
     loss, saved = mod.fused_linear_cross_entropy_forward_with_saved(x, wt, target)
@@ -254,14 +256,24 @@ def test_flce_fixup_row_width_edges(vocab):
     torch.cuda.synchronize()
     assert abs(float(loss) - float(ref_loss)) <= 1e-4 * abs(float(ref_loss))
     # each entry within 2^-6 of the sum of the absolute terms of its dot product (the
-    # unit gradient rounded to bf16, the results rounded twice more)
+    # unit gradient rounded to 16 bits, the results rounded twice more)
     logits = x.float() @ wt.float().t()
     dl = torch.softmax(logits, dim=1)
     keep = target != -100
     dl[keep, target[keep]] -= 1.0
-    dl = dl * keep[:, None] * (1.5 / float(keep.sum()))
+    scale = 1.5 / float(keep.sum())
+    dl = dl * keep[:, None] * scale
     bound_x = 2.0 ** -6 * (dl.abs() @ wt.float().abs())
     bound_w = 2.0 ** -6 * (dl.abs().t() @ x.float().abs())
+    if dtype == torch.float16:
+        # fp16 keeps values below 2^-14 as subnormals, spaced 2^-24 apart: each rounding
+        # of a tiny value errs by up to 2^-25 absolute, which no relative bound covers.
+        # The exponential and the unit gradient are rounded once each before the
+        # products, the products' unit results once, and the scaled results once more.
+        def floor(other):  # other: the |operand| summed along the product's k
+            return scale * (2.0 ** -24 * other + 2.0 ** -25) + 2.0 ** -25
+        bound_x = bound_x + floor(wt.float().abs().sum(0))[None, :]
+        bound_w = bound_w + floor(x.float().abs()[keep].sum(0))[None, :]
     assert bool(((dx.float() - 1.5 * rgx).abs() <= bound_x + 1e-12).all())
     assert bool(((dw.float() - 1.5 * rgw).abs() <= bound_w + 1e-12).all())
     assert torch.equal(dx[2], torch.zeros_like(dx[2]))  # the ignored row
