@@ -267,9 +267,10 @@ def _first_bwd_kernel(bwd, dy, saved, **kw) -> str:
 @pytest.mark.parametrize("name", ["rmsnorm", "layernorm"])
 def test_shape_dispatch_routes_to_two_programs(name):
     """The dispatched pair over two different HIP programs: below the declaration's
-    4096-row split the small-shape program (one-launch backward, norm_bwd_small),
-    at or above it the ring program (norm_bwd_ring); both pass the gate, the saved
-    state carries the route tag, and each route runs its own kernel."""
+    4096-row split the small-shape program (the one-launch backward, norm_bwd_small,
+    up to 512 rows, the ring above), at or above it the ring program
+    (norm_bwd_ring); both pass the gate, the saved state carries the route tag, and
+    each route runs the kernel its program picks for the shape."""
     from evograd_amd import dispatch_module
     from evograd_amd.opdecl import Workload
 
@@ -277,8 +278,10 @@ def test_shape_dispatch_routes_to_two_programs(name):
     pair = dispatch_module(name)
     fwd = getattr(pair, op.forward_fn_name)
     bwd = getattr(pair, op.backward_fn_name)
-    cases = ((Workload(dims=dict(rows=1500, hidden=768), dtype="bfloat16"), 0, "norm_bwd_small"),
-             (Workload(dims=dict(rows=600, hidden=1000), dtype="float32"), 0, "norm_bwd_small"),
+    cases = ((Workload(dims=dict(rows=300, hidden=768), dtype="bfloat16"), 0, "norm_bwd_small"),
+             (Workload(dims=dict(rows=512, hidden=1000), dtype="float32"), 0, "norm_bwd_small"),
+             (Workload(dims=dict(rows=513, hidden=768), dtype="bfloat16"), 0, "norm_bwd_ring"),
+             (Workload(dims=dict(rows=1500, hidden=1000), dtype="float32"), 0, "norm_bwd_ring"),
              (Workload(dims=dict(rows=4096, hidden=4096), dtype="bfloat16"), 1, "norm_bwd_ring"))
     for w, route, kernel in cases:
         print(f"\n[gpu-parity] dispatch {name} {w.dims} {w.dtype}", flush=True)
@@ -294,8 +297,9 @@ def test_shape_dispatch_routes_to_two_programs(name):
 @pytest.mark.parametrize("name", ["rmsnorm", "layernorm"])
 def test_small_norm_program_gate_and_repeatability(name):
     """The small-shape program alone: every declared correctness workload (ragged
-    widths, single rows, fp32/fp16/bf16) and the 1024-row sweep size pass the gate;
-    its backward is bitwise repeatable (fixed-order column sums, no atomics)."""
+    widths, single rows, fp32/fp16/bf16), 512 rows (the most its one-launch backward
+    takes) and the 1024-row sweep size (the ring) pass the gate; the one-launch
+    backward is bitwise repeatable (fixed-order column sums, no atomics)."""
     import importlib
 
     from evograd_amd import SMALL_PROGRAMS
@@ -303,7 +307,8 @@ def test_small_norm_program_gate_and_repeatability(name):
 
     op = decls.get_op(name)
     mod = importlib.import_module(SMALL_PROGRAMS[name])
-    ws = list(op.correctness) + [Workload(dims=dict(rows=1024, hidden=4096), dtype="bfloat16")]
+    ws = list(op.correctness) + [Workload(dims=dict(rows=1024, hidden=4096), dtype="bfloat16"),
+                                 Workload(dims=dict(rows=512, hidden=4096), dtype="bfloat16")]
     print(f"\n[gpu-parity] small {name} x{len(ws)}", flush=True)
     rep = verify(op, mod, device="cuda", workloads=tuple(ws))
     assert rep.ok, "\n".join(rep.failures())
