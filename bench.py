@@ -66,8 +66,12 @@ ALL_OPS = ("softmax", "rmsnorm", "layernorm", "swiglu", "rope", "causal_attentio
 # ones over LLAMA_VOCAB_TOKEN_SWEEP.
 LLAMA_TOKEN_SWEEP = (1024, 2048, 4096, 8192, 16384)
 LLAMA_VOCAB_TOKEN_SWEEP = (512, 1024, 2048, 4096, 8192)
+# Two points below the reference's sweep for the norms with a shape dispatcher: there
+# its small-shape program runs the one-launch backward (up to 512 rows).
+SMALL_NORM_POINTS = (256, 512)
 SWEEP_OPS = {
-    "rmsnorm": LLAMA_TOKEN_SWEEP, "layernorm": LLAMA_TOKEN_SWEEP, "swiglu": LLAMA_TOKEN_SWEEP,
+    "rmsnorm": SMALL_NORM_POINTS + LLAMA_TOKEN_SWEEP,
+    "layernorm": SMALL_NORM_POINTS + LLAMA_TOKEN_SWEEP, "swiglu": LLAMA_TOKEN_SWEEP,
     "fused_add_rms_norm": LLAMA_TOKEN_SWEEP, "rope": LLAMA_TOKEN_SWEEP,
     "cross_entropy": LLAMA_VOCAB_TOKEN_SWEEP, "softmax@vocab": LLAMA_VOCAB_TOKEN_SWEEP,
 }
