@@ -76,6 +76,10 @@ SIGNATURES: dict[str, tuple] = {
                        _i32, _i32, _p, _size, _p]),
     "eg_split_heads": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
     "eg_merge_heads": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
+    "eg_split_qkv_heads": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                  _i32, _i32, _i32, _p]),
+    "eg_merge_qkv_heads": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                  _i32, _i32, _i32, _p]),
     "eg_add": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "eg_rmsnorm_bwd_small": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "eg_layernorm_bwd_small": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),

@@ -70,6 +70,67 @@ __global__ __launch_bounds__(kLayBlock) void heads_kernel(
   store_f32<T, VEC>(dst + doff + half, x2);
 }
 
+// The q, k and v of one fused projection in one launch: a token row of the [rows, ld]
+// buffer holds heads_q query heads, then heads_kv key heads, then heads_kv value
+// heads (head_dim each, from column 0); each goes to (TO_HEADS) or comes from its own
+// head-major tensor. Query and key heads take the rotation of MODE; value heads are
+// copied. A thread owns one (token, head, chunk) triple as in heads_kernel.
+template <typename T>
+struct QkvHeads {
+  T* base[3];    // head-major q, k, v: [batch, heads of each, tokens, head_dim]
+  int first[4];  // first head of q, k, v in a token row, then the row's head count
+};
+
+template <typename T, typename TT, int VEC, int MODE, bool TO_HEADS>
+__global__ __launch_bounds__(kLayBlock) void qkv_heads_kernel(
+    const T* __restrict__ src_rows, T* __restrict__ dst_rows, QkvHeads<T> hd,
+    const TT* __restrict__ cosv, const TT* __restrict__ sinv, int64_t n, int tokens,
+    int head_dim, int64_t ld) {
+  const int64_t idx = (int64_t)blockIdx.x * kLayBlock + threadIdx.x;
+  if (idx >= n) return;
+  const int heads = hd.first[3];
+  const int half = head_dim >> 1;
+  const int cph = half / VEC;  // chunks per head
+  const int64_t th = idx / cph;
+  const int c = (int)(idx - th * cph) * VEC;
+  const int g = (int)(th % heads);  // head within the token row
+  const int64_t bt = th / heads;    // batch * tokens + token
+  const int t = (int)(bt % tokens);
+  const int64_t b = bt / tokens;
+  const int which = g < hd.first[1] ? 0 : (g < hd.first[2] ? 1 : 2);
+  const int h = g - hd.first[which];
+  const int nh = hd.first[which + 1] - hd.first[which];
+  T* hb = hd.base[which];
+  const int64_t roff = bt * ld + (int64_t)g * head_dim + c;
+  const int64_t hoff = ((b * nh + h) * tokens + t) * (int64_t)head_dim + c;
+  const T* src = TO_HEADS ? src_rows + roff : hb + hoff;
+  T* dst = TO_HEADS ? hb + hoff : dst_rows + roff;
+  float x1[VEC], x2[VEC];
+  load_f32<T, VEC>(src, x1);
+  load_f32<T, VEC>(src + half, x2);
+  if (MODE != 0 && which < 2) {
+    const int64_t to = (int64_t)t * head_dim + c;
+    float c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+    load_f32<TT, VEC>(cosv + to, c1);
+    load_f32<TT, VEC>(cosv + to + half, c2);
+    load_f32<TT, VEC>(sinv + to, s1);
+    load_f32<TT, VEC>(sinv + to + half, s2);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float a = x1[i], bb = x2[i];
+      if constexpr (MODE == 1) {
+        x1[i] = a * c1[i] - bb * s1[i];
+        x2[i] = bb * c2[i] + a * s2[i];
+      } else {
+        x1[i] = a * c1[i] + bb * s2[i];
+        x2[i] = bb * c2[i] - a * s1[i];
+      }
+    }
+  }
+  store_f32<T, VEC>(dst, x1);
+  store_f32<T, VEC>(dst + half, x2);
+}
+
 template <typename T, int VEC>
 __global__ __launch_bounds__(kLayBlock) void add_kernel(const T* __restrict__ a,
                                                         const T* __restrict__ b,
@@ -180,10 +241,111 @@ int heads_launch(const void* src, void* dst, const void* cosv, const void* sinv,
   });
 }
 
+int qkv_heads_launch(const void* rows_src, void* rows_dst, const void* q, const void* k,
+                     const void* v, const void* cosv, const void* sinv, int64_t batch,
+                     int64_t tokens, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                     int64_t ld, int rope, int table_dtype, int dtype, bool to_heads,
+                     void* stream, const char* name) {
+  clear_error();
+  if (batch < 0 || tokens < 0 || heads_q < 0 || heads_kv < 0 || head_dim < 0) {
+    set_error("%s: negative size", name);
+    return 1;
+  }
+  const int64_t heads = heads_q + 2 * heads_kv;
+  if (head_dim % 2 || ld < heads * head_dim) {
+    set_error("%s: head_dim must be even and ld >= (heads_q + 2 heads_kv) * head_dim", name);
+    return 1;
+  }
+  if (rope < 0 || rope > 2 || (rope && (!cosv || !sinv))) {
+    set_error("%s: rope must be 0 (none), 1 (rotate) or 2 (transpose) with both tables", name);
+    return 1;
+  }
+  if (rope && table_dtype != EG_F32 && table_dtype != dtype) {
+    set_error("%s: tables must be fp32 or the tensors' dtype", name);
+    return 1;
+  }
+  const int64_t rows = batch * tokens * heads;
+  if (rows == 0 || head_dim == 0) return 0;
+  const void* rows_ptr = to_heads ? rows_src : rows_dst;
+  if (!rows_ptr || (heads_q && !q) || (heads_kv && (!k || !v))) {
+    set_error("%s: null pointer", name);
+    return 1;
+  }
+  if (tokens > 0x7fffffff || heads > 0x7fffffff || head_dim > 0x7fffffff) {
+    set_error("%s: size out of range", name);
+    return 1;
+  }
+  hipStream_t st = as_stream(stream);
+  return layer_dispatch(dtype, name, [&](auto tag) {
+    using T = decltype(tag);
+    constexpr int V = 16 / sizeof(T);
+    QkvHeads<T> hd;
+    hd.base[0] = (T*)q;
+    hd.base[1] = (T*)k;
+    hd.base[2] = (T*)v;
+    hd.first[0] = 0;
+    hd.first[1] = (int)heads_q;
+    hd.first[2] = (int)(heads_q + heads_kv);
+    hd.first[3] = (int)heads;
+    const bool vec = (head_dim / 2) % V == 0 && ld % V == 0 && aligned16(rows_ptr) &&
+                     (!heads_q || aligned16(q)) && (!heads_kv || (aligned16(k) && aligned16(v))) &&
+                     (!rope || (aligned16(cosv) && aligned16(sinv)));
+    auto go = [&](auto vc, auto tt) {
+      constexpr int VC = decltype(vc)::value;
+      using TT = decltype(tt);
+      const int64_t n = rows * (head_dim / 2 / VC);
+      const unsigned grid = (unsigned)((n + kLayBlock - 1) / kLayBlock);
+      auto launch = [&](auto mode, auto dir) {
+        EG_LAUNCH((qkv_heads_kernel<T, TT, VC, decltype(mode)::value, decltype(dir)::value>),
+                  dim3(grid), dim3(kLayBlock), 0, st, (const T*)rows_src, (T*)rows_dst, hd,
+                  (const TT*)cosv, (const TT*)sinv, n, (int)tokens, (int)head_dim, ld);
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      if (to_heads) {
+        if (rope == 0) launch(I0{}, std::true_type{});
+        else if (rope == 1) launch(I1{}, std::true_type{});
+        else launch(I2{}, std::true_type{});
+      } else {
+        if (rope == 0) launch(I0{}, std::false_type{});
+        else if (rope == 1) launch(I1{}, std::false_type{});
+        else launch(I2{}, std::false_type{});
+      }
+      return check_launch(name);
+    };
+    auto pick_tables = [&](auto vc) {
+      if (rope && table_dtype == EG_F32 && !std::is_same<T, float>::value)
+        return go(vc, float{});
+      return go(vc, T{});
+    };
+    if (vec) return pick_tables(std::integral_constant<int, V>{});
+    return pick_tables(std::integral_constant<int, 1>{});
+  });
+}
+
 }  // namespace
 }  // namespace eg
 
 using namespace eg;
+
+extern "C" int eg_split_qkv_heads(const void* src, void* q, void* k, void* v, const void* cos,
+                                  const void* sin, int64_t batch, int64_t tokens,
+                                  int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t ld,
+                                  int rope, int table_dtype, int dtype, void* stream) {
+  return qkv_heads_launch(src, nullptr, q, k, v, cos, sin, batch, tokens, heads_q, heads_kv,
+                          head_dim, ld, rope, table_dtype, dtype, true, stream,
+                          "eg_split_qkv_heads");
+}
+
+extern "C" int eg_merge_qkv_heads(const void* q, const void* k, const void* v, void* dst,
+                                  const void* cos, const void* sin, int64_t batch, int64_t tokens,
+                                  int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t ld,
+                                  int rope, int table_dtype, int dtype, void* stream) {
+  return qkv_heads_launch(nullptr, dst, q, k, v, cos, sin, batch, tokens, heads_q, heads_kv,
+                          head_dim, ld, rope, table_dtype, dtype, false, stream,
+                          "eg_merge_qkv_heads");
+}
 
 extern "C" int eg_split_heads(const void* src, void* dst, const void* cos, const void* sin,
                               int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim,

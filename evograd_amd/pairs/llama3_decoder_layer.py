@@ -15,7 +15,8 @@ epilogues of the products that feed them (``x1 = x + o Wo^T``, ``out = x1 + act
 Wd^T``, and the sums ``dh = dq Wq + dk Wk + dv Wv``, ``dh2 = dgate Wg + dup Wu``);
 ``eg_split_heads`` / ``eg_merge_heads`` for the [B, T, H, D] <-> [B, H, T, D]
 layout changes with the RoPE rotation (and, backward, its transpose) applied on
-the way; ``eg_attn_gqa_fwd/bwd`` for the attention (MFMA at 16-bit head_dim 64 or
+the way (``eg_split_qkv_heads`` / ``eg_merge_qkv_heads``: q, k and v of the fused
+projection in one launch); ``eg_attn_gqa_fwd/bwd`` for the attention (MFMA at 16-bit head_dim 64 or
 128, the generic kernels for the fp32 and head_dim 16/32 correctness cases);
 ``eg_silu_mul`` / ``eg_swiglu_bwd`` for the MLP activation; ``eg_add`` where the
 residual gradient meets a norm's.
@@ -206,6 +207,20 @@ class _Ops:
                   s.B, s.T, heads, s.D, ld, rope, tag(cos.dtype) if cos is not None else self.tg,
                   self.tg, self.st)
 
+    def split_qkv(self, qkv, qh, kh, vh, s, cos, sin):
+        """The rotated q, k and the copied v heads of the fused [q | k | v] rows, one
+        launch."""
+        _lib.call("eg_split_qkv_heads", _lib.ptr(qkv), _lib.ptr(qh), _lib.ptr(kh), _lib.ptr(vh),
+                  _lib.ptr(cos), _lib.ptr(sin), s.B, s.T, s.H, s.KVH, s.D, s.qkv, 1,
+                  tag(cos.dtype), self.tg, self.st)
+
+    def merge_qkv(self, dqh, dkh, dvh, dqkv, s, cos, sin):
+        """dq, dk (transpose-rotated) and dv into the fused [dq | dk | dv] rows, one
+        launch."""
+        _lib.call("eg_merge_qkv_heads", _lib.ptr(dqh), _lib.ptr(dkh), _lib.ptr(dvh),
+                  _lib.ptr(dqkv), _lib.ptr(cos), _lib.ptr(sin), s.B, s.T, s.H, s.KVH, s.D, s.qkv,
+                  2, tag(cos.dtype), self.tg, self.st)
+
     def add(self, a, b, c):
         _lib.call("eg_add", _lib.ptr(a), _lib.ptr(b), _lib.ptr(c), c.numel(), self.tg, self.st)
 
@@ -221,19 +236,17 @@ def _qkv_heads(ops, s, h1, wq, wk, wv, cos, sin):
         qkv = ops.empty(s.M, s.qkv)
         ops.gemm_seg(h1, None, qkv, s.M, s.qkv, s.hidden, s.hidden, s.hidden, s.qkv, True, True,
                      2, [s.q_out, s.kv_out, s.kv_out], b_segs=[wq, wk, wv])
-        q, k, v = qkv, qkv[:, s.q_out:], qkv[:, s.q_out + s.kv_out:]
-        ldq = ldk = s.qkv
-    else:
-        q = ops.empty(s.M, s.q_out)
-        k = ops.empty(s.M, s.kv_out)
-        v = ops.empty(s.M, s.kv_out)
-        ops.linear(h1, wq, q, s.M, s.q_out, s.hidden, s.hidden, s.q_out)
-        ops.linear(h1, wk, k, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
-        ops.linear(h1, wv, v, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
-        ldq, ldk = s.q_out, s.kv_out
-    ops.split(q, qh, s, s.H, ldq, 1, cos, sin)
-    ops.split(k, kh, s, s.KVH, ldk, 1, cos, sin)
-    ops.split(v, vh, s, s.KVH, ldk, 0)
+        ops.split_qkv(qkv, qh, kh, vh, s, cos, sin)
+        return qh, kh, vh
+    q = ops.empty(s.M, s.q_out)
+    k = ops.empty(s.M, s.kv_out)
+    v = ops.empty(s.M, s.kv_out)
+    ops.linear(h1, wq, q, s.M, s.q_out, s.hidden, s.hidden, s.q_out)
+    ops.linear(h1, wk, k, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
+    ops.linear(h1, wv, v, s.M, s.kv_out, s.hidden, s.hidden, s.kv_out)
+    ops.split(q, qh, s, s.H, s.q_out, 1, cos, sin)
+    ops.split(k, kh, s, s.KVH, s.kv_out, 1, cos, sin)
+    ops.split(v, vh, s, s.KVH, s.kv_out, 0)
     return qh, kh, vh
 
 
@@ -393,9 +406,7 @@ def llama3_decoder_layer_backward_from_saved(dout, saved, eps: float = 1e-5):
         # Wv] (the weights as segments along K); [dWq; dWk; dWv] = [dq | dk | dv]^T h1 in
         # one buffer, returned as three views
         dqkv = ops.empty(M, s.qkv)
-        ops.merge(dqh, dqkv, s, s.H, s.qkv, 2, cos, sin)
-        ops.merge(dkh, dqkv[:, s.q_out:], s, s.KVH, s.qkv, 2, cos, sin)
-        ops.merge(dvh, dqkv[:, s.q_out + s.kv_out:], s, s.KVH, s.qkv, 0)
+        ops.merge_qkv(dqh, dkh, dvh, dqkv, s, cos, sin)
         del dqh, dkh, dvh
         if s.kseg_qkv:
             ops.gemm_seg(dqkv, None, dh1, M, hidden, s.qkv, s.qkv, hidden, hidden, True, False,

@@ -422,6 +422,22 @@ int eg_merge_heads(const void* src, void* dst, const void* cos, const void* sin,
                    int64_t tokens, int64_t heads, int64_t head_dim, int64_t ld, int rope,
                    int table_dtype, int dtype, void* stream);
 
+/* eg_split_heads / eg_merge_heads for the q, k and v of one fused projection in one
+ * launch (the [q | k | v] output of the layer's single product over Wq, Wk, Wv):
+ * each token row of src (split) or dst (merge) [batch * tokens, ld] holds heads_q
+ * query heads, then heads_kv key heads, then heads_kv value heads of head_dim
+ * from column 0; q is [batch, heads_q, tokens, head_dim], k and v
+ * [batch, heads_kv, tokens, head_dim]. rope (0, 1 or 2 as above) applies to the
+ * query and key heads; value heads are copied. */
+int eg_split_qkv_heads(const void* src, void* q, void* k, void* v, const void* cos,
+                       const void* sin, int64_t batch, int64_t tokens, int64_t heads_q,
+                       int64_t heads_kv, int64_t head_dim, int64_t ld, int rope, int table_dtype,
+                       int dtype, void* stream);
+int eg_merge_qkv_heads(const void* q, const void* k, const void* v, void* dst, const void* cos,
+                       const void* sin, int64_t batch, int64_t tokens, int64_t heads_q,
+                       int64_t heads_kv, int64_t head_dim, int64_t ld, int rope, int table_dtype,
+                       int dtype, void* stream);
+
 /* c = a + b over n elements (fp32 sum, one rounding): where a residual
  * connection's gradient meets a norm's (forward_ref.py:110 and :117, backward). */
 int eg_add(const void* a, const void* b, void* c, int64_t n, int dtype, void* stream);

@@ -148,6 +148,51 @@ def test_split_merge_heads_with_rope(dtype, D, heads, ld_pad, table_dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,hq,hkv,ld_pad", [(128, 4, 2, 0), (32, 6, 3, 8), (6, 2, 1, 2)])
+@pytest.mark.parametrize("table_dtype", [torch.float32, "same"])
+def test_qkv_heads_equal_three_separate_layout_changes(dtype, D, hq, hkv, ld_pad, table_dtype):
+    """eg_split_qkv_heads / eg_merge_qkv_heads (q, k and v of one fused projection in
+    one launch) give the bits of eg_split_heads / eg_merge_heads on the three column
+    ranges: q and k rotated (or transpose-rotated), v copied, padding columns of the
+    merged rows untouched."""
+    _note("qkv heads", dtype, D, hq, hkv, ld_pad, table_dtype)
+    B, T = 2, 37
+    ld = (hq + 2 * hkv) * D + ld_pad
+    tdt = dtype if table_dtype == "same" else table_dtype
+    g = torch.Generator(device="cuda").manual_seed(3 * D + hq)
+    src = torch.randn(B * T, ld, device="cuda", generator=g).to(dtype)
+    cos, sin = rope_tables(T, D, 10000.0, tdt, "cuda")
+    tg, ttg = _lib.dtype_tag(dtype), _lib.dtype_tag(tdt)
+    cols = (0, hq * D, (hq + hkv) * D)  # first column of q, k, v in a row
+    nh = (hq, hkv, hkv)
+
+    def heads(n):
+        return torch.empty(B, n, T, D, device="cuda", dtype=dtype)
+
+    fused = [heads(n) for n in nh]
+    _lib.call("eg_split_qkv_heads", src.data_ptr(), *(t.data_ptr() for t in fused),
+              cos.data_ptr(), sin.data_ptr(), B, T, hq, hkv, D, ld, 1, ttg, tg, _stream())
+    for j in range(3):
+        one = heads(nh[j])
+        _lib.call("eg_split_heads", src[:, cols[j]:].data_ptr(), one.data_ptr(), cos.data_ptr(),
+                  sin.data_ptr(), B, T, nh[j], D, ld, 1 if j < 2 else 0, ttg, tg, _stream())
+        torch.cuda.synchronize()
+        assert torch.equal(fused[j], one), f"split of tensor {j}"
+    grads = [torch.randn(B, n, T, D, device="cuda", generator=g).to(dtype) for n in nh]
+    out = torch.full((B * T, ld), 7.0, device="cuda", dtype=dtype)
+    _lib.call("eg_merge_qkv_heads", *(t.data_ptr() for t in grads), out.data_ptr(),
+              cos.data_ptr(), sin.data_ptr(), B, T, hq, hkv, D, ld, 2, ttg, tg, _stream())
+    want = torch.full((B * T, ld), 7.0, device="cuda", dtype=dtype)
+    for j in range(3):
+        _lib.call("eg_merge_heads", grads[j].data_ptr(), want[:, cols[j]:].data_ptr(),
+                  cos.data_ptr(), sin.data_ptr(), B, T, nh[j], D, ld, 2 if j < 2 else 0, ttg, tg,
+                  _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    assert (out[:, (hq + 2 * hkv) * D:] == 7.0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("n", [1, 1000, 4096 * 33])
 def test_add_and_silu_mul(dtype, n):
     _note("add/silu_mul", dtype, n)
