@@ -148,7 +148,8 @@ def test_split_merge_heads_with_rope(dtype, D, heads, ld_pad, table_dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("D,hq,hkv,ld_pad", [(128, 4, 2, 0), (32, 6, 3, 8), (6, 2, 1, 2)])
+@pytest.mark.parametrize("D,hq,hkv,ld_pad", [(128, 4, 2, 0), (64, 4, 4, 0), (32, 6, 3, 8),
+                                              (6, 2, 1, 2)])
 @pytest.mark.parametrize("table_dtype", [torch.float32, "same"])
 def test_qkv_heads_equal_three_separate_layout_changes(dtype, D, hq, hkv, ld_pad, table_dtype):
     """eg_split_qkv_heads / eg_merge_qkv_heads (q, k and v of one fused projection in
